@@ -1,0 +1,192 @@
+"""ctypes bindings over include/mgx.h (libmgx.so, built in place by the package Makefile).
+
+Loading fails loudly when the library is missing: there is no host fallback."""
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_PKG = os.path.dirname(_HERE)
+LIB_PATH = os.path.join(_PKG, "libmgx.so")
+
+
+class MgxError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"mgx error {code}: {msg}")
+        self.code = code
+
+
+class LmConfig(C.Structure):
+    """mgx_lm_config = ac::LmConfig (src/mg/lm.h:42-93)."""
+    _fields_ = [(n, C.c_int32) for n in ("dim", "layers", "heads", "head_dim", "ff_dim", "cond_dim", "n_q",
+                                         "card", "special_token_id", "pos_denominator")] + \
+               [(n, C.c_float) for n in ("max_period", "norm_eps", "cfg_coef")]
+
+
+class Tensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("type", C.c_int32), ("ne", C.c_int64 * 4), ("data", C.c_void_p),
+                ("nbytes", C.c_uint64)]
+
+
+class Adapter(C.Structure):
+    _fields_ = [("target", C.c_char_p), ("A", C.c_void_p), ("B", C.c_void_p), ("magnitude", C.c_void_p),
+                ("rank", C.c_int32), ("alpha", C.c_float), ("strength", C.c_float)]
+
+
+class GenerateParams(C.Structure):
+    """mgx_generate_params = ac::GenerateParams (src/mg/pipeline.h:25-34)."""
+    _fields_ = [("max_gen_len", C.c_int32), ("use_sampling", C.c_int32), ("temperature", C.c_float),
+                ("top_k", C.c_int32), ("cfg_coef", C.c_float), ("seed", C.c_uint64)]
+
+
+class GenerateReport(C.Structure):
+    _fields_ = [("cache_bytes", C.c_uint64), ("prefill_tokens", C.c_int32), ("decode_steps", C.c_int32),
+                ("forwards", C.c_int32), ("prefill_seconds", C.c_double), ("decode_seconds", C.c_double)]
+
+
+EXPORTS = ["mgx_model_create", "mgx_model_set_adapters", "mgx_model_destroy", "mgx_stream_create", "mgx_forward",
+           "mgx_stream_reset", "mgx_stream_used", "mgx_stream_forwards", "mgx_stream_cache_bytes",
+           "mgx_stream_destroy", "mgx_use_guidance", "mgx_generate", "mgx_last_error"]
+
+_lib = None
+
+
+def load(path=None):
+    """The loaded libmgx.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise MgxError(-2, f"{p} is not built; run __graft_entry__.build()")
+    lib = C.CDLL(p)
+    P = C.c_void_p
+    lib.mgx_last_error.restype = C.c_char_p
+    lib.mgx_model_create.argtypes = [C.POINTER(LmConfig), C.POINTER(Tensor), C.c_int32, C.POINTER(P)]
+    lib.mgx_model_set_adapters.argtypes = [P, C.POINTER(Adapter), C.c_int32]
+    lib.mgx_model_destroy.argtypes = [P]
+    lib.mgx_model_destroy.restype = None
+    lib.mgx_stream_create.argtypes = [P, C.c_int32, C.c_int32, P, C.c_int32, C.c_int32, C.POINTER(P)]
+    lib.mgx_forward.argtypes = [P, P, C.c_int32, P]
+    lib.mgx_stream_reset.argtypes = [P]
+    lib.mgx_stream_used.argtypes = [P]
+    lib.mgx_stream_forwards.argtypes = [P]
+    lib.mgx_stream_cache_bytes.argtypes = [P]
+    lib.mgx_stream_cache_bytes.restype = C.c_uint64
+    lib.mgx_stream_destroy.argtypes = [P]
+    lib.mgx_stream_destroy.restype = None
+    lib.mgx_use_guidance.argtypes = [C.c_float, C.c_int32]
+    lib.mgx_generate.argtypes = [P, P, C.c_int32, C.c_int32, P, C.c_int32, C.POINTER(GenerateParams), P, P, P,
+                                 C.POINTER(GenerateReport)]
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _check(lib, rc):
+    if rc != 0:
+        raise MgxError(rc, lib.mgx_last_error().decode())
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def use_guidance(cfg_coef, description_empty):
+    return bool(load().mgx_use_guidance(cfg_coef, 1 if description_empty else 0))
+
+
+class Model:
+    """mgx_model: the weights of one LM uploaded to the current HIP device."""
+
+    def __init__(self, config, tensors):
+        self.lib = load()
+        self.config = config
+        arr = (Tensor * len(tensors))()
+        self._names = []
+        for i, (name, ttype, ne0, ne1, data) in enumerate(tensors):
+            b = name.encode()
+            self._names.append(b)
+            arr[i].name = b
+            arr[i].type = ttype
+            arr[i].ne[0], arr[i].ne[1], arr[i].ne[2], arr[i].ne[3] = ne0, ne1, 1, 1
+            arr[i].data = data.ctypes.data
+            arr[i].nbytes = data.nbytes
+        h = C.c_void_p()
+        _check(self.lib, self.lib.mgx_model_create(C.byref(config), arr, len(tensors), C.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            self.lib.mgx_model_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def generate(self, t5_hidden, prompt_codes, prompt_len, params, description_empty=False, step_logits=False):
+        """mg_generate: returns (codes [n_q][T], first_logits [n_q][card], report, step_logits|None)."""
+        c = self.config
+        T = params.max_gen_len
+        S = T + c.n_q
+        start = prompt_len + 1
+        codes = np.zeros((c.n_q, T), np.int32)
+        first = np.zeros((c.n_q, c.card), np.float32)
+        steps = np.zeros((S - start, c.n_q, c.card), np.float32) if step_logits else None
+        rep = GenerateReport()
+        t5 = np.ascontiguousarray(t5_hidden, np.float32)
+        prompt = np.ascontiguousarray(prompt_codes, np.int32) if prompt_len else None
+        _check(self.lib, self.lib.mgx_generate(self.handle, _ptr(t5), t5.shape[0], 1 if description_empty else 0,
+                                               _ptr(prompt), prompt_len, C.byref(params), _ptr(codes), _ptr(first),
+                                               _ptr(steps), C.byref(rep)))
+        return codes, first, rep, steps
+
+
+class Stream:
+    """mgx_stream: one Decoder (KV cache + projected memory) over a Model."""
+
+    def __init__(self, model, capacity, n_seq, t5_hidden=None, cross_attention=True):
+        self.lib = model.lib
+        self.model = model
+        self.n_seq = n_seq
+        t5 = None if t5_hidden is None else np.ascontiguousarray(t5_hidden, np.float32)
+        h = C.c_void_p()
+        _check(self.lib, self.lib.mgx_stream_create(model.handle, capacity, n_seq, _ptr(t5),
+                                                    0 if t5 is None else t5.shape[0], 1 if cross_attention else 0,
+                                                    C.byref(h)))
+        self.handle = h
+
+    def forward(self, ids):
+        """ids [n_q][n_tokens] -> logits [n_seq][n_q][card] of the last position."""
+        c = self.model.config
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.zeros((self.n_seq, c.n_q, c.card), np.float32)
+        _check(self.lib, self.lib.mgx_forward(self.handle, _ptr(ids), ids.shape[1], _ptr(out)))
+        return out
+
+    def used(self):
+        return self.lib.mgx_stream_used(self.handle)
+
+    def forwards(self):
+        return self.lib.mgx_stream_forwards(self.handle)
+
+    def cache_bytes(self):
+        return self.lib.mgx_stream_cache_bytes(self.handle)
+
+    def reset(self):
+        _check(self.lib, self.lib.mgx_stream_reset(self.handle))
+
+    def close(self):
+        if self.handle:
+            self.lib.mgx_stream_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

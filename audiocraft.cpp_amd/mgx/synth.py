@@ -1,0 +1,147 @@
+"""Seeded synthetic MusicGen LMs in ggml tensor formats (libmgx_synth.so).
+
+Every 2-D matrix is N(0, 0.02) -- embeddings [dim, card+1], heads, qkv, out, cross.q,
+cross.kv, cross.out, ff.0, ff.2 and cond_proj [cond_dim, dim] -- and cond_proj.bias is
+N(0, 0.02); LayerNorms are weight 1, bias 0. Matrices are stored as the requested ggml type
+(F32 0, F16 1, Q4_0 2, Q8_0 8); vectors stay F32. Names follow the converter's GGUF contract
+(tools/convert_musicgen_lm.py:149-210)."""
+import ctypes as C
+import os
+
+import numpy as np
+
+from .lib import LmConfig
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+SYNTH_PATH = os.path.join(os.path.dirname(_HERE), "libmgx_synth.so")
+
+# MusicGen LM shapes (hd 64, n_q 4, card 2048, T5-base memory width 768) plus a tiny one.
+SHAPES = {
+    "tiny": dict(dim=128, layers=2, heads=2, ff_dim=512, card=256, n_ctx=5),
+    "small": dict(dim=1024, layers=24, heads=16, ff_dim=4096, card=2048, n_ctx=12),
+    "medium": dict(dim=1536, layers=48, heads=24, ff_dim=6144, card=2048, n_ctx=24),
+    "large": dict(dim=2048, layers=48, heads=32, ff_dim=8192, card=2048, n_ctx=32),
+}
+
+_synth = None
+
+
+def _lib():
+    global _synth
+    if _synth is None:
+        if not os.path.exists(SYNTH_PATH):
+            raise RuntimeError(f"{SYNTH_PATH} is not built; run __graft_entry__.build()")
+        L = C.CDLL(SYNTH_PATH)
+        L.mgx_synth_seed.restype = C.c_uint64
+        L.mgx_synth_seed.argtypes = [C.c_uint64, C.c_char_p]
+        L.mgx_synth_normal.argtypes = [C.c_uint64, C.c_float, C.c_void_p, C.c_uint64]
+        L.mgx_synth_codes.argtypes = [C.c_uint64, C.c_int32, C.c_void_p, C.c_uint64]
+        L.mgx_row_bytes.restype = C.c_uint64
+        L.mgx_row_bytes.argtypes = [C.c_int, C.c_int64]
+        L.mgx_synth_tensor.argtypes = [C.c_uint64, C.c_int, C.c_int64, C.c_int64, C.c_float, C.c_float, C.c_void_p]
+        L.mgx_pack.argtypes = [C.c_int, C.c_void_p, C.c_int64, C.c_int64, C.c_void_p]
+        _synth = L
+    return _synth
+
+
+def make_config(shape, cfg_coef=3.0, **over):
+    s = dict(SHAPES[shape]) if isinstance(shape, str) else dict(shape)
+    s.update(over)
+    c = LmConfig()
+    c.dim, c.layers, c.heads = s["dim"], s["layers"], s["heads"]
+    c.head_dim = s["dim"] // s["heads"]
+    c.ff_dim = s["ff_dim"]
+    c.cond_dim = s.get("cond_dim", 768)
+    c.n_q = s.get("n_q", 4)
+    c.card = s["card"]
+    c.special_token_id = s["card"]
+    c.pos_denominator = s.get("pos_denominator", s["dim"] // 2 - 1)
+    c.max_period, c.norm_eps, c.cfg_coef = 10000.0, 1e-5, cfg_coef
+    return c
+
+
+def synth_memory(seed, n_ctx, cond_dim=768):
+    """The T5-base stand-in: [n_ctx][cond_dim] f32 N(0, 1)."""
+    out = np.empty((n_ctx, cond_dim), np.float32)
+    _lib().mgx_synth_normal(_lib().mgx_synth_seed(seed, b"t5.memory"), 1.0, out.ctypes.data, out.size)
+    return out
+
+
+def synth_codes(seed, n_q, length, card=2048):
+    """Uniform prompt codes [n_q][length] in [0, card)."""
+    out = np.empty((n_q, length), np.int32)
+    _lib().mgx_synth_codes(_lib().mgx_synth_seed(seed, b"prompt.codes"), card, out.ctypes.data, out.size)
+    return out
+
+
+def pack(ttype, x):
+    """Packs a float32 [rows][ne0] array into ggml bytes of `ttype`."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, ne0 = x.shape
+    out = np.empty(int(_lib().mgx_row_bytes(ttype, ne0)) * rows, np.uint8)
+    if _lib().mgx_pack(ttype, x.ctypes.data, ne0, rows, out.ctypes.data):
+        raise ValueError("cannot pack this shape")
+    return out
+
+
+class SyntheticModel:
+    """Tensors of one synthetic LM: list of (name, type, ne0, ne1, uint8 bytes)."""
+
+    def __init__(self, shape, wtype, seed=0, std=0.02, cfg_coef=3.0, **over):
+        self.config = make_config(shape, cfg_coef, **over)
+        self.wtype = wtype
+        self.seed = seed
+        c = self.config
+        L = _lib()
+        self.tensors = []
+
+        def mat(name, ne0, ne1, ttype=wtype, sd=std, const=0.0):
+            buf = np.empty(int(L.mgx_row_bytes(ttype, ne0)) * ne1, np.uint8)
+            if L.mgx_synth_tensor(L.mgx_synth_seed(seed, name.encode()), ttype, ne0, ne1, sd, const,
+                                  buf.ctypes.data):
+                raise ValueError(f"cannot synthesize {name}")
+            self.tensors.append((name, ttype, ne0, ne1, buf))
+
+        def vec(name, n, sd=0.0, const=0.0):
+            mat(name, n, 1, 0, sd, const)
+
+        d, F = c.dim, c.ff_dim
+        for q in range(c.n_q):
+            mat(f"lm.emb.{q}.weight", d, c.card + 1)
+        mat("lm.cond_proj.weight", c.cond_dim, d)
+        vec("lm.cond_proj.bias", d, sd=std)
+        for i in range(c.layers):
+            p = f"lm.{i}."
+            for norm in ("norm1", "norm_cross", "norm2"):
+                vec(p + norm + ".weight", d, const=1.0)
+                vec(p + norm + ".bias", d, const=0.0)
+            mat(p + "self.qkv.weight", d, 3 * d)
+            mat(p + "self.out.weight", d, d)
+            mat(p + "cross.q.weight", d, d)
+            mat(p + "cross.kv.weight", d, 2 * d)
+            mat(p + "cross.out.weight", d, d)
+            mat(p + "ff.0.weight", d, F)
+            mat(p + "ff.2.weight", F, d)
+        vec("lm.out_norm.weight", d, const=1.0)
+        vec("lm.out_norm.bias", d, const=0.0)
+        for q in range(c.n_q):
+            mat(f"lm.head.{q}.weight", d, c.card)
+
+    def tensor(self, name):
+        for t in self.tensors:
+            if t[0] == name:
+                return t
+        raise KeyError(name)
+
+    def replace(self, name, ttype, values):
+        """Swaps one tensor for caller values (float32 [ne1][ne0]) packed as `ttype`."""
+        for i, t in enumerate(self.tensors):
+            if t[0] == name:
+                v = np.ascontiguousarray(values, np.float32)
+                self.tensors[i] = (name, ttype, v.shape[1], v.shape[0], pack(ttype, v) if ttype != 0 else
+                                   v.view(np.uint8).reshape(-1).copy())
+                return
+        raise KeyError(name)
+
+    def nbytes(self):
+        return sum(t[4].nbytes for t in self.tensors)

@@ -1,0 +1,145 @@
+/*
+ * mgx.h -- C ABI of the MI355X (gfx950) MusicGen LM decode library.
+ *
+ * It replaces the ggml graph behind audiocraft.cpp's `ac::mg_generate` (src/mg/pipeline.cpp:
+ * 199-314): the `Decoder` class (pipeline.cpp:36-195) becomes an `mgx_stream`, the weights the
+ * `GgufModel` holds (src/gguf_model.h:241-346) become an `mgx_model`, and the loop body --
+ * forward, classifier-free-guidance mix and top-k sampling -- runs on the GPU. GGUF parsing, T5,
+ * the delay pattern's host bookkeeping, EnCodec and HTTP stay with the caller.
+ *
+ * Conventions: plain pointers and sizes; the caller owns every host buffer it passes; all
+ * host pointers are read or written before the call returns. Every entry point returns
+ * MGX_OK (0) or a negative status, with a message in mgx_last_error() (thread-local) -- the
+ * reference throws std::runtime_error at the same sites (kv_cache.h:73-77, pipeline.cpp:81-83,
+ * 98-99, 204-212; gguf_model.h:425-436), and a C++ caller rethrows the message.
+ *
+ * Threading: one caller thread per stream; distinct streams may be driven from distinct
+ * threads. The reference's server runs one job at a time (src/serve/http.h:201-205).
+ */
+#ifndef MGX_H
+#define MGX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    MGX_OK = 0,
+    MGX_ERR_INVALID = -1,   /* bad argument, shape or tensor */
+    MGX_ERR_DEVICE = -2,    /* HIP runtime or allocation failure */
+    MGX_ERR_OVERFLOW = -3,  /* KV cache overflow (kv_cache.h:73-77) */
+    MGX_ERR_STATE = -4      /* multi-token forward after history (pipeline.cpp:81-83) */
+};
+
+/* ggml type ids accepted for weight matrices (gguf_model.h passes them through). */
+enum { MGX_TYPE_F32 = 0, MGX_TYPE_F16 = 1, MGX_TYPE_Q4_0 = 2, MGX_TYPE_Q8_0 = 8 };
+
+typedef struct mgx_model mgx_model;
+typedef struct mgx_stream mgx_stream;
+
+/* ac::LmConfig (src/mg/lm.h:42-93), the `ac.lm.*` GGUF metadata. */
+typedef struct mgx_lm_config {
+    int32_t dim, layers, heads, head_dim, ff_dim, cond_dim, n_q, card, special_token_id, pos_denominator;
+    float max_period, norm_eps, cfg_coef;
+} mgx_lm_config;
+
+/* One GGUF tensor as ggml holds it: name (tools/convert_musicgen_lm.py:149-210), ggml type,
+   ne[] in ggml order (ne[0] contiguous), and the raw tensor bytes (ggml block layout). */
+typedef struct mgx_tensor {
+    const char* name;
+    int32_t type;
+    int64_t ne[4];
+    const void* data;
+    uint64_t nbytes;
+} mgx_tensor;
+
+/* One adapted projection, ac::LoraProjection (src/ac/lora.h:39-47) as load_lora builds it
+   (lora.h:113-176): A ggml [in, rank], B ggml [rank, out], f32; magnitude [out] for
+   "dora-rows" adapters, NULL for "lora". */
+typedef struct mgx_adapter {
+    const char* target;      /* "lm.<i>.{self.qkv,self.out,cross.q,cross.kv,cross.out,ff.0,ff.2}.weight" */
+    const float* A;
+    const float* B;
+    const float* magnitude;
+    int32_t rank;
+    float alpha;
+    float strength;
+} mgx_adapter;
+
+/* Replaces load_gguf's device upload (gguf_model.h:363-414) and LmConfig::from's checks
+   (lm.h:60-90): validates names, shapes and types and uploads the weights to the current
+   HIP device once. `tensors` may be freed after the call. */
+int mgx_model_create(const mgx_lm_config* cfg, const mgx_tensor* tensors, int32_t n_tensors, mgx_model** out);
+
+/* Attaches adapters (load_mg_lora, lora.h:195-210) for every later forward. DoRA rows on a
+   quantized base use the dequantized base rows for ||W||^2 (the reference throws there,
+   lora.h:11-13). n == 0 detaches. */
+int mgx_model_set_adapters(mgx_model* model, const mgx_adapter* adapters, int32_t n);
+
+void mgx_model_destroy(mgx_model* model);
+
+/* Decoder's constructor (pipeline.cpp:38-47): a KV cache of `capacity` positions for `n_seq`
+   streams (2 = guided: stream 0 conditional, stream 1 null). With `cross_attention` set,
+   `t5_hidden` [n_ctx][cond_dim] f32 is projected through lm.cond_proj once into stream 0
+   (stream 1 stays zero, pipeline.cpp:135-180) and every layer's cross.kv is projected from it
+   once as well (the reference recomputes it each step, lm.h:184; the values are the same). */
+int mgx_stream_create(mgx_model* model, int32_t capacity, int32_t n_seq, const float* t5_hidden, int32_t n_ctx,
+                      int32_t cross_attention, mgx_stream** out);
+
+/* Decoder::forward (pipeline.cpp:59-132): feeds n_tokens sequence steps, ids [n_q][n_tokens]
+   codebook-major, and writes the last step's logits [n_seq][n_q][card] (ggml [card, n_q,
+   n_seq]). A multi-token call is a prefill and needs an empty cache. */
+int mgx_forward(mgx_stream* stream, const int32_t* ids, int32_t n_tokens, float* logits_out);
+
+/* KvCache::reset / used / Decoder::forwards / cache_bytes (kv_cache.h:69-81, pipeline.cpp:54-55). */
+int mgx_stream_reset(mgx_stream* stream);
+int32_t mgx_stream_used(const mgx_stream* stream);
+int32_t mgx_stream_forwards(const mgx_stream* stream);
+uint64_t mgx_stream_cache_bytes(const mgx_stream* stream);
+void mgx_stream_destroy(mgx_stream* stream);
+
+/* mg_use_guidance (pipeline.h:41-43). */
+int32_t mgx_use_guidance(float cfg_coef, int32_t description_empty);
+
+/* GenerateParams (pipeline.h:25-34). */
+typedef struct mgx_generate_params {
+    int32_t max_gen_len;
+    int32_t use_sampling;
+    float temperature;
+    int32_t top_k;
+    float cfg_coef;
+    uint64_t seed;
+} mgx_generate_params;
+
+/* GenerateReport (pipeline.h:45-56); first_logits is returned through its own buffer. */
+typedef struct mgx_generate_report {
+    uint64_t cache_bytes;
+    int32_t prefill_tokens;
+    int32_t decode_steps;
+    int32_t forwards;
+    double prefill_seconds;
+    double decode_seconds;
+} mgx_generate_report;
+
+/* ac::mg_generate (pipeline.cpp:199-314): prompt_codes [n_q][prompt_len], t5_hidden
+   [n_ctx][cond_dim]; codes_out [n_q][max_gen_len] (prompt included); first_logits_out
+   [n_q][card] (the guided mix of the first prediction, pipeline.cpp:275-276);
+   step_logits_out, if not NULL, [S - start][n_q][card] with the mixed logits of every
+   forward. The sampling stream is the reference's: mt19937(seed), one uniform per sampled
+   (step, codebook) slot in step-then-codebook order (pipeline.cpp:278-288, rng.h:20-22). */
+int mgx_generate(mgx_model* model, const float* t5_hidden, int32_t n_ctx, int32_t description_empty,
+                 const int32_t* prompt_codes, int32_t prompt_len, const mgx_generate_params* params,
+                 int32_t* codes_out, float* first_logits_out, float* step_logits_out,
+                 mgx_generate_report* report);
+
+/* The message of the last failed call on this thread. */
+const char* mgx_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MGX_H */
