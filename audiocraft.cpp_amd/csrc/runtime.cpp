@@ -111,10 +111,26 @@ struct mgx_stream {
     uint16_t* ah = nullptr;
     float* af = nullptr;
     int32_t* ids = nullptr;                  // [n_q][cap] staged ids for mgx_forward
+    // Launch timing: when `prof_on`, every GEMV and attention launch of a sampled step is
+    // bracketed by HIP events on this stream; read back by the session's profile call.
+    struct Mark { hipEvent_t a, b; int kind; double bytes; };
+    bool prof_on = false;
+    std::vector<Mark> marks;
+    std::vector<hipEvent_t> event_pool;
+    size_t event_next = 0;
     ~mgx_stream() {
         if (hs) (void)hipStreamSynchronize(hs);
         mem.release();
+        for (hipEvent_t e : event_pool) (void)hipEventDestroy(e);
         if (hs) (void)hipStreamDestroy(hs);
+    }
+    hipEvent_t event() {
+        if (event_next == event_pool.size()) {
+            hipEvent_t e;
+            HIP_OK(hipEventCreate(&e));
+            event_pool.push_back(e);
+        }
+        return event_pool[event_next++];
     }
     mgx::ActBuf act(int wtype) const {
         mgx::ActBuf a{};
@@ -225,10 +241,41 @@ std::vector<float> sin_table(int n, const mgx_lm_config& c) {
     return out;
 }
 
-// One projection of `ncol` activation columns already in s->act(type).
+double bytes_per_weight(int type) {
+    switch (type) {
+    case mgx::T_Q8_0: return 34.0 / 32.0;
+    case mgx::T_Q4_0: return 18.0 / 32.0;
+    case mgx::T_F16: return 2.0;
+    }
+    return 4.0;
+}
+
+enum { PROF_GEMV = 0, PROF_ATTN = 1 };
+
+struct ProfScope {
+    mgx_stream* s;
+    hipEvent_t b = nullptr;
+    int kind;
+    double bytes;
+    ProfScope(mgx_stream* st, int k, double by) : s(st), kind(k), bytes(by) {
+        if (s->prof_on) {
+            hipEvent_t a = s->event();
+            b = s->event();
+            HIP_OK(hipEventRecord(a, s->hs));
+            s->marks.push_back({a, b, kind, bytes});
+        }
+    }
+    ~ProfScope() {
+        if (b) (void)hipEventRecord(b, s->hs);
+    }
+};
+
+// One projection of `ncol` activation columns already in s->act(type). Algorithmic bytes
+// of a launch = the weights at their stored precision.
 void gemv(mgx_stream* s, const mgx::DevMat& w, int ncol, const mgx::GemvOut& o) {
     mgx::GemvArgs a{};
     a.w = w; a.act = s->act(w.type); a.ncol = ncol; a.o = o;
+    ProfScope ps(s, PROF_GEMV, (double)w.in * w.out * bytes_per_weight(w.type));
     mgx::launch_gemv(a, s->hs);
 }
 
@@ -275,7 +322,11 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int position, bool 
         at.q = s->qb; at.k = Kl; at.v = Vl; at.scores = s->scores; at.opart = s->opart; at.dim = D;
         at.heads = c.heads; at.cap = s->cap; at.position = position; at.max_chunks = s->max_chunks;
         at.ncol = N; at.scale = scale;
-        mgx::launch_attention(at, s->act(L.w[P_OUT].type), s->hs);
+        {
+            // f32 K and V of every key attended, both streams
+            ProfScope ps(s, PROF_ATTN, 2.0 * N * c.heads * (position + 1) * 64 * 4);
+            mgx::launch_attention(at, s->act(L.w[P_OUT].type), s->hs);
+        }
         gemv(s, L.w[P_OUT], N, out_resid(s->x, D));
         // cross-attention, conditional stream only (the null stream's contribution is 0)
         if (s->cross) {
@@ -485,101 +536,237 @@ uint64_t mgx_stream_cache_bytes(const mgx_stream* s) {
 }
 void mgx_stream_destroy(mgx_stream* s) { delete s; }
 
+}  // extern "C"
+
+// ------------------------------------------------------------------------------------
+// generation sessions: mg_generate (pipeline.cpp:199-314) cut into resumable pieces
+// ------------------------------------------------------------------------------------
+struct mgx_session {
+    mgx_model* m = nullptr;
+    std::unique_ptr<mgx_stream> s;
+    DevArena mem;
+    int K = 0, T = 0, S = 0, start = 0, next = 0;   // next: the next loop offset to run
+    bool guided = false;
+    std::vector<int32_t> seq;
+    int32_t* dseq = nullptr;
+    float *dfirst = nullptr, *dsteps = nullptr;
+    mgx::SampleArgs sa{};
+    double prefill_seconds = 0.0, decode_seconds = 0.0;
+    int prof_every = 0;
+    ~mgx_session() {
+        if (s && s->hs) (void)hipStreamSynchronize(s->hs);
+        mem.release();
+    }
+    int pattern_t(int q, int step) const { const int t = step - 1 - q; return (step > 0 && t >= 0 && t < T) ? t : -1; }
+};
+
+namespace {
+
+void session_create(mgx_model* m, const float* t5_hidden, int32_t n_ctx, int32_t description_empty,
+                    const int32_t* prompt, int32_t prompt_len, const mgx_generate_params* p, int keep_steps,
+                    mgx_session** out) {
+    if (!m || !p || !out) throw Error(MGX_ERR_INVALID, "null argument");
+    *out = nullptr;
+    const mgx_lm_config& c = m->c;
+    const int K = c.n_q, T = p->max_gen_len;
+    if (T <= 0) throw Error(MGX_ERR_INVALID, "max_gen_len must be positive");
+    if (prompt_len < 0 || prompt_len >= T) throw Error(MGX_ERR_INVALID, "the prompt must be shorter than the generation");
+    if (prompt_len > 0 && !prompt) throw Error(MGX_ERR_INVALID, "prompt codes do not hold n_q * prompt_len values");
+    if (n_ctx <= 0) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
+    for (int64_t i = 0; i < (int64_t)K * prompt_len; ++i)
+        if (prompt[i] < 0 || prompt[i] >= c.card) throw Error(MGX_ERR_INVALID, "prompt code out of range");
+    auto ss = std::make_unique<mgx_session>();
+    ss->m = m; ss->K = K; ss->T = T;
+    // DelayPattern with delays 0..n_q-1 (pattern.h:31-115): S = T + n_q, start = P + 1.
+    ss->S = 1 + T + (K - 1);
+    ss->start = prompt_len + 1;
+    ss->next = ss->start;
+    const int S = ss->S, start = ss->start;
+    ss->seq.assign((size_t)K * S, c.special_token_id);
+    std::vector<uint8_t> mask((size_t)K * S, 0);
+    for (int q = 0; q < K; ++q)
+        for (int st = 0; st < S; ++st) {
+            const int t = ss->pattern_t(q, st);
+            if (t < 0) continue;
+            mask[(size_t)q * S + st] = 1;
+            ss->seq[(size_t)q * S + st] = t < prompt_len ? prompt[(size_t)q * prompt_len + t] : -1;
+        }
+    ss->guided = mgx_use_guidance(p->cfg_coef, description_empty) != 0;
+    const bool sampling = p->use_sampling && p->temperature > 0.0f;
+    // The reference draws one uniform per sampled slot, step by step and codebook by
+    // codebook (pipeline.cpp:278-288, rng.h:20-22); which slots draw depends only on the
+    // mask, so the whole stream is drawn here.
+    std::vector<float> uni((size_t)S * K, 0.0f);
+    if (sampling) {
+        std::mt19937 g((uint32_t)p->seed);
+        for (int st = start; st < S; ++st)
+            for (int q = 0; q < K; ++q)
+                if (mask[(size_t)q * S + st]) uni[(size_t)st * K + q] = ((g() >> 8) + 0.5f) * (1.0f / 16777216.0f);
+    }
+    mgx_stream* raw = nullptr;
+    make_stream(m, S, ss->guided ? 2 : 1, t5_hidden, n_ctx, ss->guided ? 1 : 0, &raw);
+    ss->s.reset(raw);
+    mgx_stream* st = ss->s.get();
+    ss->dseq = ss->mem.alloc<int32_t>(ss->seq.size());
+    uint8_t* dmask = ss->mem.alloc<uint8_t>(mask.size());
+    float* duni = ss->mem.alloc<float>(uni.size());
+    ss->dfirst = ss->mem.alloc<float>((size_t)K * c.card);
+    if (keep_steps) ss->dsteps = ss->mem.alloc<float>((size_t)(S - start) * K * c.card);
+    HIP_OK(hipMemcpyAsync(ss->dseq, ss->seq.data(), ss->seq.size() * 4, hipMemcpyHostToDevice, st->hs));
+    HIP_OK(hipMemcpyAsync(dmask, mask.data(), mask.size(), hipMemcpyHostToDevice, st->hs));
+    HIP_OK(hipMemcpyAsync(duni, uni.data(), uni.size() * 4, hipMemcpyHostToDevice, st->hs));
+    HIP_OK(hipStreamSynchronize(st->hs));
+    mgx::SampleArgs& sa = ss->sa;
+    sa.logits = st->logits; sa.n_q = K; sa.card = c.card; sa.guided = ss->guided; sa.cfg_coef = p->cfg_coef;
+    sa.mask = dmask; sa.steps = S; sa.use_sampling = p->use_sampling; sa.temperature = p->temperature;
+    sa.top_k = p->top_k; sa.uniforms = duni; sa.special = c.special_token_id; sa.seq = ss->dseq;
+    *out = ss.release();
+}
+
+// Runs up to n more loop iterations (the first is the prefill), then waits for them.
+int session_step(mgx_session* ss, int n) {
+    mgx_stream* s = ss->s.get();
+    const mgx_lm_config& c = ss->m->c;
+    HIP_OK(hipSetDevice(ss->m->device));
+    const double t0 = now_s();
+    const int first = ss->next;
+    int done = 0;
+    for (; done < n && ss->next < ss->S; ++done) {
+        const int offset = ss->next++;
+        const bool sampled_step = ss->prof_every > 0 && (offset - ss->start) % ss->prof_every == 0;
+        s->prof_on = sampled_step;
+        if (offset == ss->start)
+            for (int pos = 0; pos < ss->start; ++pos) step(s, ss->dseq + pos, ss->S, pos, pos == ss->start - 1);
+        else
+            step(s, ss->dseq + (offset - 1), ss->S, offset - 1, true);
+        s->prof_on = false;
+        ss->sa.offset = offset;
+        ss->sa.first_logits = offset == ss->start ? ss->dfirst : nullptr;
+        ss->sa.step_logits = ss->dsteps ? ss->dsteps + (size_t)(offset - ss->start) * ss->K * c.card : nullptr;
+        mgx::launch_sample(ss->sa, s->hs);
+        if (offset == ss->start) {
+            HIP_OK(hipGetLastError());
+            HIP_OK(hipStreamSynchronize(s->hs));
+            ss->prefill_seconds += now_s() - t0;
+        }
+    }
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipStreamSynchronize(s->hs));
+    if (done > 0) {
+        // decode time excludes the prefill iteration, as report.decode_seconds does
+        double el = now_s() - t0;
+        if (first == ss->start) el -= ss->prefill_seconds;
+        ss->decode_seconds += el;
+    }
+    s->used = ss->next > ss->start ? ss->next - 1 : 0;
+    s->forwards = ss->next - ss->start;
+    return done;
+}
+
+void session_finish(mgx_session* ss, int32_t* codes_out, float* first_logits_out, float* step_logits_out,
+                    mgx_generate_report* rep) {
+    const mgx_lm_config& c = ss->m->c;
+    mgx_stream* s = ss->s.get();
+    const int K = ss->K, T = ss->T, S = ss->S;
+    if (rep) {
+        rep->prefill_tokens = ss->start;
+        rep->decode_steps = S - ss->start - 1;
+        rep->forwards = ss->next - ss->start;
+        rep->prefill_seconds = ss->prefill_seconds;
+        rep->decode_seconds = ss->decode_seconds;
+        rep->cache_bytes = mgx_stream_cache_bytes(s);
+    }
+    HIP_OK(hipMemcpy(ss->seq.data(), ss->dseq, ss->seq.size() * 4, hipMemcpyDeviceToHost));
+    if (first_logits_out && ss->next > ss->start)
+        HIP_OK(hipMemcpy(first_logits_out, ss->dfirst, sizeof(float) * (size_t)K * c.card, hipMemcpyDeviceToHost));
+    if (step_logits_out && ss->dsteps)
+        HIP_OK(hipMemcpy(step_logits_out, ss->dsteps, sizeof(float) * (size_t)(S - ss->start) * K * c.card,
+                         hipMemcpyDeviceToHost));
+    if (!codes_out) return;
+    // revert_pattern_sequence + the final check (pipeline.cpp:307-313)
+    for (size_t i = 0; i < (size_t)K * T; ++i) codes_out[i] = c.special_token_id;
+    for (int q = 0; q < K; ++q)
+        for (int st = 0; st < S; ++st) {
+            const int t = ss->pattern_t(q, st);
+            if (t >= 0) codes_out[(size_t)q * T + t] = ss->seq[(size_t)q * S + st];
+        }
+    if (ss->next == S)
+        for (size_t i = 0; i < (size_t)K * T; ++i)
+            if (codes_out[i] < 0 || codes_out[i] >= c.card)
+                throw Error(MGX_ERR_INVALID, "the generated sequence has a position the pattern never filled");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mgx_session_create(mgx_model* m, const float* t5_hidden, int32_t n_ctx, int32_t description_empty,
+                       const int32_t* prompt_codes, int32_t prompt_len, const mgx_generate_params* params,
+                       int32_t keep_step_logits, mgx_session** out) {
+    return guarded([&] {
+        session_create(m, t5_hidden, n_ctx, description_empty, prompt_codes, prompt_len, params, keep_step_logits, out);
+    });
+}
+
+int mgx_session_step(mgx_session* ss, int32_t n_forwards, int32_t* done) {
+    return guarded([&] {
+        if (!ss) throw Error(MGX_ERR_INVALID, "null session");
+        const int d = session_step(ss, n_forwards);
+        if (done) *done = d;
+    });
+}
+
+int32_t mgx_session_remaining(const mgx_session* ss) { return ss ? ss->S - ss->next : -1; }
+
+int mgx_session_finish(mgx_session* ss, int32_t* codes_out, float* first_logits_out, float* step_logits_out,
+                       mgx_generate_report* report) {
+    return guarded([&] {
+        if (!ss) throw Error(MGX_ERR_INVALID, "null session");
+        session_finish(ss, codes_out, first_logits_out, step_logits_out, report);
+    });
+}
+
+int mgx_session_profile(mgx_session* ss, int32_t every) {
+    return guarded([&] {
+        if (!ss) throw Error(MGX_ERR_INVALID, "null session");
+        if (every < 0) throw Error(MGX_ERR_INVALID, "every must be >= 0");
+        ss->prof_every = every;
+    });
+}
+
+int mgx_session_profile_read(mgx_session* ss, int32_t kind, double* ms_total, double* bytes_total, int32_t* launches) {
+    return guarded([&] {
+        if (!ss) throw Error(MGX_ERR_INVALID, "null session");
+        mgx_stream* s = ss->s.get();
+        HIP_OK(hipStreamSynchronize(s->hs));
+        double ms = 0.0, by = 0.0;
+        int n = 0;
+        for (const auto& mk : s->marks) {
+            if (mk.kind != kind) continue;
+            float e = 0.0f;
+            HIP_OK(hipEventElapsedTime(&e, mk.a, mk.b));
+            ms += e; by += mk.bytes; ++n;
+        }
+        if (ms_total) *ms_total = ms;
+        if (bytes_total) *bytes_total = by;
+        if (launches) *launches = n;
+    });
+}
+
+void* mgx_session_hip_stream(mgx_session* ss) { return ss ? (void*)ss->s->hs : nullptr; }
+
+void mgx_session_destroy(mgx_session* ss) { delete ss; }
+
 int mgx_generate(mgx_model* m, const float* t5_hidden, int32_t n_ctx, int32_t description_empty,
                  const int32_t* prompt, int32_t prompt_len, const mgx_generate_params* p,
                  int32_t* codes_out, float* first_logits_out, float* step_logits_out, mgx_generate_report* rep) {
     return guarded([&] {
-        if (!m || !p || !codes_out || !rep) throw Error(MGX_ERR_INVALID, "null argument");
-        const mgx_lm_config& c = m->c;
-        const int K = c.n_q, T = p->max_gen_len;
-        if (T <= 0) throw Error(MGX_ERR_INVALID, "max_gen_len must be positive");
-        if (prompt_len < 0 || prompt_len >= T) throw Error(MGX_ERR_INVALID, "the prompt must be shorter than the generation");
-        if (prompt_len > 0 && !prompt) throw Error(MGX_ERR_INVALID, "prompt codes do not hold n_q * prompt_len values");
-        if (n_ctx <= 0) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
-        for (int64_t i = 0; i < (int64_t)K * prompt_len; ++i)
-            if (prompt[i] < 0 || prompt[i] >= c.card) throw Error(MGX_ERR_INVALID, "prompt code out of range");
-        // DelayPattern with delays 0..n_q-1 (pattern.h:31-115): S = T + n_q, start = P + 1.
-        const int S = 1 + T + (K - 1), start = prompt_len + 1;
-        auto at = [&](int q, int s) { const int t = s - 1 - q; return (s > 0 && t >= 0 && t < T) ? t : -1; };
-        std::vector<int32_t> seq((size_t)K * S, c.special_token_id);
-        std::vector<uint8_t> mask((size_t)K * S, 0);
-        for (int q = 0; q < K; ++q)
-            for (int s = 0; s < S; ++s) {
-                const int t = at(q, s);
-                if (t < 0) continue;
-                mask[(size_t)q * S + s] = 1;
-                seq[(size_t)q * S + s] = t < prompt_len ? prompt[(size_t)q * prompt_len + t] : -1;
-            }
-        const bool guided = mgx_use_guidance(p->cfg_coef, description_empty) != 0;
-        const bool sampling = p->use_sampling && p->temperature > 0.0f;
-        // The reference draws one uniform per sampled slot, step by step and codebook by
-        // codebook; which slots draw depends only on the mask, so the stream is fixed here.
-        std::vector<float> uni((size_t)S * K, 0.0f);
-        {
-            std::mt19937 g((uint32_t)p->seed);
-            if (sampling)
-                for (int s = start; s < S; ++s)
-                    for (int q = 0; q < K; ++q)
-                        if (mask[(size_t)q * S + s]) uni[(size_t)s * K + q] = ((g() >> 8) + 0.5f) * (1.0f / 16777216.0f);
-        }
-        mgx_stream* raw = nullptr;
-        make_stream(m, S, guided ? 2 : 1, t5_hidden, n_ctx, guided ? 1 : 0, &raw);
-        std::unique_ptr<mgx_stream> s(raw);
-        DevArena mem;
-        struct Rel { DevArena& a; ~Rel() { a.release(); } } rel{mem};
-        int32_t* dseq = mem.alloc<int32_t>(seq.size());
-        uint8_t* dmask = mem.alloc<uint8_t>(mask.size());
-        float* duni = mem.alloc<float>(uni.size());
-        float* dfirst = mem.alloc<float>((size_t)K * c.card);
-        float* dsteps = step_logits_out ? mem.alloc<float>((size_t)(S - start) * K * c.card) : nullptr;
-        HIP_OK(hipMemcpyAsync(dseq, seq.data(), seq.size() * 4, hipMemcpyHostToDevice, s->hs));
-        HIP_OK(hipMemcpyAsync(dmask, mask.data(), mask.size(), hipMemcpyHostToDevice, s->hs));
-        HIP_OK(hipMemcpyAsync(duni, uni.data(), uni.size() * 4, hipMemcpyHostToDevice, s->hs));
-        HIP_OK(hipStreamSynchronize(s->hs));
-        mgx::SampleArgs sa{};
-        sa.logits = s->logits; sa.n_q = K; sa.card = c.card; sa.guided = guided; sa.cfg_coef = p->cfg_coef;
-        sa.mask = dmask; sa.steps = S; sa.use_sampling = p->use_sampling; sa.temperature = p->temperature;
-        sa.top_k = p->top_k; sa.uniforms = duni; sa.special = c.special_token_id; sa.seq = dseq;
-        rep->prefill_tokens = start;
-        rep->decode_steps = S - start - 1;
-        double t0 = now_s();
-        for (int offset = start; offset < S; ++offset) {
-            if (offset == start)
-                for (int pos = 0; pos < start; ++pos) step(s.get(), dseq + pos, S, pos, pos == start - 1);
-            else
-                step(s.get(), dseq + (offset - 1), S, offset - 1, true);
-            sa.offset = offset;
-            sa.first_logits = offset == start ? dfirst : nullptr;
-            sa.step_logits = dsteps ? dsteps + (size_t)(offset - start) * K * c.card : nullptr;
-            mgx::launch_sample(sa, s->hs);
-            if (offset == start) {
-                HIP_OK(hipGetLastError());
-                HIP_OK(hipStreamSynchronize(s->hs));
-                rep->prefill_seconds = now_s() - t0;
-                t0 = now_s();
-            }
-        }
-        HIP_OK(hipGetLastError());
-        HIP_OK(hipStreamSynchronize(s->hs));
-        rep->decode_seconds = now_s() - t0;
-        s->used = S;
-        s->forwards = S - start;
-        rep->forwards = S - start;
-        rep->cache_bytes = mgx_stream_cache_bytes(s.get());
-        HIP_OK(hipMemcpy(seq.data(), dseq, seq.size() * 4, hipMemcpyDeviceToHost));
-        if (first_logits_out) HIP_OK(hipMemcpy(first_logits_out, dfirst, sizeof(float) * (size_t)K * c.card, hipMemcpyDeviceToHost));
-        if (step_logits_out)
-            HIP_OK(hipMemcpy(step_logits_out, dsteps, sizeof(float) * (size_t)(S - start) * K * c.card, hipMemcpyDeviceToHost));
-        // revert_pattern_sequence + the final check (pipeline.cpp:307-313)
-        for (size_t i = 0; i < (size_t)K * T; ++i) codes_out[i] = c.special_token_id;
-        for (int q = 0; q < K; ++q)
-            for (int s2 = 0; s2 < S; ++s2) {
-                const int t = at(q, s2);
-                if (t >= 0) codes_out[(size_t)q * T + t] = seq[(size_t)q * S + s2];
-            }
-        for (size_t i = 0; i < (size_t)K * T; ++i)
-            if (codes_out[i] < 0 || codes_out[i] >= c.card)
-                throw Error(MGX_ERR_INVALID, "the generated sequence has a position the pattern never filled");
+        if (!codes_out || !rep) throw Error(MGX_ERR_INVALID, "null argument");
+        mgx_session* raw = nullptr;
+        session_create(m, t5_hidden, n_ctx, description_empty, prompt, prompt_len, p, step_logits_out != nullptr, &raw);
+        std::unique_ptr<mgx_session> ss(raw);
+        session_step(ss.get(), ss->S);
+        session_finish(ss.get(), codes_out, first_logits_out, step_logits_out, rep);
     });
 }
 

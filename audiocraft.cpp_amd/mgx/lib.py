@@ -47,7 +47,9 @@ class GenerateReport(C.Structure):
 
 EXPORTS = ["mgx_model_create", "mgx_model_set_adapters", "mgx_model_destroy", "mgx_stream_create", "mgx_forward",
            "mgx_stream_reset", "mgx_stream_used", "mgx_stream_forwards", "mgx_stream_cache_bytes",
-           "mgx_stream_destroy", "mgx_use_guidance", "mgx_generate", "mgx_last_error"]
+           "mgx_stream_destroy", "mgx_use_guidance", "mgx_generate", "mgx_session_create", "mgx_session_step",
+           "mgx_session_remaining", "mgx_session_finish", "mgx_session_destroy", "mgx_session_profile",
+           "mgx_session_profile_read", "mgx_session_hip_stream", "mgx_last_error"]
 
 _lib = None
 
@@ -79,6 +81,18 @@ def load(path=None):
     lib.mgx_use_guidance.argtypes = [C.c_float, C.c_int32]
     lib.mgx_generate.argtypes = [P, P, C.c_int32, C.c_int32, P, C.c_int32, C.POINTER(GenerateParams), P, P, P,
                                  C.POINTER(GenerateReport)]
+    lib.mgx_session_create.argtypes = [P, P, C.c_int32, C.c_int32, P, C.c_int32, C.POINTER(GenerateParams),
+                                       C.c_int32, C.POINTER(P)]
+    lib.mgx_session_step.argtypes = [P, C.c_int32, C.POINTER(C.c_int32)]
+    lib.mgx_session_remaining.argtypes = [P]
+    lib.mgx_session_finish.argtypes = [P, P, P, P, C.POINTER(GenerateReport)]
+    lib.mgx_session_destroy.argtypes = [P]
+    lib.mgx_session_destroy.restype = None
+    lib.mgx_session_profile.argtypes = [P, C.c_int32]
+    lib.mgx_session_profile_read.argtypes = [P, C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                             C.POINTER(C.c_int32)]
+    lib.mgx_session_hip_stream.restype = P
+    lib.mgx_session_hip_stream.argtypes = [P]
     if path is None:
         _lib = lib
     return lib
@@ -183,6 +197,68 @@ class Stream:
     def close(self):
         if self.handle:
             self.lib.mgx_stream_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Session:
+    """mgx_session: mg_generate cut into resumable pieces (prefill first, then decodes)."""
+
+    def __init__(self, model, t5_hidden, prompt_codes, prompt_len, params, description_empty=False,
+                 keep_step_logits=False):
+        self.lib = model.lib
+        self.model = model
+        self.params = params
+        self.prompt_len = prompt_len
+        self.keep = keep_step_logits
+        t5 = np.ascontiguousarray(t5_hidden, np.float32)
+        prompt = np.ascontiguousarray(prompt_codes, np.int32) if prompt_len else None
+        h = C.c_void_p()
+        _check(self.lib, self.lib.mgx_session_create(model.handle, _ptr(t5), t5.shape[0], 1 if description_empty else 0,
+                                                     _ptr(prompt), prompt_len, C.byref(params),
+                                                     1 if keep_step_logits else 0, C.byref(h)))
+        self.handle = h
+
+    def step(self, n):
+        done = C.c_int32()
+        _check(self.lib, self.lib.mgx_session_step(self.handle, n, C.byref(done)))
+        return done.value
+
+    def remaining(self):
+        return self.lib.mgx_session_remaining(self.handle)
+
+    def profile(self, every):
+        _check(self.lib, self.lib.mgx_session_profile(self.handle, every))
+
+    def profile_read(self, kind):
+        ms, by, n = C.c_double(), C.c_double(), C.c_int32()
+        _check(self.lib, self.lib.mgx_session_profile_read(self.handle, kind, C.byref(ms), C.byref(by), C.byref(n)))
+        return ms.value, by.value, n.value
+
+    def hip_stream(self):
+        return self.lib.mgx_session_hip_stream(self.handle)
+
+    def finish(self):
+        c = self.model.config
+        T = self.params.max_gen_len
+        S = T + c.n_q
+        start = self.prompt_len + 1
+        codes = np.zeros((c.n_q, T), np.int32)
+        first = np.zeros((c.n_q, c.card), np.float32)
+        steps = np.zeros((S - start, c.n_q, c.card), np.float32) if self.keep else None
+        rep = GenerateReport()
+        _check(self.lib, self.lib.mgx_session_finish(self.handle, _ptr(codes), _ptr(first), _ptr(steps),
+                                                     C.byref(rep)))
+        return codes, first, rep, steps
+
+    def close(self):
+        if self.handle:
+            self.lib.mgx_session_destroy(self.handle)
             self.handle = None
 
     def __del__(self):

@@ -1,0 +1,194 @@
+#!/usr/bin/env python3
+"""Benchmark: MusicGen LM decode frames/s (and HBM GB/s) on one MI355X.
+
+A step is one decode forward of the LM -- one delay-pattern sequence step, 4 codes, 20 ms of
+audio -- including the on-device CFG mix and top-k sampling, exactly the loop body of the
+reference's mg_generate (src/mg/pipeline.cpp:255-302). The workload is MusicGen-medium-shaped
+(48 layers, dim 1536, 24 heads, FFN 6144, 4 x 2048 codebooks) with random N(0, 0.02) weights
+quantized to Q8_0, CFG 3 over two streams, a 24 x 768 N(0,1) memory, a 500-frame random-code
+prompt (prefilled, untimed) and a 1500-frame continuation sampled with top-k 250, temperature 1,
+seed 1. W warmup decode steps run untimed, then exactly K decode steps are timed; if the
+continuation runs out, a fresh session is prefilled outside the timed segments.
+
+Prints one JSON line. `value` is decode frames/s; `roofline` is the Q8_0 GEMV family's
+achieved HBM bandwidth (weight bytes at 34/32 B per weight over HIP-event-timed launch
+durations of every 64th timed step); `cpu_baseline` times the oracle's CPU restatement of the
+reference decode step on the host for a bounded sample of the same workload.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "audiocraft.cpp_amd"))
+sys.path.insert(0, ROOT)
+
+WORKLOADS = {
+    # name: shape, ggml weight type, prompt frames, continuation frames (max_gen_len = prompt + gen), seed, n_ctx
+    "medium-q8": dict(shape="medium", wtype=8, prompt=500, gen=1500, seed=1, n_ctx=24,
+                      desc="musicgen-medium-shaped LM, Q8_0, CFG 2 streams, 500-frame prompt + 1500-frame continuation"),
+    "small-q8": dict(shape="small", wtype=8, prompt=250, gen=500, seed=0, n_ctx=12,
+                     desc="musicgen-small-shaped LM, Q8_0, CFG 2 streams, 250-frame prompt + 500-frame continuation"),
+    "small-f16": dict(shape="small", wtype=1, prompt=500, gen=1500, seed=0, n_ctx=12,
+                      desc="musicgen-small-shaped LM, F16, CFG 2 streams, 500-frame prompt + 1500-frame continuation"),
+    "large-q4": dict(shape="large", wtype=2, prompt=1500, gen=1500, seed=1, n_ctx=32,
+                     desc="musicgen-large-shaped LM, Q4_0, CFG 2 streams, 1500-frame prompt + 1500-frame continuation"),
+}
+BPW = {8: 34 / 32, 2: 18 / 32, 1: 2.0, 0: 4.0}
+HBM_PEAK_GBS = 8000.0
+
+
+def step_bytes(c, wbpw, n_seq, n_ctx, u):
+    """Algorithmic HBM bytes of one decode step attending u keys: weights at stored precision
+    (cross.kv excluded: projected once per request) + f32 LN params + f32 K/V read and write +
+    the conditional stream's cross K/V + logits."""
+    L, d, F, Q, C = c.layers, c.dim, c.ff_dim, c.n_q, c.card
+    w = (L * (3 * d * d + d * d + d * d + d * d + 2 * d * F) + Q * C * d + Q * d) * wbpw + (6 * L + 2) * d * 4
+    kv_read = 2 * L * d * u * n_seq * 4
+    kv_write = 2 * L * d * n_seq * 4
+    xkv = 2 * L * d * n_ctx * 4
+    return w + kv_read + kv_write + xkv + Q * C * n_seq * 4
+
+
+def hip_sync():
+    lib = ctypes.CDLL("libamdhip64.so.7")
+    rc = lib.hipDeviceSynchronize()
+    if rc:
+        raise RuntimeError(f"hipDeviceSynchronize failed: {rc}")
+
+
+def cpu_baseline(w, model, t5, prompt, seconds):
+    """The oracle (a CPU restatement of the reference's ggml-CPU decode step, including its
+    per-step cross.kv projection) on the host: prefill untimed, then decode steps for about
+    `seconds` of wall time."""
+    from oracle import cpu_ref as R
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    R.set_threads(threads)
+    rm = R.RefModel(model.config, model.tensors)
+    # calibrate on a few steps, then run the bounded sample
+    T = w["prompt"] + w["gen"]
+    _, _, rep, _ = rm.generate(t5, prompt, w["prompt"], T, top_k=250, temperature=1.0, cfg_coef=3.0,
+                               seed=w["seed"], recompute_cross_kv=True, max_forwards=4)
+    per = max(rep.decode_seconds / 3, 1e-3)
+    n = max(4, min(w["gen"], int(seconds / per)))
+    _, _, rep, _ = rm.generate(t5, prompt, w["prompt"], T, top_k=250, temperature=1.0, cfg_coef=3.0,
+                               seed=w["seed"], recompute_cross_kv=True, max_forwards=n + 1)
+    steps = rep.forwards - 1
+    return dict(value=round(steps / rep.decode_seconds, 3), unit="frames/s", cores=R.lib().ref_get_threads(),
+                kind="port",
+                sample=f"oracle CPU restatement of the reference ggml path, same workload: {w['prompt'] + 1}-token "
+                       f"prefill untimed, then the first {steps} decode steps timed "
+                       f"({rep.decode_seconds:.1f} s, prefill {rep.prefill_seconds:.1f} s)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1500)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="medium-q8", choices=sorted(WORKLOADS))
+    ap.add_argument("--profile-every", type=int, default=64)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} requested). "
+              "The decode step shards by request; see DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+    import mgx
+    w = WORKLOADS[args.workload]
+    mgx.load()
+    t_build = time.time()
+    model = mgx.SyntheticModel(w["shape"], w["wtype"], seed=w["seed"])
+    c = model.config
+    t5 = mgx.synth_memory(w["seed"], w["n_ctx"])
+    prompt = mgx.synth_codes(w["seed"], c.n_q, w["prompt"], c.card)
+    gm = mgx.Model(c, model.tensors)
+    print(f"[bench] {args.workload}: {model.nbytes() / 1e9:.2f} GB of weights built and uploaded in "
+          f"{time.time() - t_build:.1f} s", file=sys.stderr, flush=True)
+    T = w["prompt"] + w["gen"]
+    params = mgx.GenerateParams(T, 1, 1.0, 250, 3.0, w["seed"])
+    S = T + c.n_q
+    start = w["prompt"] + 1
+
+    timed = 0.0
+    timed_steps = 0
+    bytes_total = 0.0
+    gemv = [0.0, 0.0, 0]
+    attn = [0.0, 0.0, 0]
+    warm_left = args.warmup
+    sess = None
+    while timed_steps < args.steps:
+        if sess is None or sess.remaining() == 0:
+            if sess is not None:
+                for k, acc in ((0, gemv), (1, attn)):
+                    ms, by, n = sess.profile_read(k)
+                    acc[0] += ms; acc[1] += by; acc[2] += n
+                sess.close()
+            sess = mgx.Session(gm, t5, prompt, w["prompt"], params)
+            sess.step(1)                                   # prefill, untimed
+            print(f"[bench] session prefilled ({start} tokens)", file=sys.stderr, flush=True)
+        if warm_left > 0:
+            warm_left -= sess.step(min(warm_left, sess.remaining()))
+            continue
+        n = min(args.steps - timed_steps, sess.remaining())
+        pos0 = S - sess.remaining() - 1                    # cache position of the first step
+        sess.profile(args.profile_every)
+        hip_sync()
+        t0 = time.perf_counter()
+        done = sess.step(n)
+        hip_sync()
+        timed += time.perf_counter() - t0
+        sess.profile(0)
+        for i in range(done):
+            bytes_total += step_bytes(c, BPW[w["wtype"]], 2, w["n_ctx"], pos0 + i + 1)
+        timed_steps += done
+        print(f"[bench] timed {timed_steps}/{args.steps} steps, {timed:.2f} s", file=sys.stderr, flush=True)
+    for k, acc in ((0, gemv), (1, attn)):
+        ms, by, nn = sess.profile_read(k)
+        acc[0] += ms; acc[1] += by; acc[2] += nn
+    sess.close()
+
+    fps = timed_steps / timed
+    gemv_gbs = gemv[1] / (gemv[0] * 1e-3) / 1e9 if gemv[0] > 0 else 0.0
+    attn_gbs = attn[1] / (attn[0] * 1e-3) / 1e9 if attn[0] > 0 else 0.0
+    out = {
+        "metric": "LM frames/sec & HBM GB/s, MusicGen-medium Q8_0 CFG=2, 30 s continuation"
+        if args.workload == "medium-q8" else f"LM frames/sec & HBM GB/s, {args.workload}",
+        "value": round(fps, 3),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": timed_steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1000.0 * timed / timed_steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {8: "int8xq8_0+f32", 2: "int8xq4_0+f32", 1: "f16+f32", 0: "f32"}[w["wtype"]],
+        "data": "synthetic (seeded random N(0,0.02) weights, N(0,1) memory, uniform prompt codes)",
+        "config": {"workload": w["desc"], "layers": c.layers, "dim": c.dim, "heads": c.heads, "ff_dim": c.ff_dim,
+                   "weights": {8: "Q8_0", 2: "Q4_0", 1: "F16", 0: "F32"}[w["wtype"]], "n_ctx": w["n_ctx"],
+                   "prompt_frames": w["prompt"], "continuation_frames": w["gen"], "cfg_coef": 3.0, "top_k": 250,
+                   "temperature": 1.0, "seed": w["seed"], "parallelism": "single GPU"},
+        "hbm_gbs_step": round(bytes_total / timed / 1e9, 1),
+        "roofline_frac_step": round(bytes_total / timed / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemv (Q8_0 weight GEMV, all projections)", "launches_timed": gemv[2],
+                     "avg_launch_us": round(1000.0 * gemv[0] / max(gemv[2], 1), 3)},
+        "attention": {"achieved": round(attn_gbs, 1), "unit": "GB/s", "launches_timed": attn[2],
+                      "avg_launch_us": round(1000.0 * attn[0] / max(attn[2], 1), 3)},
+    }
+    if not args.no_cpu:
+        try:
+            out["cpu_baseline"] = cpu_baseline(w, model, t5, prompt, args.cpu_seconds)
+        except Exception as e:  # the GPU figure stands without it
+            out["cpu_baseline"] = {"error": str(e)}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -135,6 +135,36 @@ int mgx_generate(mgx_model* model, const float* t5_hidden, int32_t n_ctx, int32_
                  int32_t* codes_out, float* first_logits_out, float* step_logits_out,
                  mgx_generate_report* report);
 
+/* mg_generate in resumable pieces, for callers that report progress after every step as
+   the reference's ProgressFn does (pipeline.cpp:301) or time a subset of the steps.
+   mgx_session_create builds the delay-pattern sequence, the pre-drawn uniform stream and a
+   stream, and runs nothing. mgx_session_step runs up to n_forwards more loop iterations --
+   the first is the prefill of the prompt, the rest single-token decodes -- each ending with
+   the on-device CFG mix, sampling and sequence write, then waits for them; *done gets the
+   count. mgx_session_finish reads the codes back (reverted, pipeline.cpp:307-313; the
+   final check only once every step has run), the first logits, the per-step logits when
+   keep_step_logits was set, and the report. */
+typedef struct mgx_session mgx_session;
+int mgx_session_create(mgx_model* model, const float* t5_hidden, int32_t n_ctx, int32_t description_empty,
+                       const int32_t* prompt_codes, int32_t prompt_len, const mgx_generate_params* params,
+                       int32_t keep_step_logits, mgx_session** out);
+int mgx_session_step(mgx_session* session, int32_t n_forwards, int32_t* done);
+int32_t mgx_session_remaining(const mgx_session* session);
+int mgx_session_finish(mgx_session* session, int32_t* codes_out, float* first_logits_out, float* step_logits_out,
+                       mgx_generate_report* report);
+void mgx_session_destroy(mgx_session* session);
+
+/* Launch timing (no reference counterpart; the reference has wall clocks only,
+   pipeline.cpp:15-18): with every > 0, each GEMV (kind 0) and self-attention (kind 1) launch
+   of every `every`-th loop iteration is bracketed by HIP events on the session's stream.
+   profile_read sums the elapsed milliseconds, the algorithmic bytes (weights at their
+   stored precision; f32 K and V of the keys attended) and the launch count. */
+int mgx_session_profile(mgx_session* session, int32_t every);
+int mgx_session_profile_read(mgx_session* session, int32_t kind, double* ms_total, double* bytes_total,
+                             int32_t* launches);
+/* The hipStream_t the session's kernels run on. */
+void* mgx_session_hip_stream(mgx_session* session);
+
 /* The message of the last failed call on this thread. */
 const char* mgx_last_error(void);
 

@@ -280,6 +280,23 @@ static inline void transpose8(__m256* r) {
 }
 #endif
 
+/* Exact integer dot of 32 int8 pairs (the order of integer adds does not matter). */
+static inline int idot32(const int8_t* w, const int8_t* x) {
+#ifdef __AVX2__
+    const __m256i wv = _mm256_loadu_si256((const __m256i*)w), xv = _mm256_loadu_si256((const __m256i*)x);
+    const __m256i p16 = _mm256_maddubs_epi16(_mm256_sign_epi8(wv, wv), _mm256_sign_epi8(xv, wv));
+    const __m256i p32 = _mm256_madd_epi16(p16, _mm256_set1_epi16(1));
+    __m128i s = _mm_add_epi32(_mm256_castsi256_si128(p32), _mm256_extracti128_si256(p32, 1));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0x4e));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0xb1));
+    return _mm_cvtsi128_si32(s);
+#else
+    int isum = 0;
+    for (int j = 0; j < 32; ++j) isum += (int)w[j] * (int)x[j];
+    return isum;
+#endif
+}
+
 static float dot_row(const mat_t* W, int r, const act_t* a, int c) {
     const uint8_t* row = W->data + (size_t)r * W->row_bytes;
     const int in = W->in;
@@ -291,9 +308,7 @@ static float dot_row(const mat_t* W, int r, const act_t* a, int c) {
         for (int b = 0; b < in / 32; ++b) {
             const uint8_t* blk = row + (size_t)b * 34;
             const int8_t* qw = (const int8_t*)(blk + 2);
-            const int8_t* qx = xq + b * 32;
-            int isum = 0;
-            for (int j = 0; j < 32; ++j) isum += (int)qw[j] * (int)qx[j];
+            const int isum = idot32(qw, xq + b * 32);
             const float term = (float)isum * (f16at(blk) * xd[b]);
             part[b & 63] = part[b & 63] + term;
         }
@@ -303,12 +318,9 @@ static float dot_row(const mat_t* W, int r, const act_t* a, int c) {
         for (int b = 0; b < in / 32; ++b) {
             const uint8_t* blk = row + (size_t)b * 18;
             const uint8_t* qs = blk + 2;
-            const int8_t* qx = xq + b * 32;
-            int isum = 0;
-            for (int j = 0; j < 16; ++j) {
-                isum += ((int)(qs[j] & 15) - 8) * (int)qx[j];
-                isum += ((int)(qs[j] >> 4) - 8) * (int)qx[j + 16];
-            }
+            int8_t wq[32];
+            for (int j = 0; j < 16; ++j) { wq[j] = (int8_t)((qs[j] & 15) - 8); wq[j + 16] = (int8_t)((qs[j] >> 4) - 8); }
+            const int isum = idot32(wq, xq + b * 32);
             const float term = (float)isum * (f16at(blk) * xd[b]);
             part[b & 63] = part[b & 63] + term;
         }
