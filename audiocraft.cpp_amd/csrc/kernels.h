@@ -7,9 +7,14 @@ namespace mgx {
 
 enum { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8 };
 enum { ACT_Q8 = 0, ACT_F16 = 1, ACT_F32 = 2 };
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_GELU = 2, EPI_QKV = 3 };
+// GEMV prologues: LayerNorm of f32 columns, plain conversion of f32 columns, or a copy of
+// columns already in activation form -- all into LDS, while the weight loads are in flight.
+enum { PRO_LN = 0, PRO_F32 = 1, PRO_ACT = 2 };
+// GEMV epilogues: store, residual add, q + KV-cache append, GELU then activation form.
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GELU_ACT = 3 };
 
 constexpr int ATT_CHUNK = 256;   // keys per attention chunk (fixes the reduction order)
+constexpr int ATT_MAX_CHUNKS = 16;  // capacity up to 4096 positions
 constexpr int MAX_CARD = 2048;   // sampler's LDS rows
 
 // A weight matrix in device layout: `out` rows of `in`. Q8_0: int8 q[out][in] + fp16
@@ -33,61 +38,53 @@ struct ActBuf {
 struct EmbedArgs {
     DevMat emb[8];
     int n_q;
-    const int32_t* ids;
-    int ids_stride;    // ids of codebook q at ids[q * ids_stride]
-    const float* pos;  // [capacity][dim]
-    int position;
+    const int32_t* ids;   // codebook q's token for position p at ids[q * ids_stride + p - ids_base]
+    int ids_stride, ids_base;
+    const float* table;   // sinusoid [capacity][dim]
+    const int* pos;       // device position of this step
     int dim;
-    float* x;          // [ncol][dim]
+    float* x;             // [ncol][dim]
     int ncol;
-};
-
-struct LnArgs {
-    const float* x;
-    int x_stride, dim;
-    const float *w, *b;
-    float eps;
-    ActBuf out;
-};
-
-struct ActArgs {
-    const float* x;
-    int x_stride, n;
-    ActBuf out;
-};
-
-struct GemvOut {
-    int mode;
-    float* y;        // STORE / GELU: y[col][y_stride]; RESID: y += ; QKV: q [col][dim]
-    int y_stride;
-    float *k, *v;    // QKV: caches [col][heads][cap][64]
-    int dim, heads, cap, position;
 };
 
 struct GemvArgs {
     DevMat w;
-    ActBuf act;
     int ncol;
-    GemvOut o;
+    int pro;
+    const float* x;       // PRO_LN / PRO_F32 source [col][x_stride]
+    int x_stride;
+    const float *ln_w, *ln_b;
+    float eps;
+    ActBuf src;           // PRO_ACT source
+    int epi;
+    float* y;             // STORE / RESID: [col][y_stride]; QKV: q [col][dim]
+    int y_stride;
+    float *k, *v;         // QKV: caches [col][heads][cap][64]
+    int dim, heads, cap;
+    const int* pos;       // QKV: device position
+    ActBuf dst;           // GELU_ACT destination
 };
 
 struct AttnArgs {
-    const float* q;   // [col][dim]
-    const float* k;   // [col][heads][cap][64]
-    const float* v;   // [col][heads][cap][64]
-    float* scores;    // [col][heads][cap]
-    float* opart;     // [col][heads][max_chunks][64]
-    int dim, heads, cap, position, max_chunks, ncol;
+    const float* q;       // [col][dim]
+    const float* k;       // [col][heads][cap][64]
+    const float* v;       // [col][heads][cap][64]
+    float* scores;        // [col][heads][cap]
+    float* opart;         // [col][heads][max_chunks][64]
+    float* cmax;          // [col][heads][max_chunks]
+    int dim, heads, cap, max_chunks, ncol;
     float scale;
+    const int* pos;       // device position: keys [0, pos]
+    ActBuf out;           // the out-projection's activation
 };
 
 struct XAttnArgs {
     const float* q;   // [dim]
     const float* k;   // [heads][n_ctx][64]
     const float* v;
-    float* o;         // [dim]
     int n_ctx;
     float scale;
+    ActBuf out;       // column 0 of cross.out's activation
 };
 
 struct SampleArgs {
@@ -95,26 +92,26 @@ struct SampleArgs {
     int n_q, card, guided;
     float cfg_coef;
     const uint8_t* mask;     // [n_q][steps]
-    int steps, offset;
+    int steps, start;
+    const int* pos;          // the loop offset is *pos + 1
     int use_sampling;
     float temperature;
     int top_k;
     const float* uniforms;   // [steps][n_q]
     int special;
     int32_t* seq;            // [n_q][steps]
-    float* first_logits;     // [n_q][card] or null
-    float* step_logits;      // [n_q][card] or null
+    float* first_logits;     // [n_q][card], written at offset == start
+    float* step_logits;      // [steps - start][n_q][card] or null
 };
 
 void launch_embed(const EmbedArgs& a, hipStream_t s);
-void launch_ln_act(const LnArgs& a, int ncol, hipStream_t s);
-void launch_act(const ActArgs& a, int ncol, hipStream_t s);
-void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s);
 void launch_gemv(const GemvArgs& a, hipStream_t s);
-void launch_attention(const AttnArgs& a, const ActBuf& out, hipStream_t s);
+void launch_attention(const AttnArgs& a, hipStream_t s);
 void launch_xattn(const XAttnArgs& a, int heads, hipStream_t s);
+void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s);
 void launch_xkv_split(const float* kv, int n_ctx, int dim, float* k, float* v, hipStream_t s);
 void launch_sample(const SampleArgs& a, hipStream_t s);
+void launch_advance(int* pos, hipStream_t s);
 void launch_repack(int type, const uint8_t* raw, int64_t rows, int in, void* q, uint16_t* d, hipStream_t s);
 
 }  // namespace mgx

@@ -31,12 +31,6 @@ namespace mgx {
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
 
-__device__ __constant__ double RECIP_FACT[14] = {
-    1.0, 1.0, 0.5, 0.16666666666666666, 0.041666666666666664, 0.008333333333333333,
-    0.001388888888888889, 0.0001984126984126984, 2.48015873015873e-05,
-    2.7557319223985893e-06, 2.755731922398589e-07, 2.505210838544172e-08,
-    2.08767569878681e-09, 1.6059043836821613e-10};
-
 // e^x: x = k ln2 + r with ln2 split in two doubles, e^r by its Taylor series to r^13.
 __device__ double dexp(double x) {
     if (x != x) return x;
@@ -158,52 +152,18 @@ __device__ __forceinline__ float mat_elem(const DevMat& m, int r, int i) {
 __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= a.dim) return;
+    const int p = *a.pos;
     float e = 0.0f;
     for (int q = 0; q < a.n_q; ++q) {
-        const int id = a.ids[(size_t)q * a.ids_stride];
+        const int id = a.ids[(size_t)q * a.ids_stride + (p - a.ids_base)];
         const float v = mat_elem(a.emb[q], id, i);
         e = q == 0 ? v : e + v;
     }
-    const float x = a.pos[(size_t)a.position * a.dim + i] + e;
+    const float x = a.table[(size_t)p * a.dim + i] + e;
     for (int n = 0; n < a.ncol; ++n) a.x[(size_t)n * a.dim + i] = x;
 }
 
-// ------------------------------------------------------------------------------------
-// LayerNorm of one column per wave, then conversion to the activation form
-// (transformer.h:28-38; the ggml_norm arithmetic is spelled out in the file header)
-// ------------------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void k_ln_act(LnArgs a) {
-    const int col = blockIdx.x, lane = threadIdx.x;
-    const float* x = a.x + (size_t)col * a.x_stride;
-    const int n = a.dim;
-    double s = 0.0;
-    for (int i = lane; i < n; i += 64) s = s + (double)x[i];
-    s = fold64d(s);
-    const float mean = (float)(s / (double)n);
-    double s2 = 0.0;
-    for (int i = lane; i < n; i += 64) {
-        const float v = x[i] - mean;
-        s2 = s2 + (double)(v * v);
-    }
-    s2 = fold64d(s2);
-    const float var = (float)(s2 / (double)n);
-    const float scale = 1.0f / __builtin_sqrtf(var + a.eps);
-    for (int i = lane; i < n; i += 64) {
-        float v = x[i] - mean;
-        v = v * scale;
-        v = v * a.w[i];
-        v = v + a.b[i];
-        put_act(a.out, col, i, v, lane);
-    }
-}
-
-// f32 columns -> activation form (the GELU output before ff.2).
-__global__ __launch_bounds__(256) void k_act(ActArgs a) {
-    const int col = blockIdx.y;
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= a.n) return;
-    put_act(a.out, col, i, a.x[(size_t)col * a.x_stride + i], threadIdx.x & 63);
-}
+__global__ void k_advance(int* pos) { *pos = *pos + 1; }
 
 __global__ __launch_bounds__(256) void k_add_bias(float* y, const float* b, int n, int ncol) {
     const int i = blockIdx.x * 256 + threadIdx.x;
@@ -212,258 +172,488 @@ __global__ __launch_bounds__(256) void k_add_bias(float* y, const float* b, int 
 }
 
 // ------------------------------------------------------------------------------------
-// GEMV: y[col][r] = W[r] . act[col], one wave per row, lane l owns blocks l, l+64, ...
+// GEMV: y[col][r] = W[r] . act[col]. A wave owns R consecutive rows; lane l owns the row's
+// units l, l+64, ... (a unit is a 32-element block for Q8_0 / Q4_0, 8 elements for F16 /
+// F32). The first pass of weights is requested before the prologue builds the activation
+// columns in LDS, so HBM latency hides behind the LayerNorm / quantization work.
 // ------------------------------------------------------------------------------------
-template <int NC>
-__device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int r, const float* acc, int ncol) {
-    const GemvOut& o = a.o;
-    for (int n = 0; n < ncol && n < NC; ++n) {
-        const float v = acc[n];
-        switch (o.mode) {
-        case EPI_STORE: o.y[(size_t)n * o.y_stride + r] = v; break;
-        case EPI_RESID: { float* p = o.y + (size_t)n * o.y_stride + r; *p = *p + v; break; }
-        case EPI_GELU: o.y[(size_t)n * o.y_stride + r] = gelu_erf(v); break;
-        case EPI_QKV: {
-            const int sec = r / o.dim, w = r - sec * o.dim, head = w >> 6, dim = w & 63;
-            if (sec == 0) o.y[(size_t)n * o.dim + w] = v;
-            else {
-                float* cache = sec == 1 ? o.k : o.v;
-                cache[(((size_t)n * o.heads + head) * o.cap + o.position) * 64 + dim] = v;
-            }
-            break;
-        }
-        }
-    }
-}
+struct LdsAct {
+    int8_t* q;     // Q8 [col][in]
+    float* d;      // Q8 [col][in/32]
+    uint16_t* h;   // F16 [col][in]
+    float* f;      // F32 [col][in]
+    int in;
+};
 
-template <int NC>
-__global__ __launch_bounds__(256) void k_gemv_q8(GemvArgs a) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r = blockIdx.x * 4 + wave;
-    if (r >= a.w.out) return;
-    const int in = a.w.in, nb = in / 32;
-    const int8_t* wq = (const int8_t*)a.w.q + (size_t)r * in;
-    const uint16_t* wd = a.w.d + (size_t)r * nb;
-    float part[NC];
-#pragma unroll
-    for (int n = 0; n < NC; ++n) part[n] = 0.0f;
-    for (int b = lane; b < nb; b += 64) {
-        const int4 w0 = *(const int4*)(wq + b * 32), w1 = *(const int4*)(wq + b * 32 + 16);
-        const float dw = h2f(wd[b]);
-#pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            if (n >= a.ncol) break;
-            const int8_t* xq = a.act.q + (size_t)n * a.act.stride + b * 32;
-            const int4 x0 = *(const int4*)xq, x1 = *(const int4*)(xq + 16);
-            int s = __builtin_amdgcn_sdot4(w0.x, x0.x, 0, false);
-            s = __builtin_amdgcn_sdot4(w0.y, x0.y, s, false);
-            s = __builtin_amdgcn_sdot4(w0.z, x0.z, s, false);
-            s = __builtin_amdgcn_sdot4(w0.w, x0.w, s, false);
-            s = __builtin_amdgcn_sdot4(w1.x, x1.x, s, false);
-            s = __builtin_amdgcn_sdot4(w1.y, x1.y, s, false);
-            s = __builtin_amdgcn_sdot4(w1.z, x1.z, s, false);
-            s = __builtin_amdgcn_sdot4(w1.w, x1.w, s, false);
-            const float dd = dw * a.act.d[(size_t)n * (a.act.stride / 32) + b];
-            const float term = (float)s * dd;
-            part[n] = part[n] + term;
-        }
+template <int WT> struct WUnit;
+template <> struct WUnit<T_Q8_0> {
+    int4 a, b;
+    uint16_t d;
+    __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
+        const int8_t* p = (const int8_t*)m.q + (size_t)r * m.in + u * 32;
+        a = *(const int4*)p; b = *(const int4*)(p + 16);
+        d = m.d[(size_t)r * (m.in / 32) + u];
     }
-#pragma unroll
-    for (int n = 0; n < NC; ++n) part[n] = fold64(part[n]);
-    if (lane == 0) gemv_epilogue<NC>(a, r, part, a.ncol);
-}
+    __device__ __forceinline__ float dot(const LdsAct& x, int n, int u, float p) const {
+        const int8_t* xq = x.q + (size_t)n * x.in + u * 32;
+        const int4 x0 = *(const int4*)xq, x1 = *(const int4*)(xq + 16);
+        int s = __builtin_amdgcn_sdot4(a.x, x0.x, 0, false);
+        s = __builtin_amdgcn_sdot4(a.y, x0.y, s, false);
+        s = __builtin_amdgcn_sdot4(a.z, x0.z, s, false);
+        s = __builtin_amdgcn_sdot4(a.w, x0.w, s, false);
+        s = __builtin_amdgcn_sdot4(b.x, x1.x, s, false);
+        s = __builtin_amdgcn_sdot4(b.y, x1.y, s, false);
+        s = __builtin_amdgcn_sdot4(b.z, x1.z, s, false);
+        s = __builtin_amdgcn_sdot4(b.w, x1.w, s, false);
+        const float dd = h2f(d) * x.d[(size_t)n * (x.in / 32) + u];
+        const float term = (float)s * dd;
+        return p + term;
+    }
+};
 
 // Q4_0: sum((nib-8)*x) = sum(nib*x) - 8*sum(x), both exact integer dots.
-__device__ __forceinline__ int q4_isum(const int4 w, const int4 x0, const int4 x1) {
-    const uint32_t ws[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
-    const int xl[4] = {x0.x, x0.y, x0.z, x0.w}, xh[4] = {x1.x, x1.y, x1.z, x1.w};
-    int s = 0, sx = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        s = __builtin_amdgcn_sdot4((int)(ws[k] & 0x0f0f0f0fu), xl[k], s, false);
-        s = __builtin_amdgcn_sdot4((int)((ws[k] >> 4) & 0x0f0f0f0fu), xh[k], s, false);
-        sx = __builtin_amdgcn_sdot4(0x01010101, xl[k], sx, false);
-        sx = __builtin_amdgcn_sdot4(0x01010101, xh[k], sx, false);
+template <> struct WUnit<T_Q4_0> {
+    int4 a;
+    uint16_t d;
+    __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
+        a = *(const int4*)((const uint8_t*)m.q + (size_t)r * (m.in / 2) + u * 16);
+        d = m.d[(size_t)r * (m.in / 32) + u];
     }
-    return s - 8 * sx;
+    __device__ __forceinline__ float dot(const LdsAct& x, int n, int u, float p) const {
+        const int8_t* xq = x.q + (size_t)n * x.in + u * 32;
+        const int4 x0 = *(const int4*)xq, x1 = *(const int4*)(xq + 16);
+        const uint32_t ws[4] = {(uint32_t)a.x, (uint32_t)a.y, (uint32_t)a.z, (uint32_t)a.w};
+        const int xl[4] = {x0.x, x0.y, x0.z, x0.w}, xh[4] = {x1.x, x1.y, x1.z, x1.w};
+        int s = 0, sx = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            s = __builtin_amdgcn_sdot4((int)(ws[k] & 0x0f0f0f0fu), xl[k], s, false);
+            s = __builtin_amdgcn_sdot4((int)((ws[k] >> 4) & 0x0f0f0f0fu), xh[k], s, false);
+            sx = __builtin_amdgcn_sdot4(0x01010101, xl[k], sx, false);
+            sx = __builtin_amdgcn_sdot4(0x01010101, xh[k], sx, false);
+        }
+        const int isum = s - 8 * sx;
+        const float dd = h2f(d) * x.d[(size_t)n * (x.in / 32) + u];
+        const float term = (float)isum * dd;
+        return p + term;
+    }
+};
+
+// F16 weights x fp16-rounded activations: products exact in f32, fmaf in element order.
+template <> struct WUnit<T_F16> {
+    int4 a;
+    __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
+        a = *(const int4*)((const uint16_t*)m.q + (size_t)r * m.in + u * 8);
+    }
+    __device__ __forceinline__ float dot(const LdsAct& x, int n, int u, float p) const {
+        const int4 xv = *(const int4*)(x.h + (size_t)n * x.in + u * 8);
+        const uint32_t w32[4] = {(uint32_t)a.x, (uint32_t)a.y, (uint32_t)a.z, (uint32_t)a.w};
+        const uint32_t x32[4] = {(uint32_t)xv.x, (uint32_t)xv.y, (uint32_t)xv.z, (uint32_t)xv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            p = __builtin_fmaf(h2f((uint16_t)(w32[e] & 0xffffu)), h2f((uint16_t)(x32[e] & 0xffffu)), p);
+            p = __builtin_fmaf(h2f((uint16_t)(w32[e] >> 16)), h2f((uint16_t)(x32[e] >> 16)), p);
+        }
+        return p;
+    }
+};
+
+template <> struct WUnit<T_F32> {
+    float4 a, b;
+    __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
+        const float* p = (const float*)m.q + (size_t)r * m.in + u * 8;
+        a = *(const float4*)p; b = *(const float4*)(p + 4);
+    }
+    __device__ __forceinline__ float dot(const LdsAct& x, int n, int u, float p) const {
+        const float* xf = x.f + (size_t)n * x.in + u * 8;
+        const float4 x0 = *(const float4*)xf, x1 = *(const float4*)(xf + 4);
+        p = __builtin_fmaf(a.x, x0.x, p); p = __builtin_fmaf(a.y, x0.y, p);
+        p = __builtin_fmaf(a.z, x0.z, p); p = __builtin_fmaf(a.w, x0.w, p);
+        p = __builtin_fmaf(b.x, x1.x, p); p = __builtin_fmaf(b.y, x1.y, p);
+        p = __builtin_fmaf(b.z, x1.z, p); p = __builtin_fmaf(b.w, x1.w, p);
+        return p;
+    }
+};
+
+// LayerNorm / conversion prologue: the activation columns of one launch are built in LDS by
+// every block (cheap, and it saves a launch and a round trip through memory). Wave n owns
+// column n, lane b its 32-element block b. The loads are issued before the weight loads --
+// vector-memory completions are counted in order, so loads issued after the weights would
+// wait for them -- and held in kernel-local registers until the weights are in flight.
+template <int WT>
+__device__ __forceinline__ void pro_load(const GemvArgs& a, int wave, int lane, float4 (&xv)[8], float4 (&wv)[8],
+                                         float4 (&bv)[8]) {
+    if (wave < a.ncol && lane < a.w.in / 32) {
+        const float4* xs = (const float4*)(a.x + (size_t)wave * a.x_stride + lane * 32);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) xv[k] = xs[k];
+        if (a.pro == PRO_LN) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                wv[k] = ((const float4*)(a.ln_w + lane * 32))[k];
+                bv[k] = ((const float4*)(a.ln_b + lane * 32))[k];
+            }
+        }
+    }
 }
 
-template <int NC>
-__global__ __launch_bounds__(256) void k_gemv_q4(GemvArgs a) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r = blockIdx.x * 4 + wave;
-    if (r >= a.w.out) return;
+template <int WT>
+__device__ __forceinline__ void pro_store(const GemvArgs& a, const LdsAct& x, int wave, int lane, const float4 (&xv)[8],
+                                          const float4 (&wv)[8], const float4 (&bv)[8]) {
+    if (wave >= a.ncol) return;
     const int in = a.w.in, nb = in / 32;
-    const uint8_t* wq = (const uint8_t*)a.w.q + (size_t)r * (in / 2);
-    const uint16_t* wd = a.w.d + (size_t)r * nb;
-    float part[NC];
+    const bool mine = lane < nb;
+    float v[32];
 #pragma unroll
-    for (int n = 0; n < NC; ++n) part[n] = 0.0f;
-    for (int b = lane; b < nb; b += 64) {
-        const int4 w = *(const int4*)(wq + b * 16);
-        const float dw = h2f(wd[b]);
+    for (int k = 0; k < 8; ++k) {
+        v[4 * k] = xv[k].x; v[4 * k + 1] = xv[k].y; v[4 * k + 2] = xv[k].z; v[4 * k + 3] = xv[k].w;
+    }
+    if (a.pro == PRO_LN) {
+        // LayerNorm (transformer.h:28-38): block b's elements summed in order (double) by
+        // lane b, lanes folded by the butterfly.
+        double s = 0.0;
+        if (mine) {
 #pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            if (n >= a.ncol) break;
-            const int8_t* xq = a.act.q + (size_t)n * a.act.stride + b * 32;
-            const int s = q4_isum(w, *(const int4*)xq, *(const int4*)(xq + 16));
-            const float dd = dw * a.act.d[(size_t)n * (a.act.stride / 32) + b];
-            const float term = (float)s * dd;
-            part[n] = part[n] + term;
+            for (int j = 0; j < 32; ++j) s = s + (double)v[j];
+        }
+        s = fold64d(s);
+        const float mean = (float)(s / (double)in);
+        double s2 = 0.0;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            v[j] = v[j] - mean;
+            if (mine) s2 = s2 + (double)(v[j] * v[j]);
+        }
+        s2 = fold64d(s2);
+        const float var = (float)(s2 / (double)in);
+        const float scale = 1.0f / __builtin_sqrtf(var + a.eps);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float w4[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
+            const float b4[4] = {bv[k].x, bv[k].y, bv[k].z, bv[k].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float t = v[4 * k + e] * scale;
+                t = t * w4[e];
+                v[4 * k + e] = t + b4[e];
+            }
         }
     }
+    if (!mine) return;
+    const int n = wave, i0 = lane * 32;
+    if (WT == T_Q8_0 || WT == T_Q4_0) {
+        float amax = 0.0f;
 #pragma unroll
-    for (int n = 0; n < NC; ++n) part[n] = fold64(part[n]);
-    if (lane == 0) gemv_epilogue<NC>(a, r, part, a.ncol);
+        for (int j = 0; j < 32; ++j) { const float t = __builtin_fabsf(v[j]); amax = amax > t ? amax : t; }
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        int32_t packed[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                word |= (uint32_t)(uint8_t)(int8_t)__builtin_roundf(v[4 * k + e] * id) << (8 * e);
+            packed[k] = (int32_t)word;
+        }
+        int4* dst = (int4*)(x.q + (size_t)n * in + i0);
+        dst[0] = make_int4(packed[0], packed[1], packed[2], packed[3]);
+        dst[1] = make_int4(packed[4], packed[5], packed[6], packed[7]);
+        x.d[(size_t)n * nb + lane] = h2f(f2h(d));
+    } else if (WT == T_F16) {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) x.h[(size_t)n * in + i0 + j] = f2h(v[j]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) x.f[(size_t)n * in + i0 + j] = v[j];
+    }
 }
 
-// F16 weights x fp16-rounded activations (products exact in f32), 8-element chunks.
-template <int NC>
-__global__ __launch_bounds__(256) void k_gemv_f16(GemvArgs a) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r = blockIdx.x * 4 + wave;
-    if (r >= a.w.out) return;
-    const int in = a.w.in, nch = in / 8;
-    const uint16_t* w = (const uint16_t*)a.w.q + (size_t)r * in;
-    float part[NC];
-#pragma unroll
-    for (int n = 0; n < NC; ++n) part[n] = 0.0f;
-    for (int c = lane; c < nch; c += 64) {
-        const int4 wv = *(const int4*)(w + c * 8);
-        const uint16_t* wh = (const uint16_t*)&wv;
-#pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            if (n >= a.ncol) break;
-            const int4 xv = *(const int4*)(a.act.h + (size_t)n * a.act.stride + c * 8);
-            const uint16_t* xh = (const uint16_t*)&xv;
-            float p = part[n];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) p = __builtin_fmaf(h2f(wh[e]), h2f(xh[e]), p);
-            part[n] = p;
-        }
-    }
-#pragma unroll
-    for (int n = 0; n < NC; ++n) part[n] = fold64(part[n]);
-    if (lane == 0) gemv_epilogue<NC>(a, r, part, a.ncol);
+template <int WT>
+__host__ __device__ constexpr int unit_elems() { return (WT == T_Q8_0 || WT == T_Q4_0) ? 32 : 8; }
+
+__host__ __device__ inline size_t lds_act_bytes(int wt, int ncol, int in) {
+    if (wt == T_Q8_0 || wt == T_Q4_0) return (size_t)ncol * in + (size_t)ncol * (in / 32) * 4;
+    if (wt == T_F16) return (size_t)ncol * in * 2;
+    return (size_t)ncol * in * 4;
 }
 
-template <int NC>
-__global__ __launch_bounds__(256) void k_gemv_f32(GemvArgs a) {
+// LNP: the prologue builds the activation in LDS (PRO_LN / PRO_F32); otherwise (PRO_ACT)
+// every lane reads its units' activation straight from global memory next to its weights.
+template <int WT, int NC, int R, bool LNP>
+__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r = blockIdx.x * 4 + wave;
-    if (r >= a.w.out) return;
-    const int in = a.w.in, nch = in / 8;
-    const float* w = (const float*)a.w.q + (size_t)r * in;
-    float part[NC];
+    const int in = a.w.in, out = a.w.out;
+    const int units = in / unit_elems<WT>();
+    const int row0 = (blockIdx.x * 4 + wave) * R;
+    LdsAct x;
+    if (LNP) {
+        x.in = in;
+        x.q = (int8_t*)lds;
+        x.d = (float*)(lds + (size_t)NC * in);
+        x.h = (uint16_t*)lds;
+        x.f = (float*)lds;
+    } else {
+        x.in = a.src.stride;
+        x.q = a.src.q; x.d = a.src.d; x.h = a.src.h; x.f = a.src.f;
+    }
+    float* tile = (float*)(lds + (LNP ? lds_act_bytes(WT, NC, in) : 0));   // GELU_ACT staging [NC][4*R]
+
+    float4 xv[8], wv[8], bv[8];
+    if (LNP) pro_load<WT>(a, wave, lane, xv, wv, bv);
+    WUnit<WT> cur[R];
+    if (lane < units) {
 #pragma unroll
-    for (int n = 0; n < NC; ++n) part[n] = 0.0f;
-    for (int c = lane; c < nch; c += 64) {
-        const float4 w0 = *(const float4*)(w + c * 8), w1 = *(const float4*)(w + c * 8 + 4);
-        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        for (int r = 0; r < R; ++r)
+            if (row0 + r < out) cur[r].load(a.w, row0 + r, lane);
+    }
+    if (LNP) {
+        pro_store<WT>(a, x, wave, lane, xv, wv, bv);
+        __syncthreads();
+    }
+
+    float part[R][NC];
 #pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            if (n >= a.ncol) break;
-            const float* x = a.act.f + (size_t)n * a.act.stride + c * 8;
-            float p = part[n];
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) p = __builtin_fmaf(wv[e], x[e], p);
-            part[n] = p;
+        for (int n = 0; n < NC; ++n) part[r][n] = 0.0f;
+    if (row0 < out) {
+        for (int u = lane; u < units; u += 64) {
+            WUnit<WT> nxt[R];
+            const bool more = u + 64 < units;
+            if (more) {
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    if (row0 + r < out) nxt[r].load(a.w, row0 + r, u + 64);
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int n = 0; n < NC; ++n)
+                    if (n < a.ncol) part[r][n] = cur[r].dot(x, n, u, part[r][n]);
+            if (more) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) cur[r] = nxt[r];
+            }
         }
     }
 #pragma unroll
-    for (int n = 0; n < NC; ++n) part[n] = fold64(part[n]);
-    if (lane == 0) gemv_epilogue<NC>(a, r, part, a.ncol);
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int n = 0; n < NC; ++n) part[r][n] = fold64(part[r][n]);
+
+    if (a.epi == EPI_GELU_ACT) {
+        // rows [blockIdx.x*4R, +4R) -> GELU -> LDS tile -> activation form (32-row blocks)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int n = 0; n < NC; ++n)
+                if (lane == r * NC + n && n < a.ncol) tile[n * 4 * R + wave * R + r] = gelu_erf(part[r][n]);
+        __syncthreads();
+        const int rows = 4 * R, base = blockIdx.x * rows;
+        for (int n = 0; n < a.ncol; ++n)
+            for (int i0 = 0; i0 < rows; i0 += 256) {
+                const int i = i0 + threadIdx.x;
+                const float v = i < rows ? tile[n * rows + i] : 0.0f;
+                const int ln = threadIdx.x & 63;
+                if (i0 + (threadIdx.x & ~63) < rows) {
+                    const ActBuf& d = a.dst;
+                    if (d.kind == ACT_Q8) {
+                        int8_t qv;
+                        float dv;
+                        quant_q8_lane(v, ln, &qv, &dv);
+                        if (i < rows) {
+                            d.q[(size_t)n * d.stride + base + i] = qv;
+                            if ((ln & 31) == 0) d.d[(size_t)n * (d.stride / 32) + (base + i) / 32] = dv;
+                        }
+                    } else if (i < rows) {
+                        if (d.kind == ACT_F16) d.h[(size_t)n * d.stride + base + i] = f2h(v);
+                        else d.f[(size_t)n * d.stride + base + i] = v;
+                    }
+                }
+            }
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = row0 + r;
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            if (lane != r * NC + n || n >= a.ncol || row >= out) continue;
+            const float v = part[r][n];
+            if (a.epi == EPI_STORE) a.y[(size_t)n * a.y_stride + row] = v;
+            else if (a.epi == EPI_RESID) {
+                float* p = a.y + (size_t)n * a.y_stride + row;
+                *p = *p + v;
+            } else {
+                const int sec = row / a.dim, w = row - sec * a.dim, head = w >> 6, dim = w & 63;
+                if (sec == 0) a.y[(size_t)n * a.dim + w] = v;
+                else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + *a.pos) * 64 + dim] = v;
+            }
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------
-// decode self-attention over keys [0, position] (nn.h:186-191, no mask for one query)
+// decode self-attention over keys [0, pos] (nn.h:186-191, no mask for one query)
 // ------------------------------------------------------------------------------------
-// Scores of one 256-key chunk: 16 lanes per key, each lane four dims.
+// Sum over the 16 lanes of a lane group of 16 values per lane, by recursive halving: after
+// the four levels lane t holds the sum of value t. Each value's additions follow the
+// butterfly p[l] + p[l+off], off = 8, 4, 2, 1 (the side that keeps a value adds its partner's).
+__device__ __forceinline__ float halving16(float (&p)[16], int t) {
+    float a[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const bool lo = (t & 8) == 0;
+        const float recv = shfl_xor(lo ? p[i + 8] : p[i], 8);
+        a[i] = (lo ? p[i] : p[i + 8]) + recv;
+    }
+    float b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bool lo = (t & 4) == 0;
+        const float recv = shfl_xor(lo ? a[i + 4] : a[i], 4);
+        b[i] = (lo ? a[i] : a[i + 4]) + recv;
+    }
+    float c[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const bool lo = (t & 2) == 0;
+        const float recv = shfl_xor(lo ? b[i + 2] : b[i], 2);
+        c[i] = (lo ? b[i] : b[i + 2]) + recv;
+    }
+    const bool lo = (t & 1) == 0;
+    const float recv = shfl_xor(lo ? c[1] : c[0], 1);
+    return (lo ? c[0] : c[1]) + recv;
+}
+
+// Scores of one 256-key chunk (16 lanes per key, four dims each) and the chunk's max.
 __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
     const int c = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
-    const int u = a.position + 1;
+    const int u = *a.pos + 1;
     if (c * ATT_CHUNK >= u) return;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, t = lane & 15;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, t = lane & 15;
     const size_t head = (size_t)n * a.heads + h;
     const float* K = a.k + head * a.cap * 64;
-    const float4 q = ((const float4*)(a.q + (size_t)n * a.dim + h * 64))[t];
     float* S = a.scores + head * a.cap;
-    for (int it = 0; it < ATT_CHUNK / 16; ++it) {
-        const int j = c * ATT_CHUNK + it * 16 + wave * 4 + g;
-        float p = 0.0f;
-        if (j < u) {
-            const float4 k = ((const float4*)(K + (size_t)j * 64))[t];
-            p = __builtin_fmaf(q.x, k.x, 0.0f);
-            p = __builtin_fmaf(q.y, k.y, p);
-            p = __builtin_fmaf(q.z, k.z, p);
-            p = __builtin_fmaf(q.w, k.w, p);
-        }
-        p = p + shfl_xor(p, 8);
-        p = p + shfl_xor(p, 4);
-        p = p + shfl_xor(p, 2);
-        p = p + shfl_xor(p, 1);
-        if (t == 0 && j < u) S[j] = p * a.scale;
-    }
-}
-
-// Max and softmax denominator over all keys (redone by every chunk's block, deterministic),
-// then this chunk's share of V^T p.
-__global__ __launch_bounds__(256) void k_attn_softmax_v(AttnArgs a) {
-    const int c = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
-    const int u = a.position + 1;
-    if (c * ATT_CHUNK >= u) return;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const size_t head = (size_t)n * a.heads + h;
-    const float* S = a.scores + head * a.cap;
     __shared__ float red_f[4];
-    __shared__ double red_d[256];
-    __shared__ float pv[ATT_CHUNK];
-    __shared__ float4 vred[16][16];
-    __shared__ float inv_sh;
+    const float4 q = ((const float4*)(a.q + (size_t)n * a.dim + h * 64))[t];
+    float4 kv[16];
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+        const int j = c * ATT_CHUNK + it * 16 + wave * 4 + g;
+        kv[it] = j < u ? ((const float4*)(K + (size_t)j * 64))[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float p[16];
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+        float v = __builtin_fmaf(q.x, kv[it].x, 0.0f);
+        v = __builtin_fmaf(q.y, kv[it].y, v);
+        v = __builtin_fmaf(q.z, kv[it].z, v);
+        p[it] = __builtin_fmaf(q.w, kv[it].w, v);
+    }
+    const int jt = c * ATT_CHUNK + t * 16 + wave * 4 + g;   // lane t now holds key jt
+    const float sc = halving16(p, t) * a.scale;
     float mx = -__builtin_inff();
-    for (int j = tid; j < u; j += 256) { const float s = S[j]; mx = mx > s ? mx : s; }
+    if (jt < u) { S[jt] = sc; mx = sc; }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(mx, off); mx = mx > o ? mx : o; }
     if (lane == 0) red_f[wave] = mx;
     __syncthreads();
-    mx = red_f[0];
-    for (int w = 1; w < 4; ++w) mx = mx > red_f[w] ? mx : red_f[w];
-    const int nch = (u + ATT_CHUNK - 1) / ATT_CHUNK;
-    double total = 0.0;
-    for (int cc = 0; cc < nch; ++cc) {
-        const int j = cc * ATT_CHUNK + tid;
-        red_d[tid] = j < u ? (double)dexpf(S[j] - mx) : 0.0;
-        __syncthreads();
-        if (tid < 128) red_d[tid] = red_d[tid] + red_d[tid + 128];
-        __syncthreads();
-        if (tid < 64) {
-            double v = red_d[tid] + red_d[tid + 64];
-            v = fold64d(v);
-            if (tid == 0) total = total + v;
-        }
-        __syncthreads();
+    if (tid == 0) {
+        float m = red_f[0];
+        for (int w = 1; w < 4; ++w) m = m > red_f[w] ? m : red_f[w];
+        a.cmax[head * a.max_chunks + c] = m;
     }
-    if (tid == 0) inv_sh = (float)(1.0 / total);
+}
+
+// Softmax of one head's scores into probabilities: global max, exps, chunk sums in double
+// (butterfly over each chunk's 256 keys), chunks added in order, p = e * (float)(1/sum).
+__global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
+    const int h = blockIdx.x, n = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int u = *a.pos + 1, nch = (u + ATT_CHUNK - 1) / ATT_CHUNK;
+    const size_t head = (size_t)n * a.heads + h;
+    float* S = a.scores + head * a.cap;
+    __shared__ double red_d[ATT_MAX_CHUNKS][128];
+    __shared__ double csum[ATT_MAX_CHUNKS];
+    __shared__ float inv_sh;
+    float s[ATT_MAX_CHUNKS];
+#pragma unroll
+    for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc) {
+        const int j = cc * ATT_CHUNK + tid;
+        s[cc] = (cc < nch && j < u) ? S[j] : 0.0f;
+    }
+    float M = a.cmax[head * a.max_chunks];
+    for (int cc = 1; cc < nch; ++cc) { const float o = a.cmax[head * a.max_chunks + cc]; M = M > o ? M : o; }
+    float e[ATT_MAX_CHUNKS];
+#pragma unroll
+    for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc) {
+        const int j = cc * ATT_CHUNK + tid;
+        e[cc] = (cc < nch && j < u) ? dexpf(s[cc] - M) : 0.0f;
+    }
+    // every chunk's 256-key butterfly at once: off 128 through LDS, 64..1 in wave 0
+#pragma unroll
+    for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc)
+        if (cc < nch && tid >= 128) red_d[cc][tid - 128] = (double)e[cc];
+    __syncthreads();
+    if (tid < 128) {
+#pragma unroll
+        for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc)
+            if (cc < nch) red_d[cc][tid] = (double)e[cc] + red_d[cc][tid];
+    }
+    __syncthreads();
+    if (tid < 64) {
+        for (int cc = 0; cc < nch; ++cc) {
+            double v = red_d[cc][tid] + red_d[cc][tid + 64];
+            v = fold64d(v);
+            if (tid == 0) csum[cc] = v;
+        }
+        if (tid == 0) {
+            double total = 0.0;
+            for (int cc = 0; cc < nch; ++cc) total = total + csum[cc];
+            inv_sh = (float)(1.0 / total);
+        }
+    }
     __syncthreads();
     const float inv = inv_sh;
-    {
-        const int j = c * ATT_CHUNK + tid;
-        pv[tid] = j < u ? dexpf(S[j] - mx) * inv : 0.0f;
+#pragma unroll
+    for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc) {
+        const int j = cc * ATT_CHUNK + tid;
+        if (cc < nch && j < u) S[j] = e[cc] * inv;
     }
-    __syncthreads();
-    // V pass: partial g = key mod 16 (g = 4*wave + lane/16), lane%16 -> dims 4*(lane%16)..+3.
+}
+
+// This chunk's share of V^T p: partial g = key mod 16 (g = 4*wave + lane/16), lane%16 ->
+// dims 4*(lane%16)..+3, keys in increasing order, then the 16 partials folded.
+__global__ __launch_bounds__(256) void k_attn_v(AttnArgs a) {
+    const int c = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
+    const int u = *a.pos + 1;
+    if (c * ATT_CHUNK >= u) return;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const size_t head = (size_t)n * a.heads + h;
+    const float* P = a.scores + head * a.cap;
+    __shared__ float4 vred[16][16];
     const int g = wave * 4 + (lane >> 4), dq = lane & 15;
     const float* V = a.v + head * a.cap * 64;
+    float4 vv[16];
+    float pp[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+        const int j = c * ATT_CHUNK + g + 16 * m;
+        const bool in = j < u;
+        vv[m] = in ? ((const float4*)(V + (size_t)j * 64))[dq] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        pp[m] = in ? P[j] : 0.0f;
+    }
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int m = 0; m < ATT_CHUNK / 16; ++m) {
-        const int jj = g + 16 * m, j = c * ATT_CHUNK + jj;
-        if (j < u) {
-            const float p = pv[jj];
-            const float4 v = ((const float4*)(V + (size_t)j * 64))[dq];
-            acc.x = __builtin_fmaf(p, v.x, acc.x);
-            acc.y = __builtin_fmaf(p, v.y, acc.y);
-            acc.z = __builtin_fmaf(p, v.z, acc.z);
-            acc.w = __builtin_fmaf(p, v.w, acc.w);
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+        if (c * ATT_CHUNK + g + 16 * m < u) {
+            acc.x = __builtin_fmaf(pp[m], vv[m].x, acc.x);
+            acc.y = __builtin_fmaf(pp[m], vv[m].y, acc.y);
+            acc.z = __builtin_fmaf(pp[m], vv[m].z, acc.z);
+            acc.w = __builtin_fmaf(pp[m], vv[m].w, acc.w);
         }
     }
     vred[g][dq] = acc;
@@ -474,9 +664,8 @@ __global__ __launch_bounds__(256) void k_attn_softmax_v(AttnArgs a) {
     }
     __syncthreads();
     if (g < 4) {
-        const float4 s = vred[g][dq], o = vred[g + 4][dq];
-        float4 r = make_float4(s.x + o.x, s.y + o.y, s.z + o.z, s.w + o.w);
-        // g = lane>>4 in wave 0: off 2 -> lane xor 32, off 1 -> lane xor 16
+        const float4 sv = vred[g][dq], o = vred[g + 4][dq];
+        float4 r = make_float4(sv.x + o.x, sv.y + o.y, sv.z + o.z, sv.w + o.w);
         r.x = r.x + shfl_xor(r.x, 32); r.y = r.y + shfl_xor(r.y, 32);
         r.z = r.z + shfl_xor(r.z, 32); r.w = r.w + shfl_xor(r.w, 32);
         r.x = r.x + shfl_xor(r.x, 16); r.y = r.y + shfl_xor(r.y, 16);
@@ -485,14 +674,20 @@ __global__ __launch_bounds__(256) void k_attn_softmax_v(AttnArgs a) {
     }
 }
 
-// Chunk results added in order, then the head's 64 outputs go to the out-proj activation.
-__global__ __launch_bounds__(64) void k_attn_reduce(AttnArgs a, ActBuf out) {
+// Chunk results added in order; the head's 64 outputs go to the out-projection activation.
+__global__ __launch_bounds__(64) void k_attn_reduce(AttnArgs a) {
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
-    const int u = a.position + 1, nch = (u + ATT_CHUNK - 1) / ATT_CHUNK;
+    const int u = *a.pos + 1, nch = (u + ATT_CHUNK - 1) / ATT_CHUNK;
     const size_t head = (size_t)n * a.heads + h;
+    float part[ATT_MAX_CHUNKS];
+#pragma unroll
+    for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc)
+        part[cc] = cc < nch ? a.opart[(head * a.max_chunks + cc) * 64 + lane] : 0.0f;
     float r = 0.0f;
-    for (int c = 0; c < nch; ++c) r = r + a.opart[(head * a.max_chunks + c) * 64 + lane];
-    put_act(out, n, h * 64 + lane, r, lane);
+#pragma unroll
+    for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc)
+        if (cc < nch) r = r + part[cc];
+    put_act(a.out, n, h * 64 + lane, r, lane);
 }
 
 // ------------------------------------------------------------------------------------
@@ -574,8 +769,10 @@ __global__ __launch_bounds__(256) void k_xattn(XAttnArgs a) {
         r.z = r.z + shfl_xor(r.z, 32); r.w = r.w + shfl_xor(r.w, 32);
         r.x = r.x + shfl_xor(r.x, 16); r.y = r.y + shfl_xor(r.y, 16);
         r.z = r.z + shfl_xor(r.z, 16); r.w = r.w + shfl_xor(r.w, 16);
-        if (gg == 0) ((float4*)a.o)[h * 16 + dq] = make_float4(0.0f + r.x, 0.0f + r.y, 0.0f + r.z, 0.0f + r.w);
+        if (gg == 0) ((float4*)s)[dq] = make_float4(0.0f + r.x, 0.0f + r.y, 0.0f + r.z, 0.0f + r.w);
     }
+    __syncthreads();
+    if (tid < 64) put_act(a.out, 0, h * 64 + tid, s[tid], tid);
 }
 
 // The hoisted cross K/V: projected [n_ctx][2*dim] -> K [H][n_ctx][64], V [H][n_ctx][64].
@@ -591,30 +788,81 @@ __global__ __launch_bounds__(256) void k_xkv_split(const float* kv, int n_ctx, i
 // sampling: CFG mix + argmax / softmax, top-k, categorical (pipeline.cpp:264-294,
 // sampling.h:32-105), one block per codebook
 // ------------------------------------------------------------------------------------
+constexpr int SMP_PER = MAX_CARD / 256;   // elements per thread
+
+// Sequential double sum of n values held in LDS, in index order (one lane; loads batched
+// ahead of the dependent adds).
+__device__ __forceinline__ double seq_sum_d(const double* x, int n) {
+    double t = 0.0;
+    int i = 0;
+    for (; i + 16 <= n; i += 16) {
+        double b[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) b[k] = x[i + k];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) t += b[k];
+    }
+    for (; i < n; ++i) t += x[i];
+    return t;
+}
+__device__ __forceinline__ double seq_sum_f(const float* x, int n) {
+    double t = 0.0;
+    int i = 0;
+    for (; i + 16 <= n; i += 16) {
+        float b[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) b[k] = x[i + k];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) t += (double)b[k];
+    }
+    for (; i < n; ++i) t += (double)x[i];
+    return t;
+}
+
+// Block-wide inclusive scan of one int per thread (256 threads), through LDS.
+__device__ __forceinline__ int block_scan_i(int v, int* tmp) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(v, off, 64);
+        if (lane >= off) v += o;
+    }
+    if (lane == 63) tmp[wave] = v;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += tmp[w];
+    __syncthreads();
+    return v + base;
+}
+
 __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
     const int q = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int C = a.card;
     __shared__ float lg[MAX_CARD];
     __shared__ double ex[MAX_CARD];
     __shared__ float pr[MAX_CARD];
-    __shared__ uint32_t hist[256];
+    __shared__ int hist[256];
+    __shared__ int itmp[8];
     __shared__ float red_f[4];
     __shared__ int red_i[4];
-    __shared__ int tok_sh;
+    __shared__ double red_d[4];
+    __shared__ int tok_sh, pick_sh, exact_sh;
     __shared__ float inv_sh;
     __shared__ uint32_t prefix_sh;
     __shared__ int k_sh;
     const float* cond = a.logits + (size_t)q * C;
     const float* null_l = a.logits + (size_t)(a.n_q + q) * C;
+    const int offset = *a.pos + 1;
+    float* first = offset == a.start ? a.first_logits : nullptr;
+    float* stepl = a.step_logits ? a.step_logits + ((size_t)(offset - a.start) * a.n_q + q) * C : nullptr;
     for (int i = tid; i < C; i += 256) {
         float v = cond[i];
         if (a.guided) v = null_l[i] + (cond[i] - null_l[i]) * a.cfg_coef;
         lg[i] = v;
-        if (a.first_logits) a.first_logits[(size_t)q * C + i] = v;
-        if (a.step_logits) a.step_logits[(size_t)q * C + i] = v;
+        if (first) first[(size_t)q * C + i] = v;
+        if (stepl) stepl[i] = v;
     }
     __syncthreads();
-    const int offset = a.offset;
     const bool live = a.mask[(size_t)q * a.steps + offset] != 0;
     int token;
     if (!live) token = a.special;
@@ -641,7 +889,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
         __syncthreads();
         token = tok_sh;
     } else {
-        // softmax_into: peak, double exps, sequential double total, float scale
+        // softmax_into: peak, double exps, total in index order, float scale
         float pk = -__builtin_inff();
         for (int i = tid; i < C; i += 256) pk = pk < lg[i] ? lg[i] : pk;
 #pragma unroll
@@ -656,67 +904,124 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
             pr[i] = (float)e;
         }
         __syncthreads();
-        if (tid == 0) {
-            double total = 0.0;
-            for (int i = 0; i < C; ++i) total += ex[i];
-            inv_sh = (float)(1.0 / total);
-        }
+        if (tid == 0) inv_sh = (float)(1.0 / seq_sum_d(ex, C));
         __syncthreads();
         for (int i = tid; i < C; i += 256) pr[i] = pr[i] * inv_sh;
         __syncthreads();
-        // top_k_filter: the k-th largest value (counting repeats) by MSB-first radix select
-        // over the bit patterns (non-negative floats order like their bits).
         const int k = a.top_k;
         if (k > 0 && k < C) {
+            // top_k_filter: the k-th largest value counting repeats, by MSB-first radix select
+            // over the bit patterns (non-negative floats order like their bits)
             if (tid == 0) { prefix_sh = 0; k_sh = k; }
             __syncthreads();
             for (int shift = 24; shift >= 0; shift -= 8) {
+                // read before the barriers below; the one writer writes after them
+                const uint32_t pre = prefix_sh;
+                const int kk = k_sh;
                 hist[tid] = 0;
                 __syncthreads();
-                const uint32_t pre = prefix_sh;
                 const uint32_t hmask = shift == 24 ? 0u : (0xffffffffu << (shift + 8));
                 for (int i = tid; i < C; i += 256) {
                     const uint32_t bits = __float_as_uint(pr[i]);
-                    if ((bits & hmask) == (pre & hmask)) atomicAdd(&hist[(bits >> shift) & 255u], 1u);
+                    if ((bits & hmask) == (pre & hmask)) atomicAdd(&hist[(bits >> shift) & 255u], 1);
                 }
                 __syncthreads();
-                if (tid == 0) {
-                    int kk = k_sh;
-                    int bin = 255;
-                    for (; bin > 0; --bin) {
-                        if ((int)hist[bin] >= kk) break;
-                        kk -= (int)hist[bin];
-                    }
-                    k_sh = kk;
-                    prefix_sh = pre | ((uint32_t)bin << shift);
+                // counts from the top bin down; the bin where the running count reaches k
+                const int cnt = hist[255 - tid];
+                const int incl = block_scan_i(cnt, itmp);
+                if (incl >= kk && incl - cnt < kk) {
+                    k_sh = kk - (incl - cnt);
+                    prefix_sh = pre | ((uint32_t)(255 - tid) << shift);
                 }
                 __syncthreads();
             }
             const float cutoff = __uint_as_float(prefix_sh);
-            for (int i = tid; i < C; i += 256) if (pr[i] < cutoff) pr[i] = 0.0f;
+            float mn = __builtin_inff();
+            for (int i = tid; i < C; i += 256) {
+                if (pr[i] < cutoff) pr[i] = 0.0f;
+                else if (pr[i] > 0.0f) mn = mn < pr[i] ? mn : pr[i];
+            }
+            // Every partial sum of these floats is exact in double when no survivor is below
+            // 2^-29 (each is a multiple of 2^-52 and the sums stay below 2): any summation
+            // order then gives the reference's sequential result.
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(mn, off); mn = mn < o ? mn : o; }
+            if (lane == 0) red_f[wave] = mn;
             __syncthreads();
             if (tid == 0) {
-                double total = 0.0;
-                for (int i = 0; i < C; ++i) total += (double)pr[i];
-                inv_sh = (float)(1.0 / total);
+                float m = red_f[0];
+                for (int w = 1; w < 4; ++w) m = m < red_f[w] ? m : red_f[w];
+                exact_sh = m >= 1.862645149230957e-09f;   // 2^-29
+            }
+            __syncthreads();
+            double t = 0.0;
+            if (exact_sh) {
+                for (int i = tid; i < C; i += 256) t += (double)pr[i];
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) t += shfl_xor(t, off);
+                if (lane == 0) red_d[wave] = t;
+                __syncthreads();
+                if (tid == 0) inv_sh = (float)(1.0 / (red_d[0] + red_d[1] + red_d[2] + red_d[3]));
+            } else if (tid == 0) {
+                inv_sh = (float)(1.0 / seq_sum_f(pr, C));
             }
             __syncthreads();
             for (int i = tid; i < C; i += 256) pr[i] = pr[i] * inv_sh;
             __syncthreads();
         }
-        // categorical(probs, 1.0): first i whose running double sum exceeds u
+        // categorical(probs, 1.0): the first i whose running double sum exceeds u
+        float mn = __builtin_inff();
+        for (int i = tid; i < C; i += 256) if (pr[i] > 0.0f) mn = mn < pr[i] ? mn : pr[i];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(mn, off); mn = mn < o ? mn : o; }
+        if (lane == 0) red_f[wave] = mn;
+        __syncthreads();
         if (tid == 0) {
-            const double target = (double)a.uniforms[(size_t)offset * a.n_q + q] * 1.0;
+            float m = red_f[0];
+            for (int w = 1; w < 4; ++w) m = m < red_f[w] ? m : red_f[w];
+            exact_sh = m >= 1.862645149230957e-09f;
+            pick_sh = C - 1;
+        }
+        __syncthreads();
+        const double target = (double)a.uniforms[(size_t)offset * a.n_q + q] * 1.0;
+        if (exact_sh) {
+            // thread t owns elements [SMP_PER*t, SMP_PER*t + SMP_PER); exact prefix sums
+            double loc[SMP_PER];
+            double s = 0.0;
+#pragma unroll
+            for (int e = 0; e < SMP_PER; ++e) {
+                const int i = tid * SMP_PER + e;
+                s += i < C ? (double)pr[i] : 0.0;
+                loc[e] = s;
+            }
+            double incl = s;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const double o = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += o;
+            }
+            if (lane == 63) red_d[wave] = incl;
+            __syncthreads();
+            double base = incl - s;
+            for (int w = 0; w < wave; ++w) base += red_d[w];
+            int found = 0x7fffffff;
+#pragma unroll
+            for (int e = SMP_PER - 1; e >= 0; --e) {
+                const int i = tid * SMP_PER + e;
+                if (i < C && base + loc[e] > target) found = i;
+            }
+            if (found != 0x7fffffff) atomicMin(&pick_sh, found);
+        } else if (tid == 0) {
             double acc = 0.0;
             int pick = C - 1;
             for (int i = 0; i < C; ++i) {
                 acc += (double)pr[i];
                 if (acc > target) { pick = i; break; }
             }
-            tok_sh = pick;
+            pick_sh = pick;
         }
         __syncthreads();
-        token = tok_sh;
+        token = pick_sh;
     }
     if (tid == 0) {
         int32_t* slot = a.seq + (size_t)q * a.steps + offset;
@@ -725,59 +1030,9 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
 }
 
 // ------------------------------------------------------------------------------------
-// launchers
+// repack: ggml blocks -> device layout. Q8_0 {d, q[32]} rows split into q[out][in] +
+// d[out][in/32]; Q4_0 {d, qs[16]} into qs[out][in/2] + d. One thread per block.
 // ------------------------------------------------------------------------------------
-void launch_embed(const EmbedArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed, dim3((a.dim + 255) / 256), dim3(256), 0, s, a);
-}
-void launch_ln_act(const LnArgs& a, int ncol, hipStream_t s) {
-    hipLaunchKernelGGL(k_ln_act, dim3(ncol), dim3(64), 0, s, a);
-}
-void launch_act(const ActArgs& a, int ncol, hipStream_t s) {
-    hipLaunchKernelGGL(k_act, dim3((a.n + 255) / 256, ncol), dim3(256), 0, s, a);
-}
-void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s) {
-    hipLaunchKernelGGL(k_add_bias, dim3((n * ncol + 255) / 256), dim3(256), 0, s, y, b, n, ncol);
-}
-
-template <int NC> static void gemv_nc(const GemvArgs& a, hipStream_t s) {
-    const dim3 grid((a.w.out + 3) / 4), block(256);
-    switch (a.w.type) {
-    case T_Q8_0: hipLaunchKernelGGL(k_gemv_q8<NC>, grid, block, 0, s, a); break;
-    case T_Q4_0: hipLaunchKernelGGL(k_gemv_q4<NC>, grid, block, 0, s, a); break;
-    case T_F16: hipLaunchKernelGGL(k_gemv_f16<NC>, grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL(k_gemv_f32<NC>, grid, block, 0, s, a); break;
-    }
-}
-void launch_gemv(const GemvArgs& a, hipStream_t s) {
-    if (a.ncol <= 1) gemv_nc<1>(a, s);
-    else if (a.ncol <= 2) gemv_nc<2>(a, s);
-    else if (a.ncol <= 4) gemv_nc<4>(a, s);
-    else if (a.ncol <= 8) gemv_nc<8>(a, s);
-    else gemv_nc<16>(a, s);
-}
-void launch_attention(const AttnArgs& a, const ActBuf& out, hipStream_t s) {
-    const dim3 grid(a.max_chunks, a.heads, a.ncol);
-    hipLaunchKernelGGL(k_attn_scores, grid, dim3(256), 0, s, a);
-    hipLaunchKernelGGL(k_attn_softmax_v, grid, dim3(256), 0, s, a);
-    hipLaunchKernelGGL(k_attn_reduce, dim3(a.heads, a.ncol), dim3(64), 0, s, a, out);
-}
-void launch_xattn(const XAttnArgs& a, int heads, hipStream_t s) {
-    hipLaunchKernelGGL(k_xattn, dim3(heads), dim3(256), 0, s, a);
-}
-void launch_xkv_split(const float* kv, int n_ctx, int dim, float* k, float* v, hipStream_t s) {
-    hipLaunchKernelGGL(k_xkv_split, dim3((n_ctx * 2 * dim + 255) / 256), dim3(256), 0, s, kv, n_ctx, dim, k, v);
-}
-void launch_sample(const SampleArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_sample, dim3(a.n_q), dim3(256), 0, s, a);
-}
-
-}  // namespace mgx
-
-namespace mgx {
-
-// ggml blocks -> device layout: Q8_0 {d, q[32]} rows split into q[out][in] + d[out][in/32];
-// Q4_0 {d, qs[16]} into qs[out][in/2] + d. One thread per block.
 __global__ __launch_bounds__(256) void k_repack(int type, const uint8_t* raw, int64_t nblocks, int8_t* q, uint16_t* d) {
     const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (b >= nblocks) return;
@@ -792,6 +1047,70 @@ __global__ __launch_bounds__(256) void k_repack(int type, const uint8_t* raw, in
     }
 }
 
+// ------------------------------------------------------------------------------------
+// launchers
+// ------------------------------------------------------------------------------------
+void launch_embed(const EmbedArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(k_embed, dim3((a.dim + 255) / 256), dim3(256), 0, s, a);
+}
+void launch_advance(int* pos, hipStream_t s) { hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, s, pos); }
+void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s) {
+    hipLaunchKernelGGL(k_add_bias, dim3((n * ncol + 255) / 256), dim3(256), 0, s, y, b, n, ncol);
+}
+
+// Rows per wave: enough rows per launch to keep every CU fed, 8 for the GELU epilogue
+// (32-row blocks quantize inside one workgroup).
+static int rows_per_wave(const GemvArgs& a) {
+    if (a.epi == EPI_GELU_ACT) return 8;
+    if (a.w.out >= 4096) return 4;
+    if (a.w.out >= 2048) return 2;
+    return 1;
+}
+
+template <int WT, int NC, bool LNP> static void gemv_wt_nc_p(const GemvArgs& a, hipStream_t s) {
+    const int R = rows_per_wave(a);
+    const size_t lds = (LNP ? lds_act_bytes(WT, NC, a.w.in) : 0) + (size_t)NC * 4 * 8 * sizeof(float);
+    const dim3 grid((a.w.out + 4 * R - 1) / (4 * R)), block(256);
+    switch (R) {
+    case 8: hipLaunchKernelGGL((k_gemv<WT, NC, 8, LNP>), grid, block, lds, s, a); break;
+    case 4: hipLaunchKernelGGL((k_gemv<WT, NC, 4, LNP>), grid, block, lds, s, a); break;
+    case 2: hipLaunchKernelGGL((k_gemv<WT, NC, 2, LNP>), grid, block, lds, s, a); break;
+    default: hipLaunchKernelGGL((k_gemv<WT, NC, 1, LNP>), grid, block, lds, s, a); break;
+    }
+}
+template <int WT, int NC> static void gemv_wt_nc(const GemvArgs& a, hipStream_t s) {
+    if (a.pro == PRO_ACT) gemv_wt_nc_p<WT, NC, false>(a, s);
+    else gemv_wt_nc_p<WT, NC, true>(a, s);
+}
+template <int WT> static void gemv_wt(const GemvArgs& a, hipStream_t s) {
+    if (a.ncol <= 1) gemv_wt_nc<WT, 1>(a, s);
+    else if (a.ncol <= 2) gemv_wt_nc<WT, 2>(a, s);
+    else gemv_wt_nc<WT, 4>(a, s);
+}
+void launch_gemv(const GemvArgs& a, hipStream_t s) {
+    switch (a.w.type) {
+    case T_Q8_0: gemv_wt<T_Q8_0>(a, s); break;
+    case T_Q4_0: gemv_wt<T_Q4_0>(a, s); break;
+    case T_F16: gemv_wt<T_F16>(a, s); break;
+    default: gemv_wt<T_F32>(a, s); break;
+    }
+}
+void launch_attention(const AttnArgs& a, hipStream_t s) {
+    const dim3 grid(a.max_chunks, a.heads, a.ncol);
+    hipLaunchKernelGGL(k_attn_scores, grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_attn_softmax, dim3(a.heads, a.ncol), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_attn_v, grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_attn_reduce, dim3(a.heads, a.ncol), dim3(64), 0, s, a);
+}
+void launch_xattn(const XAttnArgs& a, int heads, hipStream_t s) {
+    hipLaunchKernelGGL(k_xattn, dim3(heads), dim3(256), 0, s, a);
+}
+void launch_xkv_split(const float* kv, int n_ctx, int dim, float* k, float* v, hipStream_t s) {
+    hipLaunchKernelGGL(k_xkv_split, dim3((n_ctx * 2 * dim + 255) / 256), dim3(256), 0, s, kv, n_ctx, dim, k, v);
+}
+void launch_sample(const SampleArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(k_sample, dim3(a.n_q), dim3(256), 0, s, a);
+}
 void launch_repack(int type, const uint8_t* raw, int64_t rows, int in, void* q, uint16_t* d, hipStream_t s) {
     const int64_t nblocks = rows * (in / 32);
     hipLaunchKernelGGL(k_repack, dim3((unsigned)((nblocks + 255) / 256)), dim3(256), 0, s, type, raw, nblocks, (int8_t*)q, d);

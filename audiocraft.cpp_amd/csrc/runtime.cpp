@@ -13,6 +13,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <algorithm>
 #include <map>
@@ -96,25 +97,41 @@ struct mgx_model {
     ~mgx_model() { mem.release(); }
 };
 
+// Device buffers of activation columns in one of the three forms (Q8_0 blocks, fp16, f32).
+struct ActStore {
+    int8_t* q = nullptr;
+    float* d = nullptr;
+    uint16_t* h = nullptr;
+    float* f = nullptr;
+    int stride = 0;
+    mgx::ActBuf view(int wtype) const {
+        mgx::ActBuf a{};
+        a.kind = act_kind(wtype);
+        a.stride = stride;
+        a.q = q; a.d = d; a.h = h; a.f = f;
+        return a;
+    }
+};
+
 struct mgx_stream {
     mgx_model* m = nullptr;
-    int cap = 0, n_seq = 0, cross = 0, n_ctx = 0, used = 0, forwards = 0, max_chunks = 0, max_in = 0;
+    int cap = 0, n_seq = 0, cross = 0, n_ctx = 0, used = 0, forwards = 0, max_chunks = 0;
     hipStream_t hs = nullptr;
     DevArena mem;
     float *K = nullptr, *V = nullptr;        // per layer [n_seq][H][cap][64]
     float *xk = nullptr, *xv = nullptr;      // per layer [H][n_ctx][64], stream 0
-    float* pos = nullptr;                    // [cap][dim]
-    float *x = nullptr, *qb = nullptr, *ff = nullptr, *scores = nullptr, *opart = nullptr, *logits = nullptr;
-    float *qc = nullptr, *oc = nullptr;      // cross q, cross attention output [dim]
-    int8_t* aq = nullptr;
-    float* ad = nullptr;
-    uint16_t* ah = nullptr;
-    float* af = nullptr;
+    float* table = nullptr;                  // sinusoid [cap][dim]
+    int* dpos = nullptr;                     // the position the next step processes
+    float* cmax = nullptr;                   // [n_seq][H][max_chunks] attention chunk maxima
+    float *x = nullptr, *qb = nullptr, *scores = nullptr, *opart = nullptr, *logits = nullptr;
+    float* qc = nullptr;                     // cross q [dim]
+    ActStore act_o, act_c, act_f;            // attention out, cross-attention out, GELU out
     int32_t* ids = nullptr;                  // [n_q][cap] staged ids for mgx_forward
-    // Launch timing: when `prof_on`, every GEMV and attention launch of a sampled step is
-    // bracketed by HIP events on this stream; read back by the session's profile call.
+    // Launch timing: when `prof_on`, every GEMV and attention launch is bracketed by HIP
+    // events on this stream; read back by the session's profile call.
     struct Mark { hipEvent_t a, b; int kind; double bytes; };
     bool prof_on = false;
+    int prof_pos = 0;                        // host view of the position, for profiling
     std::vector<Mark> marks;
     std::vector<hipEvent_t> event_pool;
     size_t event_next = 0;
@@ -132,14 +149,14 @@ struct mgx_stream {
         }
         return event_pool[event_next++];
     }
-    mgx::ActBuf act(int wtype) const {
-        mgx::ActBuf a{};
-        a.kind = act_kind(wtype);
-        a.stride = max_in;
-        a.q = aq; a.d = ad; a.h = ah; a.f = af;
-        return a;
-    }
     size_t layer_kv() const { return (size_t)n_seq * m->c.heads * cap * 64; }
+    void alloc_act(ActStore& a, int cols, int stride) {
+        a.stride = stride;
+        a.q = mem.alloc<int8_t>((size_t)cols * stride);
+        a.d = mem.alloc<float>((size_t)cols * stride / 32);
+        a.h = mem.alloc<uint16_t>((size_t)cols * stride);
+        a.f = mem.alloc<float>((size_t)cols * stride);
+    }
 };
 
 namespace {
@@ -270,85 +287,111 @@ struct ProfScope {
     }
 };
 
-// One projection of `ncol` activation columns already in s->act(type). Algorithmic bytes
-// of a launch = the weights at their stored precision.
-void gemv(mgx_stream* s, const mgx::DevMat& w, int ncol, const mgx::GemvOut& o) {
-    mgx::GemvArgs a{};
-    a.w = w; a.act = s->act(w.type); a.ncol = ncol; a.o = o;
-    ProfScope ps(s, PROF_GEMV, (double)w.in * w.out * bytes_per_weight(w.type));
+// One projection. Algorithmic bytes of a launch = the weights at their stored precision.
+void gemv(mgx_stream* s, const mgx::GemvArgs& a) {
+    ProfScope ps(s, PROF_GEMV, (double)a.w.in * a.w.out * bytes_per_weight(a.w.type));
     mgx::launch_gemv(a, s->hs);
 }
 
-mgx::GemvOut out_store(float* y, int stride) { mgx::GemvOut o{}; o.mode = mgx::EPI_STORE; o.y = y; o.y_stride = stride; return o; }
-mgx::GemvOut out_resid(float* y, int stride) { mgx::GemvOut o{}; o.mode = mgx::EPI_RESID; o.y = y; o.y_stride = stride; return o; }
-mgx::GemvOut out_gelu(float* y, int stride) { mgx::GemvOut o{}; o.mode = mgx::EPI_GELU; o.y = y; o.y_stride = stride; return o; }
-
-void ln_act(mgx_stream* s, const float* x, int ncol, const float* w, const float* b, int wtype) {
-    mgx::LnArgs a{};
-    a.x = x; a.x_stride = s->m->c.dim; a.dim = s->m->c.dim; a.w = w; a.b = b; a.eps = s->m->c.norm_eps;
-    a.out = s->act(wtype);
-    mgx::launch_ln_act(a, ncol, s->hs);
+mgx::GemvArgs ga(const mgx::DevMat& w, int ncol) {
+    mgx::GemvArgs a{};
+    a.w = w; a.ncol = ncol;
+    return a;
+}
+mgx::GemvArgs& pro_ln(mgx::GemvArgs& a, const float* x, int stride, const float* w, const float* b, float eps) {
+    a.pro = mgx::PRO_LN; a.x = x; a.x_stride = stride; a.ln_w = w; a.ln_b = b; a.eps = eps;
+    return a;
+}
+mgx::GemvArgs& pro_f32(mgx::GemvArgs& a, const float* x, int stride) {
+    a.pro = mgx::PRO_F32; a.x = x; a.x_stride = stride;
+    return a;
+}
+mgx::GemvArgs& pro_act(mgx::GemvArgs& a, const mgx::ActBuf& src) {
+    a.pro = mgx::PRO_ACT; a.src = src;
+    return a;
+}
+mgx::GemvArgs& epi_store(mgx::GemvArgs& a, float* y, int stride, bool resid = false) {
+    a.epi = resid ? mgx::EPI_RESID : mgx::EPI_STORE; a.y = y; a.y_stride = stride;
+    return a;
 }
 
-void to_act(mgx_stream* s, const float* x, int x_stride, int n, int ncol, int wtype) {
-    mgx::ActArgs a{};
-    a.x = x; a.x_stride = x_stride; a.n = n; a.out = s->act(wtype);
-    mgx::launch_act(a, ncol, s->hs);
-}
-
-// One sequence step at cache position `position` for every stream: ids of codebook q at
-// ids[q * ids_stride]. With `heads`, ends with the logits of this step in s->logits.
-void step(mgx_stream* s, const int32_t* ids, int ids_stride, int position, bool heads) {
+// One sequence step at the device position *s->dpos for every stream (codebook q's id at
+// ids[q * ids_stride + pos - ids_base]); with `heads`, the step's logits land in s->logits.
+// Ends by advancing the device position unless `advance` is false.
+void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, bool heads, const mgx::SampleArgs* sample) {
     const mgx_model* m = s->m;
     const mgx_lm_config& c = m->c;
     const int N = s->n_seq, D = c.dim;
     mgx::EmbedArgs e{};
     for (int q = 0; q < c.n_q; ++q) e.emb[q] = m->emb[q];
-    e.n_q = c.n_q; e.ids = ids; e.ids_stride = ids_stride; e.pos = s->pos; e.position = position;
-    e.dim = D; e.x = s->x; e.ncol = N;
+    e.n_q = c.n_q; e.ids = ids; e.ids_stride = ids_stride; e.ids_base = ids_base; e.table = s->table;
+    e.pos = s->dpos; e.dim = D; e.x = s->x; e.ncol = N;
     mgx::launch_embed(e, s->hs);
     const float scale = 1.0f / std::sqrt((float)c.head_dim);
     for (int l = 0; l < c.layers; ++l) {
         const LayerW& L = m->L[(size_t)l];
         float* Kl = s->K + (size_t)l * s->layer_kv();
         float* Vl = s->V + (size_t)l * s->layer_kv();
-        // self-attention
-        ln_act(s, s->x, N, L.n1w, L.n1b, L.w[P_QKV].type);
-        mgx::GemvOut oq{};
-        oq.mode = mgx::EPI_QKV; oq.y = s->qb; oq.k = Kl; oq.v = Vl; oq.dim = D; oq.heads = c.heads;
-        oq.cap = s->cap; oq.position = position;
-        gemv(s, L.w[P_QKV], N, oq);
-        mgx::AttnArgs at{};
-        at.q = s->qb; at.k = Kl; at.v = Vl; at.scores = s->scores; at.opart = s->opart; at.dim = D;
-        at.heads = c.heads; at.cap = s->cap; at.position = position; at.max_chunks = s->max_chunks;
-        at.ncol = N; at.scale = scale;
+        // self-attention: LN1 + qkv with the K/V append, scores, softmax + V (+ chunk reduce)
         {
-            // f32 K and V of every key attended, both streams
-            ProfScope ps(s, PROF_ATTN, 2.0 * N * c.heads * (position + 1) * 64 * 4);
-            mgx::launch_attention(at, s->act(L.w[P_OUT].type), s->hs);
+            mgx::GemvArgs a = ga(L.w[P_QKV], N);
+            pro_ln(a, s->x, D, L.n1w, L.n1b, c.norm_eps);
+            a.epi = mgx::EPI_QKV; a.y = s->qb; a.k = Kl; a.v = Vl; a.dim = D; a.heads = c.heads; a.cap = s->cap;
+            a.pos = s->dpos;
+            gemv(s, a);
         }
-        gemv(s, L.w[P_OUT], N, out_resid(s->x, D));
+        {
+            mgx::AttnArgs at{};
+            at.q = s->qb; at.k = Kl; at.v = Vl; at.scores = s->scores; at.opart = s->opart; at.cmax = s->cmax;
+            at.dim = D; at.heads = c.heads; at.cap = s->cap; at.max_chunks = s->max_chunks; at.ncol = N;
+            at.scale = scale; at.pos = s->dpos; at.out = s->act_o.view(L.w[P_OUT].type);
+            // f32 K and V of every key attended, both streams (bytes known only on device: the
+            // profile records the host's view of the position)
+            ProfScope ps(s, PROF_ATTN, 2.0 * N * c.heads * (s->prof_pos + 1) * 64 * 4);
+            mgx::launch_attention(at, s->hs);
+        }
+        {
+            mgx::GemvArgs a = ga(L.w[P_OUT], N);
+            pro_act(a, s->act_o.view(L.w[P_OUT].type));
+            epi_store(a, s->x, D, true);
+            gemv(s, a);
+        }
         // cross-attention, conditional stream only (the null stream's contribution is 0)
         if (s->cross) {
-            ln_act(s, s->x, 1, L.ncw, L.ncb, L.w[P_CQ].type);
-            gemv(s, L.w[P_CQ], 1, out_store(s->qc, D));
+            mgx::GemvArgs a = ga(L.w[P_CQ], 1);
+            pro_ln(a, s->x, D, L.ncw, L.ncb, c.norm_eps);
+            epi_store(a, s->qc, D);
+            gemv(s, a);
             mgx::XAttnArgs xa{};
             xa.q = s->qc; xa.k = s->xk + (size_t)l * c.heads * s->n_ctx * 64;
-            xa.v = s->xv + (size_t)l * c.heads * s->n_ctx * 64; xa.o = s->oc; xa.n_ctx = s->n_ctx; xa.scale = scale;
+            xa.v = s->xv + (size_t)l * c.heads * s->n_ctx * 64; xa.n_ctx = s->n_ctx; xa.scale = scale;
+            xa.out = s->act_c.view(L.w[P_COUT].type);
             mgx::launch_xattn(xa, c.heads, s->hs);
-            to_act(s, s->oc, D, D, 1, L.w[P_COUT].type);
-            gemv(s, L.w[P_COUT], 1, out_resid(s->x, D));
+            mgx::GemvArgs b = ga(L.w[P_COUT], 1);
+            pro_act(b, s->act_c.view(L.w[P_COUT].type));
+            epi_store(b, s->x, D, true);
+            gemv(s, b);
         }
-        // feed-forward
-        ln_act(s, s->x, N, L.n2w, L.n2b, L.w[P_FF0].type);
-        gemv(s, L.w[P_FF0], N, out_gelu(s->ff, c.ff_dim));
-        to_act(s, s->ff, c.ff_dim, c.ff_dim, N, L.w[P_FF2].type);
-        gemv(s, L.w[P_FF2], N, out_resid(s->x, D));
+        // feed-forward: LN2 + ff.0 + GELU (quantized in the epilogue), ff.2 + residual
+        {
+            mgx::GemvArgs a = ga(L.w[P_FF0], N);
+            pro_ln(a, s->x, D, L.n2w, L.n2b, c.norm_eps);
+            a.epi = mgx::EPI_GELU_ACT; a.dst = s->act_f.view(L.w[P_FF2].type);
+            gemv(s, a);
+            mgx::GemvArgs b = ga(L.w[P_FF2], N);
+            pro_act(b, s->act_f.view(L.w[P_FF2].type));
+            epi_store(b, s->x, D, true);
+            gemv(s, b);
+        }
     }
     if (heads) {
-        ln_act(s, s->x, N, m->out_w, m->out_b, m->heads.type);
-        gemv(s, m->heads, N, out_store(s->logits, c.n_q * c.card));
+        mgx::GemvArgs a = ga(m->heads, N);
+        pro_ln(a, s->x, D, m->out_w, m->out_b, c.norm_eps);
+        epi_store(a, s->logits, c.n_q * c.card);
+        gemv(s, a);
     }
+    if (sample) mgx::launch_sample(*sample, s->hs);
+    mgx::launch_advance(s->dpos, s->hs);
 }
 
 void check_config(const mgx_lm_config& c) {
@@ -359,6 +402,8 @@ void check_config(const mgx_lm_config& c) {
     if (c.n_q <= 0 || c.n_q > 8) throw Error(MGX_ERR_INVALID, "n_q must be in [1, 8]");
     if (c.card <= 0 || c.card > mgx::MAX_CARD) throw Error(MGX_ERR_INVALID, "card must be in [1, 2048]");
     if (c.layers <= 0 || c.cond_dim <= 0 || c.cond_dim % 32) throw Error(MGX_ERR_INVALID, "bad layers or cond_dim");
+    // LayerNorm / conversion prologues give each lane one 32-element block of a column
+    if (c.dim > 2048 || c.cond_dim > 2048) throw Error(MGX_ERR_INVALID, "dim and cond_dim must be at most 2048");
 }
 
 void make_stream(mgx_model* m, int capacity, int n_seq, const float* t5, int n_ctx, int cross, mgx_stream** out) {
@@ -371,29 +416,28 @@ void make_stream(mgx_model* m, int capacity, int n_seq, const float* t5, int n_c
     auto s = std::make_unique<mgx_stream>();
     s->m = m; s->cap = capacity; s->n_seq = n_seq; s->cross = cross ? 1 : 0; s->n_ctx = cross ? n_ctx : 0;
     s->max_chunks = (capacity + mgx::ATT_CHUNK - 1) / mgx::ATT_CHUNK;
-    s->max_in = std::max(c.dim, std::max(c.ff_dim, c.cond_dim));
     HIP_OK(hipStreamCreateWithFlags(&s->hs, hipStreamNonBlocking));
     const size_t kv = s->layer_kv() * c.layers;
     s->K = s->mem.alloc<float>(kv);
     s->V = s->mem.alloc<float>(kv);
     HIP_OK(hipMemsetAsync(s->K, 0, kv * sizeof(float), s->hs));
     HIP_OK(hipMemsetAsync(s->V, 0, kv * sizeof(float), s->hs));
-    s->pos = s->mem.alloc<float>((size_t)capacity * c.dim);
-    const std::vector<float> pos = sin_table(capacity, c);
-    HIP_OK(hipMemcpyAsync(s->pos, pos.data(), pos.size() * sizeof(float), hipMemcpyHostToDevice, s->hs));
-    const int cols = std::max(n_seq, s->n_ctx);
-    s->x = s->mem.alloc<float>((size_t)cols * c.dim);
+    s->table = s->mem.alloc<float>((size_t)capacity * c.dim);
+    const std::vector<float> tab = sin_table(capacity, c);
+    HIP_OK(hipMemcpyAsync(s->table, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice, s->hs));
+    s->dpos = s->mem.alloc<int>(1);
+    HIP_OK(hipMemsetAsync(s->dpos, 0, sizeof(int), s->hs));
+    if (s->max_chunks > mgx::ATT_MAX_CHUNKS) throw Error(MGX_ERR_INVALID, "capacity above 4096 positions");
+    s->cmax = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks);
+    s->x = s->mem.alloc<float>((size_t)n_seq * c.dim);
     s->qb = s->mem.alloc<float>((size_t)n_seq * c.dim);
-    s->ff = s->mem.alloc<float>((size_t)n_seq * c.ff_dim);
     s->scores = s->mem.alloc<float>((size_t)n_seq * c.heads * capacity);
     s->opart = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * 64);
     s->logits = s->mem.alloc<float>((size_t)n_seq * c.n_q * c.card);
     s->qc = s->mem.alloc<float>((size_t)c.dim);
-    s->oc = s->mem.alloc<float>((size_t)c.dim);
-    s->aq = s->mem.alloc<int8_t>((size_t)cols * s->max_in);
-    s->ad = s->mem.alloc<float>((size_t)cols * s->max_in / 32);
-    s->ah = s->mem.alloc<uint16_t>((size_t)cols * s->max_in);
-    s->af = s->mem.alloc<float>((size_t)cols * s->max_in);
+    s->alloc_act(s->act_o, n_seq, c.dim);
+    s->alloc_act(s->act_c, 1, c.dim);
+    s->alloc_act(s->act_f, n_seq, c.ff_dim);
     s->ids = s->mem.alloc<int32_t>((size_t)c.n_q * capacity);
     if (s->cross) {
         // lm.cond_proj . t5 + bias, stream 0 only (pipeline.cpp:144-180), then every layer's
@@ -406,15 +450,18 @@ void make_stream(mgx_model* m, int capacity, int n_seq, const float* t5, int n_c
         s->xk = s->mem.alloc<float>((size_t)c.layers * c.heads * nc * 64);
         s->xv = s->mem.alloc<float>((size_t)c.layers * c.heads * nc * 64);
         for (int col = 0; col < nc; ++col) {
-            to_act(s.get(), t5d + (size_t)col * c.cond_dim, c.cond_dim, c.cond_dim, 1, m->cond_proj.type);
-            gemv(s.get(), m->cond_proj, 1, out_store(ctx + (size_t)col * c.dim, c.dim));
+            mgx::GemvArgs a = ga(m->cond_proj, 1);
+            pro_f32(a, t5d + (size_t)col * c.cond_dim, c.cond_dim);
+            epi_store(a, ctx + (size_t)col * c.dim, c.dim);
+            gemv(s.get(), a);
         }
         mgx::launch_add_bias(ctx, m->cond_proj_b, c.dim, nc, s->hs);
         for (int l = 0; l < c.layers; ++l) {
-            const mgx::DevMat& w = m->L[(size_t)l].w[P_CKV];
             for (int col = 0; col < nc; ++col) {
-                to_act(s.get(), ctx + (size_t)col * c.dim, c.dim, c.dim, 1, w.type);
-                gemv(s.get(), w, 1, out_store(kvp + (size_t)col * 2 * c.dim, 2 * c.dim));
+                mgx::GemvArgs a = ga(m->L[(size_t)l].w[P_CKV], 1);
+                pro_f32(a, ctx + (size_t)col * c.dim, c.dim);
+                epi_store(a, kvp + (size_t)col * 2 * c.dim, 2 * c.dim);
+                gemv(s.get(), a);
             }
             mgx::launch_xkv_split(kvp, nc, c.dim, s->xk + (size_t)l * c.heads * nc * 64,
                                   s->xv + (size_t)l * c.heads * nc * 64, s->hs);
@@ -510,9 +557,11 @@ int mgx_forward(mgx_stream* s, const int32_t* ids, int32_t n_tokens, float* logi
             if (ids[i] < 0 || ids[i] > c.card) throw Error(MGX_ERR_INVALID, "token id out of range");
         HIP_OK(hipSetDevice(s->m->device));
         HIP_OK(hipMemcpyAsync(s->ids, ids, sizeof(int32_t) * (size_t)c.n_q * n_tokens, hipMemcpyHostToDevice, s->hs));
+        const int used = s->used;
+        HIP_OK(hipMemcpyAsync(s->dpos, &used, sizeof(int), hipMemcpyHostToDevice, s->hs));
         // A prefill is the same per-position arithmetic as single steps (its causal mask only
         // adds exact zeros), so the tokens run one position at a time.
-        for (int t = 0; t < n_tokens; ++t) step(s, s->ids + t, n_tokens, s->used + t, t == n_tokens - 1);
+        for (int t = 0; t < n_tokens; ++t) step(s, s->ids, n_tokens, used, t == n_tokens - 1, nullptr);
         HIP_OK(hipGetLastError());
         if (logits_out)
             HIP_OK(hipMemcpyAsync(logits_out, s->logits, sizeof(float) * (size_t)s->n_seq * c.n_q * c.card,
@@ -553,8 +602,17 @@ struct mgx_session {
     mgx::SampleArgs sa{};
     double prefill_seconds = 0.0, decode_seconds = 0.0;
     int prof_every = 0;
+    // One captured prefill position (no heads) and one captured decode step (heads, CFG
+    // mix, sampling, position advance): every kernel reads the position from the device, so
+    // the same graphs replay for every step.
+    hipGraphExec_t g_body = nullptr, g_step = nullptr;
+    // MGX_GRAPHS=0 launches the same kernels one by one (for tools that do not follow
+    // stream capture, such as kernel tracers).
+    bool use_graphs = true;
     ~mgx_session() {
         if (s && s->hs) (void)hipStreamSynchronize(s->hs);
+        if (g_body) (void)hipGraphExecDestroy(g_body);
+        if (g_step) (void)hipGraphExecDestroy(g_step);
         mem.release();
     }
     int pattern_t(int q, int step) const { const int t = step - 1 - q; return (step > 0 && t >= 0 && t < T) ? t : -1; }
@@ -577,6 +635,7 @@ void session_create(mgx_model* m, const float* t5_hidden, int32_t n_ctx, int32_t
         if (prompt[i] < 0 || prompt[i] >= c.card) throw Error(MGX_ERR_INVALID, "prompt code out of range");
     auto ss = std::make_unique<mgx_session>();
     ss->m = m; ss->K = K; ss->T = T;
+    if (const char* g = std::getenv("MGX_GRAPHS")) ss->use_graphs = std::strcmp(g, "0") != 0;
     // DelayPattern with delays 0..n_q-1 (pattern.h:31-115): S = T + n_q, start = P + 1.
     ss->S = 1 + T + (K - 1);
     ss->start = prompt_len + 1;
@@ -620,34 +679,60 @@ void session_create(mgx_model* m, const float* t5_hidden, int32_t n_ctx, int32_t
     sa.logits = st->logits; sa.n_q = K; sa.card = c.card; sa.guided = ss->guided; sa.cfg_coef = p->cfg_coef;
     sa.mask = dmask; sa.steps = S; sa.use_sampling = p->use_sampling; sa.temperature = p->temperature;
     sa.top_k = p->top_k; sa.uniforms = duni; sa.special = c.special_token_id; sa.seq = ss->dseq;
+    sa.start = start; sa.pos = st->dpos; sa.first_logits = ss->dfirst; sa.step_logits = ss->dsteps;
     *out = ss.release();
+}
+
+hipGraphExec_t capture(mgx_session* ss, bool full) {
+    mgx_stream* s = ss->s.get();
+    hipGraph_t g = nullptr;
+    hipGraphExec_t e = nullptr;
+    HIP_OK(hipStreamBeginCapture(s->hs, hipStreamCaptureModeThreadLocal));
+    step(s, ss->dseq, ss->S, 0, full, full ? &ss->sa : nullptr);
+    HIP_OK(hipStreamEndCapture(s->hs, &g));
+    const hipError_t rc = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    HIP_OK(rc);
+    return e;
+}
+
+// One loop iteration's position: the body at a prefill position, or the full step.
+void run_position(mgx_session* ss, bool full, bool profiled, int position) {
+    mgx_stream* s = ss->s.get();
+    if (profiled) {
+        s->prof_on = true;
+        s->prof_pos = position;
+        step(s, ss->dseq, ss->S, 0, full, full ? &ss->sa : nullptr);
+        s->prof_on = false;
+        return;
+    }
+    if (!ss->use_graphs) {
+        step(s, ss->dseq, ss->S, 0, full, full ? &ss->sa : nullptr);
+        return;
+    }
+    hipGraphExec_t& g = full ? ss->g_step : ss->g_body;
+    if (!g) g = capture(ss, full);
+    HIP_OK(hipGraphLaunch(g, s->hs));
 }
 
 // Runs up to n more loop iterations (the first is the prefill), then waits for them.
 int session_step(mgx_session* ss, int n) {
     mgx_stream* s = ss->s.get();
-    const mgx_lm_config& c = ss->m->c;
     HIP_OK(hipSetDevice(ss->m->device));
     const double t0 = now_s();
     const int first = ss->next;
     int done = 0;
     for (; done < n && ss->next < ss->S; ++done) {
         const int offset = ss->next++;
-        const bool sampled_step = ss->prof_every > 0 && (offset - ss->start) % ss->prof_every == 0;
-        s->prof_on = sampled_step;
-        if (offset == ss->start)
-            for (int pos = 0; pos < ss->start; ++pos) step(s, ss->dseq + pos, ss->S, pos, pos == ss->start - 1);
-        else
-            step(s, ss->dseq + (offset - 1), ss->S, offset - 1, true);
-        s->prof_on = false;
-        ss->sa.offset = offset;
-        ss->sa.first_logits = offset == ss->start ? ss->dfirst : nullptr;
-        ss->sa.step_logits = ss->dsteps ? ss->dsteps + (size_t)(offset - ss->start) * ss->K * c.card : nullptr;
-        mgx::launch_sample(ss->sa, s->hs);
+        const bool profiled = ss->prof_every > 0 && (offset - ss->start) % ss->prof_every == 0;
         if (offset == ss->start) {
+            for (int pos = 0; pos < ss->start - 1; ++pos) run_position(ss, false, false, pos);
+            run_position(ss, true, false, ss->start - 1);
             HIP_OK(hipGetLastError());
             HIP_OK(hipStreamSynchronize(s->hs));
             ss->prefill_seconds += now_s() - t0;
+        } else {
+            run_position(ss, true, profiled, offset - 1);
         }
     }
     HIP_OK(hipGetLastError());

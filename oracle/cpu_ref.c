@@ -38,8 +38,9 @@
  *   mul_mat, F16 weights: the activation is rounded to fp16 (RNE); products are exact in
  *     f32; 8-element chunks, chunk c -> partial c mod 64, fmaf in increasing element
  *     order inside a partial, same butterfly. F32 weights: same, without the rounding.
- *   norm: mean and variance as double sums over 64 strided partials + butterfly; result
- *     (x - mean) * (1.0f / sqrtf(var + eps)), then * w, then + b, each rounded in f32.
+ *   norm: mean and variance as double sums, element i -> partial (i/32) mod 64 accumulated
+ *     in increasing i, folded by the same butterfly; result (x - mean) * (1.0f / sqrtf(var +
+ *     eps)), then * w, then + b, each rounded in f32.
  *   soft_max_ext: x*scale (+mask); max; e = expf(x - max); sum of e in double over chunks
  *     of 256 keys (butterfly inside a chunk, chunks added in order); p = e * (float)(1/sum).
  *   attention matmuls (f32 x f32): q.k as 16 partials (dim i -> partial (i/4) mod 16,
@@ -434,13 +435,13 @@ static void matmul(const mat_t* W, const adapter_t* ad, const float* X, int ncol
 REF_API void ref_layer_norm(const float* x, int n, const float* w, const float* b, float eps, float* y) {
     double part[64];
     for (int l = 0; l < 64; ++l) part[l] = 0.0;
-    for (int i = 0; i < n; ++i) part[i & 63] = part[i & 63] + (double)x[i];
+    for (int i = 0; i < n; ++i) part[(i >> 5) & 63] = part[(i >> 5) & 63] + (double)x[i];
     const float mean = (float)(fold_d(part, 64) / (double)n);
     for (int l = 0; l < 64; ++l) part[l] = 0.0;
     for (int i = 0; i < n; ++i) {
         const float v = x[i] - mean;
         y[i] = v;
-        part[i & 63] = part[i & 63] + (double)(v * v);
+        part[(i >> 5) & 63] = part[(i >> 5) & 63] + (double)(v * v);
     }
     const float var = (float)(fold_d(part, 64) / (double)n);
     const float scale = 1.0f / sqrtf(var + eps);
@@ -1145,6 +1146,9 @@ REF_API int ref_generate(const ref_model* m, const float* t5_hidden, int n_ctx, 
     free(codes); free(seq); free(mask); free(out); free(combined); free(scratch); free(feed);
     return rc;
 }
+
+/* Bumped whenever a documented reduction order changes; fixtures record it. */
+REF_API int ref_convention(void) { return 2; }
 
 REF_API void ref_set_threads(int n) {
 #ifdef _OPENMP

@@ -98,6 +98,7 @@ def lib():
         L.ref_generate.argtypes = [P, P, C.c_int, C.c_int, P, C.c_int, C.POINTER(RefGenParams), C.c_int, C.c_int, P, P,
                                    P, C.POINTER(RefReport)]
         L.ref_set_threads.argtypes = [C.c_int]
+        L.ref_convention.restype = C.c_int
         _lib = L
     return _lib
 

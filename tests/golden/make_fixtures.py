@@ -69,7 +69,8 @@ def make(name):
     np.savez_compressed(os.path.join(HERE, name + ".npz"), codes=codes, first_logits=first, step_crc=crc,
                         model_sha256=np.frombuffer(bytes.fromhex(model_digest(m)), np.uint8),
                         t5_crc=np.uint32(zlib.crc32(t5.tobytes())), prompt_crc=np.uint32(zlib.crc32(prompt.tobytes())),
-                        prefill_seconds=rep.prefill_seconds, decode_seconds=rep.decode_seconds)
+                        prefill_seconds=rep.prefill_seconds, decode_seconds=rep.decode_seconds,
+                        convention=np.int32(R.lib().ref_convention()))
     print(f"{name}: {rep.forwards} forwards, prefill {rep.prefill_seconds:.1f} s, decode {rep.decode_seconds:.1f} s, "
           f"total {time.time() - t0:.1f} s", flush=True)
 

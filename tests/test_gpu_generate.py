@@ -98,7 +98,9 @@ def test_full_length_generation_matches_fixture(M, name):
     import sys
     sys.path.insert(0, GOLDEN)
     from make_fixtures import CASES, inputs, model_digest
+    from oracle import cpu_ref as R
     f = _fixture(name)
+    assert int(f["convention"]) == R.lib().ref_convention(), "fixture predates the current reduction order"
     case = CASES[name]
     print(f"full-length generation {name}", flush=True)
     m, t5, prompt = inputs(case)
