@@ -378,15 +378,25 @@ __host__ __device__ inline size_t lds_act_bytes(int wt, int ncol, int in) {
     return (size_t)ncol * in * 4;
 }
 
-// LNP: the prologue builds the activation in LDS (PRO_LN / PRO_F32); otherwise (PRO_ACT)
-// every lane reads its units' activation straight from global memory next to its weights.
-template <int WT, int NC, int R, bool LNP>
+// GEMV: y[col][r] = W[r] . act[col]. G lanes own a row (64/G rows per wave); lane t of a
+// row owns the row's partials p = t, t+G, ... (partial p accumulates units p, p+64, ... in
+// order), so the butterfly's levels off >= G fold inside the lane and only off < G cross
+// lanes -- one shuffle per level for all the wave's rows. LNP: the prologue builds the
+// activation in LDS (PRO_LN / PRO_F32); otherwise (PRO_ACT) every lane reads its units'
+// activation straight from global memory next to its weights.
+constexpr int GEMV_UMAX = 8;   // units per lane per pass
+
+template <int WT, int NC, int G, bool LNP>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+    constexpr int M = 64 / G;        // partials per lane (and rows per wave)
     extern __shared__ __align__(16) uint8_t lds[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = lane % G, rl = lane / G;
     const int in = a.w.in, out = a.w.out;
     const int units = in / unit_elems<WT>();
-    const int row0 = (blockIdx.x * 4 + wave) * R;
+    const int row = (blockIdx.x * 4 + wave) * M + rl;
+    const bool live = row < out;
+    const int upl = t < units ? (units - t + G - 1) / G : 0;   // this lane's units t + G*i
     LdsAct x;
     if (LNP) {
         x.in = in;
@@ -398,99 +408,97 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
         x.in = a.src.stride;
         x.q = a.src.q; x.d = a.src.d; x.h = a.src.h; x.f = a.src.f;
     }
-    float* tile = (float*)(lds + (LNP ? lds_act_bytes(WT, NC, in) : 0));   // GELU_ACT staging [NC][4*R]
+    float* tile = (float*)(lds + (LNP ? lds_act_bytes(WT, NC, in) : 0));   // GELU_ACT staging [NC][32]
 
     float4 xv[8], wv[8], bv[8];
     if (LNP) pro_load<WT>(a, wave, lane, xv, wv, bv);
-    WUnit<WT> cur[R];
-    if (lane < units) {
+    WUnit<WT> cur[GEMV_UMAX];
+    if (live) {
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (row0 + r < out) cur[r].load(a.w, row0 + r, lane);
+        for (int i = 0; i < GEMV_UMAX; ++i)
+            if (i < upl) cur[i].load(a.w, row, t + G * i);
     }
     if (LNP) {
         pro_store<WT>(a, x, wave, lane, xv, wv, bv);
         __syncthreads();
     }
-
-    float part[R][NC];
+    float acc[NC][M];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int n = 0; n < NC; ++n)
 #pragma unroll
-        for (int n = 0; n < NC; ++n) part[r][n] = 0.0f;
-    if (row0 < out) {
-        for (int u = lane; u < units; u += 64) {
-            WUnit<WT> nxt[R];
-            const bool more = u + 64 < units;
-            if (more) {
+        for (int m = 0; m < M; ++m) acc[n][m] = 0.0f;
+    if (live) {
+        for (int base = 0; base < upl; base += GEMV_UMAX) {
+            if (base > 0) {
 #pragma unroll
-                for (int r = 0; r < R; ++r)
-                    if (row0 + r < out) nxt[r].load(a.w, row0 + r, u + 64);
+                for (int i = 0; i < GEMV_UMAX; ++i)
+                    if (base + i < upl) cur[i].load(a.w, row, t + G * (base + i));
             }
 #pragma unroll
-            for (int r = 0; r < R; ++r)
+            for (int i = 0; i < GEMV_UMAX; ++i) {
+                if (base + i >= upl) break;
+                const int u = t + G * (base + i);
 #pragma unroll
                 for (int n = 0; n < NC; ++n)
-                    if (n < a.ncol) part[r][n] = cur[r].dot(x, n, u, part[r][n]);
-            if (more) {
-#pragma unroll
-                for (int r = 0; r < R; ++r) cur[r] = nxt[r];
+                    if (n < a.ncol) acc[n][i % M] = cur[i].dot(x, n, u, acc[n][i % M]);
             }
         }
     }
+    // butterfly: levels off >= G inside the lane, off < G across the row's lanes
+    float v[NC];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int n = 0; n < NC; ++n) {
 #pragma unroll
-        for (int n = 0; n < NC; ++n) part[r][n] = fold64(part[r][n]);
+        for (int h = M / 2; h >= 1; h >>= 1)
+#pragma unroll
+            for (int m = 0; m < h; ++m) acc[n][m] = acc[n][m] + acc[n][m + h];
+        float r = acc[n][0];
+#pragma unroll
+        for (int off = G / 2; off >= 1; off >>= 1) r = r + shfl_xor(r, off);
+        v[n] = r;
+    }
 
     if (a.epi == EPI_GELU_ACT) {
-        // rows [blockIdx.x*4R, +4R) -> GELU -> LDS tile -> activation form (32-row blocks)
+        // the block's 32 rows (G = 8) -> GELU -> LDS tile -> activation form
+        const int rb = wave * M + rl;
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int n = 0; n < NC; ++n)
-                if (lane == r * NC + n && n < a.ncol) tile[n * 4 * R + wave * R + r] = gelu_erf(part[r][n]);
+        for (int n = 0; n < NC; ++n)
+            if (t == n && n < a.ncol) tile[n * 32 + rb] = gelu_erf(v[n]);
         __syncthreads();
-        const int rows = 4 * R, base = blockIdx.x * rows;
-        for (int n = 0; n < a.ncol; ++n)
-            for (int i0 = 0; i0 < rows; i0 += 256) {
-                const int i = i0 + threadIdx.x;
-                const float v = i < rows ? tile[n * rows + i] : 0.0f;
-                const int ln = threadIdx.x & 63;
-                if (i0 + (threadIdx.x & ~63) < rows) {
-                    const ActBuf& d = a.dst;
-                    if (d.kind == ACT_Q8) {
-                        int8_t qv;
-                        float dv;
-                        quant_q8_lane(v, ln, &qv, &dv);
-                        if (i < rows) {
-                            d.q[(size_t)n * d.stride + base + i] = qv;
-                            if ((ln & 31) == 0) d.d[(size_t)n * (d.stride / 32) + (base + i) / 32] = dv;
-                        }
-                    } else if (i < rows) {
-                        if (d.kind == ACT_F16) d.h[(size_t)n * d.stride + base + i] = f2h(v);
-                        else d.f[(size_t)n * d.stride + base + i] = v;
+        const int base = blockIdx.x * 32;
+        if (wave == 0) {
+            for (int n = 0; n < a.ncol; ++n) {
+                const float g = lane < 32 ? tile[n * 32 + lane] : 0.0f;
+                const ActBuf& d = a.dst;
+                if (d.kind == ACT_Q8) {
+                    int8_t qv;
+                    float dv;
+                    quant_q8_lane(g, lane, &qv, &dv);
+                    if (lane < 32) {
+                        d.q[(size_t)n * d.stride + base + lane] = qv;
+                        if (lane == 0) d.d[(size_t)n * (d.stride / 32) + base / 32] = dv;
                     }
+                } else if (lane < 32) {
+                    if (d.kind == ACT_F16) d.h[(size_t)n * d.stride + base + lane] = f2h(g);
+                    else d.f[(size_t)n * d.stride + base + lane] = g;
                 }
             }
+        }
         return;
     }
+    if (!live) return;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int row = row0 + r;
-#pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            if (lane != r * NC + n || n >= a.ncol || row >= out) continue;
-            const float v = part[r][n];
-            if (a.epi == EPI_STORE) a.y[(size_t)n * a.y_stride + row] = v;
-            else if (a.epi == EPI_RESID) {
-                float* p = a.y + (size_t)n * a.y_stride + row;
-                *p = *p + v;
-            } else {
-                const int sec = row / a.dim, w = row - sec * a.dim, head = w >> 6, dim = w & 63;
-                if (sec == 0) a.y[(size_t)n * a.dim + w] = v;
-                else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + *a.pos) * 64 + dim] = v;
-            }
+    for (int n = 0; n < NC; ++n) {
+        if (t != n || n >= a.ncol) continue;
+        const float r = v[n];
+        if (a.epi == EPI_STORE) a.y[(size_t)n * a.y_stride + row] = r;
+        else if (a.epi == EPI_RESID) {
+            float* p = a.y + (size_t)n * a.y_stride + row;
+            *p = *p + r;
+        } else {
+            const int sec = row / a.dim, w = row - sec * a.dim, head = w >> 6, dim = w & 63;
+            if (sec == 0) a.y[(size_t)n * a.dim + w] = r;
+            else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + *a.pos) * 64 + dim] = r;
         }
     }
 }
@@ -1058,24 +1066,27 @@ void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s) {
     hipLaunchKernelGGL(k_add_bias, dim3((n * ncol + 255) / 256), dim3(256), 0, s, y, b, n, ncol);
 }
 
-// Rows per wave: enough rows per launch to keep every CU fed, 8 for the GELU epilogue
-// (32-row blocks quantize inside one workgroup).
-static int rows_per_wave(const GemvArgs& a) {
+// Lanes per row: 8 for the GELU epilogue (32-row blocks quantize inside one workgroup);
+// otherwise the fewest lanes that keep a lane's units within one pass and give >= 160
+// workgroups.
+static int lanes_per_row(const GemvArgs& a) {
+    const int units = a.w.in / ((a.w.type == T_Q8_0 || a.w.type == T_Q4_0) ? 32 : 8);
     if (a.epi == EPI_GELU_ACT) return 8;
-    if (a.w.out >= 4096) return 4;
-    if (a.w.out >= 2048) return 2;
-    return 1;
+    for (int G = 16; G < 64; G *= 2)
+        if ((units + G - 1) / G <= GEMV_UMAX && (long)a.w.out * G / 256 >= 160) return G;
+    return 64;
 }
 
 template <int WT, int NC, bool LNP> static void gemv_wt_nc_p(const GemvArgs& a, hipStream_t s) {
-    const int R = rows_per_wave(a);
-    const size_t lds = (LNP ? lds_act_bytes(WT, NC, a.w.in) : 0) + (size_t)NC * 4 * 8 * sizeof(float);
-    const dim3 grid((a.w.out + 4 * R - 1) / (4 * R)), block(256);
-    switch (R) {
+    const int G = lanes_per_row(a);
+    const size_t lds = (LNP ? lds_act_bytes(WT, NC, a.w.in) : 0) + (size_t)NC * 32 * sizeof(float);
+    const int rows_per_block = 256 / G;
+    const dim3 grid((a.w.out + rows_per_block - 1) / rows_per_block), block(256);
+    switch (G) {
     case 8: hipLaunchKernelGGL((k_gemv<WT, NC, 8, LNP>), grid, block, lds, s, a); break;
-    case 4: hipLaunchKernelGGL((k_gemv<WT, NC, 4, LNP>), grid, block, lds, s, a); break;
-    case 2: hipLaunchKernelGGL((k_gemv<WT, NC, 2, LNP>), grid, block, lds, s, a); break;
-    default: hipLaunchKernelGGL((k_gemv<WT, NC, 1, LNP>), grid, block, lds, s, a); break;
+    case 16: hipLaunchKernelGGL((k_gemv<WT, NC, 16, LNP>), grid, block, lds, s, a); break;
+    case 32: hipLaunchKernelGGL((k_gemv<WT, NC, 32, LNP>), grid, block, lds, s, a); break;
+    default: hipLaunchKernelGGL((k_gemv<WT, NC, 64, LNP>), grid, block, lds, s, a); break;
     }
 }
 template <int WT, int NC> static void gemv_wt_nc(const GemvArgs& a, hipStream_t s) {

@@ -406,6 +406,36 @@ void check_config(const mgx_lm_config& c) {
     if (c.dim > 2048 || c.cond_dim > 2048) throw Error(MGX_ERR_INVALID, "dim and cond_dim must be at most 2048");
 }
 
+// Every tensor the LM reads, checked before any device work (names, shapes, types, sizes).
+void validate_tensors(const mgx_lm_config& c, const mgx_tensor* t, int n) {
+    const mgx_tensor* h0 = nullptr;
+    for (int q = 0; q < c.n_q; ++q) {
+        need(t, n, "lm.emb." + std::to_string(q) + ".weight", c.dim, c.card + 1);
+        const mgx_tensor& h = need(t, n, "lm.head." + std::to_string(q) + ".weight", c.dim, c.card);
+        if (h0 && h.type != h0->type) throw Error(MGX_ERR_INVALID, "the output heads must share one type");
+        h0 = &h;
+    }
+    need(t, n, "lm.cond_proj.weight", c.cond_dim, c.dim);
+    auto vec = [&](const std::string& name) {
+        const mgx_tensor* x = find(t, n, name);
+        if (!x || x->type != mgx::T_F32 || x->ne[0] != c.dim || !x->data)
+            throw Error(MGX_ERR_INVALID, "missing or bad f32 vector " + name);
+    };
+    vec("lm.cond_proj.bias");
+    vec("lm.out_norm.weight");
+    vec("lm.out_norm.bias");
+    for (int i = 0; i < c.layers; ++i) {
+        const std::string p = "lm." + std::to_string(i) + ".";
+        const int ins[P_COUNT] = {c.dim, c.dim, c.dim, c.dim, c.dim, c.dim, c.ff_dim};
+        const int outs[P_COUNT] = {3 * c.dim, c.dim, c.dim, 2 * c.dim, c.dim, c.ff_dim, c.dim};
+        for (int k = 0; k < P_COUNT; ++k) need(t, n, p + PROJ[k] + ".weight", ins[k], outs[k]);
+        for (const char* nm : {"norm1", "norm_cross", "norm2"}) {
+            vec(p + nm + ".weight");
+            vec(p + nm + ".bias");
+        }
+    }
+}
+
 void make_stream(mgx_model* m, int capacity, int n_seq, const float* t5, int n_ctx, int cross, mgx_stream** out) {
     const mgx_lm_config& c = m->c;
     if (capacity <= 0 || n_seq <= 0) throw Error(MGX_ERR_INVALID, "the kv cache needs positive dimensions");
@@ -485,6 +515,7 @@ int mgx_model_create(const mgx_lm_config* cfg, const mgx_tensor* t, int32_t n, m
         if (!cfg || !t || !out) throw Error(MGX_ERR_INVALID, "null argument");
         *out = nullptr;
         check_config(*cfg);
+        validate_tensors(*cfg, t, n);
         auto m = std::make_unique<mgx_model>();
         m->c = *cfg;
         const mgx_lm_config& c = *cfg;

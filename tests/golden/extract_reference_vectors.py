@@ -1,0 +1,60 @@
+#!/usr/bin/env python3
+"""Copies the golden vectors that the reference's own unit tests hold -- as data -- into
+tests/golden/*.json: the softmax / top-k / argmax fixtures of tests/sampling_test.cpp
+(generated there by tests/gen_sampling_fixture.py from audiocraft's sample_top_k) and the
+delay-pattern fixtures of tests/pattern_test.cpp (from audiocraft's DelayedPatternProvider).
+
+Reads the reference tree as text (default /root/reference); run once, outputs committed."""
+import json
+import os
+import re
+import sys
+
+REF = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def arrays(text, ctype):
+    out = {}
+    for m in re.finditer(r"static const %s (\w+)\[\] = \{([^}]*)\};" % ctype, text):
+        vals = [v.strip().rstrip("f") for v in m.group(2).replace("\n", " ").split(",") if v.strip()]
+        out[m.group(1)] = [float(v) if ctype == "float" else int(v) for v in vals]
+    return out
+
+
+def consts(text):
+    out = {}
+    for m in re.finditer(r"constexpr (?:int|float) ([^;]+);", text):
+        for part in m.group(1).split(","):
+            k, v = part.split("=")
+            out[k.strip()] = float(v.strip().rstrip("f"))
+    return out
+
+
+def sampling():
+    text = open(os.path.join(REF, "tests", "sampling_test.cpp")).read()
+    fa, cs = arrays(text, "float"), consts(text)
+    cases = {}
+    for tag in ("PLAIN", "HOT", "COLD", "WIDE", "TIED"):
+        cases[tag] = dict(n=int(cs[f"{tag}_N"]), k=int(cs[f"{tag}_K"]), survivors=int(cs[f"{tag}_SURVIVORS"]),
+                          temperature=cs[f"{tag}_TEMPERATURE"], argmax=int(cs[f"{tag}_ARGMAX"]),
+                          logits=fa[f"{tag}_logits"], softmax=fa[f"{tag}_softmax"], filtered=fa[f"{tag}_filtered"])
+    return {"source": "tests/sampling_test.cpp:81-192", "cases": cases}
+
+
+def pattern():
+    text = open(os.path.join(REF, "tests", "pattern_test.cpp")).read()
+    ia, cs = arrays(text, "int32_t"), consts(text)
+    cases = {}
+    for tag in ("MG", "ONE", "THREE"):
+        cases[tag] = dict(n_q=int(cs[f"{tag}_NQ"]), timesteps=int(cs[f"{tag}_T"]), steps=int(cs[f"{tag}_S"]),
+                          special=int(cs[f"{tag}_SPECIAL"]), codes=ia[f"{tag}_codes"], sequence=ia[f"{tag}_sequence"],
+                          mask=ia[f"{tag}_mask"], reverted=ia[f"{tag}_reverted"], first_step=ia[f"{tag}_first_step"])
+    return {"source": "tests/pattern_test.cpp:90-146", "cases": cases}
+
+
+if __name__ == "__main__":
+    for name, fn in (("sampling_cases.json", sampling), ("pattern_cases.json", pattern)):
+        with open(os.path.join(HERE, name), "w") as f:
+            json.dump(fn(), f, indent=1)
+        print("wrote", name)
