@@ -8,7 +8,8 @@
 //     exact integer block dots (v_dot4), term = (float)isum * (dw*dx), terms of a row summed
 //     as 64 lane-strided partials (lane l owns blocks l, l+64, ...) then a xor butterfly;
 //   * F16 / F32 GEMV: the same with 8-element chunks and fmaf;
-//   * LayerNorm: double partial sums per lane, butterfly, (x-mean)*(1/sqrtf(var+eps))*w+b;
+//   * LayerNorm: 256 double partials (partial i sums float4 groups i, i+256, ... in element
+//     order), butterfly, (x-mean)*(1/sqrtf(var+eps))*w+b;
 //   * attention: keys in chunks of 256; q.k as 16 four-dim fmaf partials + butterfly;
 //     softmax sum in double per chunk (butterfly), chunks added in order; V as 16 key-strided
 //     partials per chunk + butterfly, chunk results added in order;
@@ -172,11 +173,83 @@ __global__ __launch_bounds__(256) void k_add_bias(float* y, const float* b, int 
 }
 
 // ------------------------------------------------------------------------------------
-// GEMV: y[col][r] = W[r] . act[col]. A wave owns R consecutive rows; lane l owns the row's
-// units l, l+64, ... (a unit is a 32-element block for Q8_0 / Q4_0, 8 elements for F16 /
-// F32). The first pass of weights is requested before the prologue builds the activation
-// columns in LDS, so HBM latency hides behind the LayerNorm / quantization work.
+// GEMV: y[col][r] = W[r] . act[col] for up to 4 columns per launch.
+//
+// Layout: G lanes own a row (64/G rows per wave, WAVES waves per block); lane t of a row owns
+// the row's partials p = t, t+G, ... and partial p accumulates units p, p+64, ... in order (a
+// unit is a 32-element block for Q8_0 / Q4_0, 8 elements for F16 / F32), so the 64-partial
+// butterfly's levels off >= G fold inside the lane and only off < G cross lanes.
+//
+// Issue order: the activation source (f32 columns, or the consumer-form activation), then
+// every weight unit of the lane, then the residual -- vector-memory completions are counted
+// in order, so the prologue only waits for its own loads. The prologue (LayerNorm /
+// conversion / copy) builds the activation columns in LDS; the barriers wait for LDS only,
+// so the dots start while later weight units are still arriving.
 // ------------------------------------------------------------------------------------
+constexpr int GEMV_KA = 4;   // 16-byte activation chunks per thread issued up front (PRO_ACT)
+
+// lane l gets v[l + OFF] (OFF < 16: row-local DPP shift; 16 / 32: gfx950 permlane swaps);
+// lanes whose source falls outside get garbage -- callers only use lanes that stay inside.
+template <int OFF> __device__ __forceinline__ float take_up(float v) {
+    if constexpr (OFF == 32) {
+        auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(r[1]);
+    } else if constexpr (OFF == 16) {
+        auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(r[1]);
+    } else {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + OFF, 0xf, 0xf, true));
+    }
+}
+template <int OFF> __device__ __forceinline__ double take_up_d(double v) {
+    const uint64_t b = __double_as_longlong(v);
+    const float lo = take_up<OFF>(__uint_as_float((uint32_t)b));
+    const float hi = take_up<OFF>(__uint_as_float((uint32_t)(b >> 32)));
+    return __longlong_as_double((long long)(((uint64_t)__float_as_uint(hi) << 32) | __float_as_uint(lo)));
+}
+// lane l gets v[l - OFF] inside its 16-lane row
+template <int OFF> __device__ __forceinline__ float take_dn(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x110 + OFF, 0xf, 0xf, true));
+}
+// Butterfly p[l] += p[l + off], off = G/2 .. 1: lane 0 of each G-lane group ends with the
+// group's value (the butterfly's lane-0 result).
+template <int G> __device__ __forceinline__ float fold_to0(float v) {
+    if constexpr (G >= 64) v = v + take_up<32>(v);
+    if constexpr (G >= 32) v = v + take_up<16>(v);
+    if constexpr (G >= 16) v = v + take_up<8>(v);
+    if constexpr (G >= 8) v = v + take_up<4>(v);
+    if constexpr (G >= 4) v = v + take_up<2>(v);
+    if constexpr (G >= 2) v = v + take_up<1>(v);
+    return v;
+}
+// 64-lane double butterfly, result broadcast from lane 0
+__device__ __forceinline__ double fold64d_b(double v) {
+    v = v + take_up_d<32>(v);
+    v = v + take_up_d<16>(v);
+    v = v + take_up_d<8>(v);
+    v = v + take_up_d<4>(v);
+    v = v + take_up_d<2>(v);
+    v = v + take_up_d<1>(v);
+    const uint64_t b = __double_as_longlong(v);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b), hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+// max over each 8-lane group, to the group's first lane; then to all 8 lanes
+__device__ __forceinline__ float grp8_max_to0(float v) {
+    float o = take_up<1>(v); v = v > o ? v : o;
+    o = take_up<2>(v); v = v > o ? v : o;
+    o = take_up<4>(v); v = v > o ? v : o;
+    return v;
+}
+__device__ __forceinline__ float grp8_bcast(float v, int lane) {
+    float s = take_dn<1>(v); v = (lane & 1) ? s : v;
+    s = take_dn<2>(v); v = (lane & 2) ? s : v;
+    s = take_dn<4>(v); v = (lane & 4) ? s : v;
+    return v;
+}
+// Workgroup barrier for LDS traffic only: global loads in flight are not waited for.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 struct LdsAct {
     int8_t* q;     // Q8 [col][in]
     float* d;      // Q8 [col][in/32]
@@ -194,24 +267,7 @@ template <> struct WUnit<T_Q8_0> {
         a = *(const int4*)p; b = *(const int4*)(p + 16);
         d = m.d[(size_t)r * (m.in / 32) + u];
     }
-    __device__ __forceinline__ float dot(const LdsAct& x, int n, int u, float p) const {
-        const int8_t* xq = x.q + (size_t)n * x.in + u * 32;
-        const int4 x0 = *(const int4*)xq, x1 = *(const int4*)(xq + 16);
-        int s = __builtin_amdgcn_sdot4(a.x, x0.x, 0, false);
-        s = __builtin_amdgcn_sdot4(a.y, x0.y, s, false);
-        s = __builtin_amdgcn_sdot4(a.z, x0.z, s, false);
-        s = __builtin_amdgcn_sdot4(a.w, x0.w, s, false);
-        s = __builtin_amdgcn_sdot4(b.x, x1.x, s, false);
-        s = __builtin_amdgcn_sdot4(b.y, x1.y, s, false);
-        s = __builtin_amdgcn_sdot4(b.z, x1.z, s, false);
-        s = __builtin_amdgcn_sdot4(b.w, x1.w, s, false);
-        const float dd = h2f(d) * x.d[(size_t)n * (x.in / 32) + u];
-        const float term = (float)s * dd;
-        return p + term;
-    }
 };
-
-// Q4_0: sum((nib-8)*x) = sum(nib*x) - 8*sum(x), both exact integer dots.
 template <> struct WUnit<T_Q4_0> {
     int4 a;
     uint16_t d;
@@ -219,154 +275,91 @@ template <> struct WUnit<T_Q4_0> {
         a = *(const int4*)((const uint8_t*)m.q + (size_t)r * (m.in / 2) + u * 16);
         d = m.d[(size_t)r * (m.in / 32) + u];
     }
-    __device__ __forceinline__ float dot(const LdsAct& x, int n, int u, float p) const {
-        const int8_t* xq = x.q + (size_t)n * x.in + u * 32;
-        const int4 x0 = *(const int4*)xq, x1 = *(const int4*)(xq + 16);
-        const uint32_t ws[4] = {(uint32_t)a.x, (uint32_t)a.y, (uint32_t)a.z, (uint32_t)a.w};
-        const int xl[4] = {x0.x, x0.y, x0.z, x0.w}, xh[4] = {x1.x, x1.y, x1.z, x1.w};
-        int s = 0, sx = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            s = __builtin_amdgcn_sdot4((int)(ws[k] & 0x0f0f0f0fu), xl[k], s, false);
-            s = __builtin_amdgcn_sdot4((int)((ws[k] >> 4) & 0x0f0f0f0fu), xh[k], s, false);
-            sx = __builtin_amdgcn_sdot4(0x01010101, xl[k], sx, false);
-            sx = __builtin_amdgcn_sdot4(0x01010101, xh[k], sx, false);
-        }
-        const int isum = s - 8 * sx;
-        const float dd = h2f(d) * x.d[(size_t)n * (x.in / 32) + u];
-        const float term = (float)isum * dd;
-        return p + term;
-    }
 };
-
-// F16 weights x fp16-rounded activations: products exact in f32, fmaf in element order.
 template <> struct WUnit<T_F16> {
     int4 a;
     __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
         a = *(const int4*)((const uint16_t*)m.q + (size_t)r * m.in + u * 8);
     }
-    __device__ __forceinline__ float dot(const LdsAct& x, int n, int u, float p) const {
-        const int4 xv = *(const int4*)(x.h + (size_t)n * x.in + u * 8);
-        const uint32_t w32[4] = {(uint32_t)a.x, (uint32_t)a.y, (uint32_t)a.z, (uint32_t)a.w};
-        const uint32_t x32[4] = {(uint32_t)xv.x, (uint32_t)xv.y, (uint32_t)xv.z, (uint32_t)xv.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            p = __builtin_fmaf(h2f((uint16_t)(w32[e] & 0xffffu)), h2f((uint16_t)(x32[e] & 0xffffu)), p);
-            p = __builtin_fmaf(h2f((uint16_t)(w32[e] >> 16)), h2f((uint16_t)(x32[e] >> 16)), p);
-        }
-        return p;
-    }
 };
-
 template <> struct WUnit<T_F32> {
     float4 a, b;
     __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
         const float* p = (const float*)m.q + (size_t)r * m.in + u * 8;
         a = *(const float4*)p; b = *(const float4*)(p + 4);
     }
-    __device__ __forceinline__ float dot(const LdsAct& x, int n, int u, float p) const {
+};
+
+// one unit of one activation column, read from LDS
+template <int WT> struct ActUnit {
+    int4 a, b;
+    float d;
+    __device__ __forceinline__ void load(const LdsAct& x, int n, int u) {
+        const int8_t* xq = x.q + (size_t)n * x.in + u * 32;
+        a = *(const int4*)xq; b = *(const int4*)(xq + 16);
+        d = x.d[(size_t)n * (x.in / 32) + u];
+    }
+};
+template <> struct ActUnit<T_F16> {
+    int4 a;
+    __device__ __forceinline__ void load(const LdsAct& x, int n, int u) { a = *(const int4*)(x.h + (size_t)n * x.in + u * 8); }
+};
+template <> struct ActUnit<T_F32> {
+    float4 a, b;
+    __device__ __forceinline__ void load(const LdsAct& x, int n, int u) {
         const float* xf = x.f + (size_t)n * x.in + u * 8;
-        const float4 x0 = *(const float4*)xf, x1 = *(const float4*)(xf + 4);
-        p = __builtin_fmaf(a.x, x0.x, p); p = __builtin_fmaf(a.y, x0.y, p);
-        p = __builtin_fmaf(a.z, x0.z, p); p = __builtin_fmaf(a.w, x0.w, p);
-        p = __builtin_fmaf(b.x, x1.x, p); p = __builtin_fmaf(b.y, x1.y, p);
-        p = __builtin_fmaf(b.z, x1.z, p); p = __builtin_fmaf(b.w, x1.w, p);
-        return p;
+        a = *(const float4*)xf; b = *(const float4*)(xf + 4);
     }
 };
 
-// LayerNorm / conversion prologue: the activation columns of one launch are built in LDS by
-// every block (cheap, and it saves a launch and a round trip through memory). Wave n owns
-// column n, lane b its 32-element block b. The loads are issued before the weight loads --
-// vector-memory completions are counted in order, so loads issued after the weights would
-// wait for them -- and held in kernel-local registers until the weights are in flight.
-template <int WT>
-__device__ __forceinline__ void pro_load(const GemvArgs& a, int wave, int lane, float4 (&xv)[8], float4 (&wv)[8],
-                                         float4 (&bv)[8]) {
-    if (wave < a.ncol && lane < a.w.in / 32) {
-        const float4* xs = (const float4*)(a.x + (size_t)wave * a.x_stride + lane * 32);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) xv[k] = xs[k];
-        if (a.pro == PRO_LN) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                wv[k] = ((const float4*)(a.ln_w + lane * 32))[k];
-                bv[k] = ((const float4*)(a.ln_b + lane * 32))[k];
-            }
-        }
-    }
+// Q8_0: exact integer block dot, term = (float)isum * (dw*dx).
+__device__ __forceinline__ float dotr(const WUnit<T_Q8_0>& w, const ActUnit<T_Q8_0>& x, float p) {
+    int s = __builtin_amdgcn_sdot4(w.a.x, x.a.x, 0, false);
+    s = __builtin_amdgcn_sdot4(w.a.y, x.a.y, s, false);
+    s = __builtin_amdgcn_sdot4(w.a.z, x.a.z, s, false);
+    s = __builtin_amdgcn_sdot4(w.a.w, x.a.w, s, false);
+    s = __builtin_amdgcn_sdot4(w.b.x, x.b.x, s, false);
+    s = __builtin_amdgcn_sdot4(w.b.y, x.b.y, s, false);
+    s = __builtin_amdgcn_sdot4(w.b.z, x.b.z, s, false);
+    s = __builtin_amdgcn_sdot4(w.b.w, x.b.w, s, false);
+    const float dd = h2f(w.d) * x.d;
+    const float term = (float)s * dd;
+    return p + term;
 }
-
-template <int WT>
-__device__ __forceinline__ void pro_store(const GemvArgs& a, const LdsAct& x, int wave, int lane, const float4 (&xv)[8],
-                                          const float4 (&wv)[8], const float4 (&bv)[8]) {
-    if (wave >= a.ncol) return;
-    const int in = a.w.in, nb = in / 32;
-    const bool mine = lane < nb;
-    float v[32];
+// Q4_0: sum((nib-8)*x) = sum(nib*x) - 8*sum(x), both exact integer dots.
+__device__ __forceinline__ float dotr(const WUnit<T_Q4_0>& w, const ActUnit<T_Q4_0>& x, float p) {
+    const uint32_t ws[4] = {(uint32_t)w.a.x, (uint32_t)w.a.y, (uint32_t)w.a.z, (uint32_t)w.a.w};
+    const int xl[4] = {x.a.x, x.a.y, x.a.z, x.a.w}, xh[4] = {x.b.x, x.b.y, x.b.z, x.b.w};
+    int s = 0, sx = 0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        v[4 * k] = xv[k].x; v[4 * k + 1] = xv[k].y; v[4 * k + 2] = xv[k].z; v[4 * k + 3] = xv[k].w;
+    for (int k = 0; k < 4; ++k) {
+        s = __builtin_amdgcn_sdot4((int)(ws[k] & 0x0f0f0f0fu), xl[k], s, false);
+        s = __builtin_amdgcn_sdot4((int)((ws[k] >> 4) & 0x0f0f0f0fu), xh[k], s, false);
+        sx = __builtin_amdgcn_sdot4(0x01010101, xl[k], sx, false);
+        sx = __builtin_amdgcn_sdot4(0x01010101, xh[k], sx, false);
     }
-    if (a.pro == PRO_LN) {
-        // LayerNorm (transformer.h:28-38): block b's elements summed in order (double) by
-        // lane b, lanes folded by the butterfly.
-        double s = 0.0;
-        if (mine) {
+    const int isum = s - 8 * sx;
+    const float dd = h2f(w.d) * x.d;
+    const float term = (float)isum * dd;
+    return p + term;
+}
+// F16 weights x fp16-rounded activations: products exact in f32, fmaf in element order.
+__device__ __forceinline__ float dotr(const WUnit<T_F16>& w, const ActUnit<T_F16>& x, float p) {
+    const uint32_t w32[4] = {(uint32_t)w.a.x, (uint32_t)w.a.y, (uint32_t)w.a.z, (uint32_t)w.a.w};
+    const uint32_t x32[4] = {(uint32_t)x.a.x, (uint32_t)x.a.y, (uint32_t)x.a.z, (uint32_t)x.a.w};
 #pragma unroll
-            for (int j = 0; j < 32; ++j) s = s + (double)v[j];
-        }
-        s = fold64d(s);
-        const float mean = (float)(s / (double)in);
-        double s2 = 0.0;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            v[j] = v[j] - mean;
-            if (mine) s2 = s2 + (double)(v[j] * v[j]);
-        }
-        s2 = fold64d(s2);
-        const float var = (float)(s2 / (double)in);
-        const float scale = 1.0f / __builtin_sqrtf(var + a.eps);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float w4[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
-            const float b4[4] = {bv[k].x, bv[k].y, bv[k].z, bv[k].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float t = v[4 * k + e] * scale;
-                t = t * w4[e];
-                v[4 * k + e] = t + b4[e];
-            }
-        }
+    for (int e = 0; e < 4; ++e) {
+        p = __builtin_fmaf(h2f((uint16_t)(w32[e] & 0xffffu)), h2f((uint16_t)(x32[e] & 0xffffu)), p);
+        p = __builtin_fmaf(h2f((uint16_t)(w32[e] >> 16)), h2f((uint16_t)(x32[e] >> 16)), p);
     }
-    if (!mine) return;
-    const int n = wave, i0 = lane * 32;
-    if (WT == T_Q8_0 || WT == T_Q4_0) {
-        float amax = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) { const float t = __builtin_fabsf(v[j]); amax = amax > t ? amax : t; }
-        const float d = amax / 127.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        int32_t packed[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                word |= (uint32_t)(uint8_t)(int8_t)__builtin_roundf(v[4 * k + e] * id) << (8 * e);
-            packed[k] = (int32_t)word;
-        }
-        int4* dst = (int4*)(x.q + (size_t)n * in + i0);
-        dst[0] = make_int4(packed[0], packed[1], packed[2], packed[3]);
-        dst[1] = make_int4(packed[4], packed[5], packed[6], packed[7]);
-        x.d[(size_t)n * nb + lane] = h2f(f2h(d));
-    } else if (WT == T_F16) {
-#pragma unroll
-        for (int j = 0; j < 32; ++j) x.h[(size_t)n * in + i0 + j] = f2h(v[j]);
-    } else {
-#pragma unroll
-        for (int j = 0; j < 32; ++j) x.f[(size_t)n * in + i0 + j] = v[j];
-    }
+    return p;
+}
+__device__ __forceinline__ float dotr(const WUnit<T_F32>& w, const ActUnit<T_F32>& x, float p) {
+    p = __builtin_fmaf(w.a.x, x.a.x, p); p = __builtin_fmaf(w.a.y, x.a.y, p);
+    p = __builtin_fmaf(w.a.z, x.a.z, p); p = __builtin_fmaf(w.a.w, x.a.w, p);
+    p = __builtin_fmaf(w.b.x, x.b.x, p); p = __builtin_fmaf(w.b.y, x.b.y, p);
+    p = __builtin_fmaf(w.b.z, x.b.z, p); p = __builtin_fmaf(w.b.w, x.b.w, p);
+    return p;
 }
 
 template <int WT>
@@ -378,73 +371,228 @@ __host__ __device__ inline size_t lds_act_bytes(int wt, int ncol, int in) {
     return (size_t)ncol * in * 4;
 }
 
-// GEMV: y[col][r] = W[r] . act[col]. G lanes own a row (64/G rows per wave); lane t of a
-// row owns the row's partials p = t, t+G, ... (partial p accumulates units p, p+64, ... in
-// order), so the butterfly's levels off >= G fold inside the lane and only off < G cross
-// lanes -- one shuffle per level for all the wave's rows. LNP: the prologue builds the
-// activation in LDS (PRO_LN / PRO_F32); otherwise (PRO_ACT) every lane reads its units'
-// activation straight from global memory next to its weights.
-constexpr int GEMV_UMAX = 8;   // units per lane per pass
+// Sum of 256 per-thread partials red[0..255] in butterfly order (off 128 and 64 from LDS,
+// 32..1 in-wave); every wave computes it and every lane gets it.
+__device__ __forceinline__ double fold256(const double* red, int lane) {
+    const double r = (red[lane] + red[lane + 128]) + (red[lane + 64] + red[lane + 192]);
+    return fold64d_b(r);
+}
 
-template <int WT, int NC, int G, bool LNP>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
-    constexpr int M = 64 / G;        // partials per lane (and rows per wave)
-    extern __shared__ __align__(16) uint8_t lds[];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int t = lane % G, rl = lane / G;
-    const int in = a.w.in, out = a.w.out;
-    const int units = in / unit_elems<WT>();
-    const int row = (blockIdx.x * 4 + wave) * M + rl;
-    const bool live = row < out;
-    const int upl = t < units ? (units - t + G - 1) / G : 0;   // this lane's units t + G*i
-    LdsAct x;
-    if (LNP) {
-        x.in = in;
-        x.q = (int8_t*)lds;
-        x.d = (float*)(lds + (size_t)NC * in);
-        x.h = (uint16_t*)lds;
-        x.f = (float*)lds;
-    } else {
-        x.in = a.src.stride;
-        x.q = a.src.q; x.d = a.src.d; x.h = a.src.h; x.f = a.src.f;
-    }
-    float* tile = (float*)(lds + (LNP ? lds_act_bytes(WT, NC, in) : 0));   // GELU_ACT staging [NC][32]
-
-    float4 xv[8], wv[8], bv[8];
-    if (LNP) pro_load<WT>(a, wave, lane, xv, wv, bv);
-    WUnit<WT> cur[GEMV_UMAX];
-    if (live) {
+// LayerNorm (transformer.h:28-38) or plain conversion of NC f32 columns into the activation
+// form, in LDS, by the block's 256 threads. Thread i owns partial i: float4 groups i, i+256,
+// ... of each column, summed in element order in double; the 256 partials are folded by the
+// butterfly. Then (x - mean) * (1/sqrtf(var + eps)) * w + b per element, and quantization
+// (each 32-element block is 8 consecutive lanes).
+template <int WT, int NC, int KG, bool LN>
+__device__ __forceinline__ void prologue(const GemvArgs& a, const LdsAct& x, double* red, int tid, int lane,
+                                         const float4 (&xr)[NC][KG], const float4 (&wr)[KG], const float4 (&br)[KG]) {
+    const int in = a.w.in, nf = in / 4, nb = in / 32;
+    float4 u[NC][KG];
 #pragma unroll
-        for (int i = 0; i < GEMV_UMAX; ++i)
-            if (i < upl) cur[i].load(a.w, row, t + G * i);
+    for (int n = 0; n < NC; ++n)
+#pragma unroll
+        for (int j = 0; j < KG; ++j) u[n][j] = tid + 256 * j < nf ? xr[n][j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (LN) {
+        float mean[NC];
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            double s = 0.0;
+#pragma unroll
+            for (int j = 0; j < KG; ++j) {
+                s = s + (double)u[n][j].x; s = s + (double)u[n][j].y; s = s + (double)u[n][j].z; s = s + (double)u[n][j].w;
+            }
+            red[n * 256 + tid] = s;
+        }
+        lds_barrier();
+#pragma unroll
+        for (int n = 0; n < NC; ++n) mean[n] = (float)(fold256(red + n * 256, lane) / (double)in);
+        double* red2 = red + NC * 256;
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            double s2 = 0.0;
+#pragma unroll
+            for (int j = 0; j < KG; ++j) {
+                float4 d = u[n][j];
+                d.x = d.x - mean[n]; d.y = d.y - mean[n]; d.z = d.z - mean[n]; d.w = d.w - mean[n];
+                u[n][j] = d;
+                if (tid + 256 * j < nf) {
+                    s2 = s2 + (double)(d.x * d.x); s2 = s2 + (double)(d.y * d.y);
+                    s2 = s2 + (double)(d.z * d.z); s2 = s2 + (double)(d.w * d.w);
+                }
+            }
+            red2[n * 256 + tid] = s2;
+        }
+        lds_barrier();
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            const float var = (float)(fold256(red2 + n * 256, lane) / (double)in);
+            const float scale = 1.0f / __builtin_sqrtf(var + a.eps);
+#pragma unroll
+            for (int j = 0; j < KG; ++j) {
+                float4 t = u[n][j];
+                t.x = t.x * scale; t.y = t.y * scale; t.z = t.z * scale; t.w = t.w * scale;
+                t.x = t.x * wr[j].x; t.y = t.y * wr[j].y; t.z = t.z * wr[j].z; t.w = t.w * wr[j].w;
+                t.x = t.x + br[j].x; t.y = t.y + br[j].y; t.z = t.z + br[j].z; t.w = t.w + br[j].w;
+                u[n][j] = t;
+            }
+        }
     }
-    if (LNP) {
-        pro_store<WT>(a, x, wave, lane, xv, wv, bv);
-        __syncthreads();
+#pragma unroll
+    for (int n = 0; n < NC; ++n) {
+#pragma unroll
+        for (int j = 0; j < KG; ++j) {
+            const int f = tid + 256 * j;
+            const float4 t = u[n][j];
+            if (WT == T_Q8_0 || WT == T_Q4_0) {
+                float amax = __builtin_fabsf(t.x);
+                amax = amax > __builtin_fabsf(t.y) ? amax : __builtin_fabsf(t.y);
+                amax = amax > __builtin_fabsf(t.z) ? amax : __builtin_fabsf(t.z);
+                amax = amax > __builtin_fabsf(t.w) ? amax : __builtin_fabsf(t.w);
+                amax = grp8_bcast(grp8_max_to0(amax), lane);
+                const float d = amax / 127.0f;
+                const float id = d != 0.0f ? 1.0f / d : 0.0f;
+                const uint32_t word = (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.x * id)
+                                    | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.y * id) << 8
+                                    | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.z * id) << 16
+                                    | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.w * id) << 24;
+                if (f < nf) {
+                    *(uint32_t*)(x.q + (size_t)n * in + 4 * f) = word;
+                    if ((lane & 7) == 0) x.d[(size_t)n * nb + f / 8] = h2f(f2h(d));
+                }
+            } else if (WT == T_F16) {
+                if (f < nf) {
+                    const uint32_t lo = (uint32_t)f2h(t.x) | (uint32_t)f2h(t.y) << 16;
+                    const uint32_t hi = (uint32_t)f2h(t.z) | (uint32_t)f2h(t.w) << 16;
+                    *(uint2*)(x.h + (size_t)n * in + 4 * f) = make_uint2(lo, hi);
+                }
+            } else if (f < nf) {
+                *(float4*)(x.f + (size_t)n * in + 4 * f) = t;
+            }
+        }
     }
+}
+
+// U > 0: every lane owns exactly U units (units == G * U). U == 0: any unit count, a runtime
+// loop in passes of 8 units per lane (needs G == 8 so a pass covers each partial once).
+template <int WT, int NC, int G, int U, int PRO, int EPI, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
+    constexpr int M = 64 / G, R = WAVES * M, NT = 64 * WAVES;
+    constexpr int IN = U > 0 ? unit_elems<WT>() * G * U : 2048;   // prologue size bound
+    constexpr int KG = (IN + 1023) / 1024;
+    static_assert(PRO == PRO_ACT || WAVES == 4, "the prologue has 256 partials, one per thread");
+    static_assert(U > 0 || G == 8, "the runtime unit loop folds 8 units per lane per pass");
+    static_assert(EPI != EPI_GELU_ACT || R % 32 == 0, "GELU blocks quantize whole 32-row blocks");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int t = lane % G, rl = lane / G;
+    const int in = a.w.in, out = a.w.out, nb = in / 32, ncol = a.ncol;
+    const int row = blockIdx.x * R + wave * M + rl;
+    const int row_ld = row < out ? row : out - 1;
+    LdsAct x;
+    x.in = in;
+    x.q = (int8_t*)lds; x.d = (float*)(lds + (size_t)NC * in); x.h = (uint16_t*)lds; x.f = (float*)lds;
+    float* tile = (float*)(lds + lds_act_bytes(WT, NC, in));
+    double* red = (double*)(lds + lds_act_bytes(WT, NC, in) + (size_t)NC * R * 4);
+
+    // 1. activation source
+    float4 xr[NC][PRO == PRO_ACT ? 1 : KG], wr[PRO == PRO_ACT ? 1 : KG], br[PRO == PRO_ACT ? 1 : KG];
+    int4 ch[GEMV_KA];
+    int nchunks = 0, cq = 0;
+    if constexpr (PRO != PRO_ACT) {
+        const int nf = in / 4;
+#pragma unroll
+        for (int j = 0; j < KG; ++j) {
+            const int f = tid + 256 * j < nf ? tid + 256 * j : nf - 1;
+#pragma unroll
+            for (int n = 0; n < NC; ++n) xr[n][j] = ((const float4*)(a.x + (size_t)(n < ncol ? n : ncol - 1) * a.x_stride))[f];
+            if (PRO == PRO_LN) { wr[j] = ((const float4*)a.ln_w)[f]; br[j] = ((const float4*)a.ln_b)[f]; }
+        }
+    } else {
+        // the source columns are contiguous: q [col][in] (or h / f), then Q8 scales [col][in/32]
+        const size_t bq = (WT == T_Q8_0 || WT == T_Q4_0) ? (size_t)ncol * in
+                        : (size_t)ncol * in * (WT == T_F16 ? 2 : 4);
+        const size_t bd = (WT == T_Q8_0 || WT == T_Q4_0) ? (size_t)ncol * nb * 4 : 0;
+        cq = (int)(bq / 16);
+        nchunks = cq + (int)(bd / 16);
+        const int4* sq = (const int4*)((WT == T_Q8_0 || WT == T_Q4_0) ? (const void*)a.src.q
+                          : (WT == T_F16 ? (const void*)a.src.h : (const void*)a.src.f));
+        const int4* sd = (const int4*)a.src.d;
+#pragma unroll
+        for (int k = 0; k < GEMV_KA; ++k) {
+            int c = tid + NT * k;
+            c = c < nchunks ? c : nchunks - 1;
+            const int4* p = c < cq ? sq + c : sd + (c - cq);
+            ch[k] = *p;
+        }
+    }
+    if constexpr (PRO != PRO_ACT) __builtin_amdgcn_sched_barrier(0);
+    // 2. weights
+    WUnit<WT> w[U > 0 ? U : 1];
+    if constexpr (U > 0) {
+#pragma unroll
+        for (int i = 0; i < U; ++i) w[i].load(a.w, row_ld, t + G * i);
+    }
+    // 3. residual
+    float yo[NC];
+    if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+        for (int n = 0; n < NC; ++n) yo[n] = a.y[(size_t)(n < ncol ? n : ncol - 1) * a.y_stride + row_ld];
+    }
+    if constexpr (PRO != PRO_ACT) __builtin_amdgcn_sched_barrier(0);
+    // 4. activation -> LDS
+    if constexpr (PRO != PRO_ACT) {
+        prologue<WT, NC, KG, PRO == PRO_LN>(a, x, red, tid, lane, xr, wr, br);
+    } else {
+        // a clamped index loaded the last chunk, so its store rewrites that chunk's own bytes
+#pragma unroll
+        for (int k = 0; k < GEMV_KA; ++k) {
+            const int c = tid + NT * k;
+            ((int4*)lds)[c < nchunks ? c : nchunks - 1] = ch[k];
+        }
+        const int4* sq = (const int4*)((WT == T_Q8_0 || WT == T_Q4_0) ? (const void*)a.src.q
+                          : (WT == T_F16 ? (const void*)a.src.h : (const void*)a.src.f));
+        for (int c = tid + NT * GEMV_KA; c < nchunks; c += NT)
+            ((int4*)lds)[c] = c < cq ? sq[c] : ((const int4*)a.src.d)[c - cq];
+    }
+    lds_barrier();
+    // 5. dots
     float acc[NC][M];
 #pragma unroll
     for (int n = 0; n < NC; ++n)
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[n][m] = 0.0f;
-    if (live) {
-        for (int base = 0; base < upl; base += GEMV_UMAX) {
-            if (base > 0) {
+    if constexpr (U > 0) {
 #pragma unroll
-                for (int i = 0; i < GEMV_UMAX; ++i)
-                    if (base + i < upl) cur[i].load(a.w, row, t + G * (base + i));
+        for (int i = 0; i < U; ++i) {
+            ActUnit<WT> xa[NC];
+#pragma unroll
+            for (int n = 0; n < NC; ++n) xa[n].load(x, n, t + G * i);
+#pragma unroll
+            for (int n = 0; n < NC; ++n) acc[n][i % M] = dotr(w[i], xa[n], acc[n][i % M]);
+        }
+    } else {
+        const int units = in / unit_elems<WT>();
+        const int upl = t < units ? (units - t + G - 1) / G : 0;   // units t + G*i of this lane
+        for (int i0 = 0; i0 < upl; i0 += M) {
+            WUnit<WT> wp[M];
+#pragma unroll
+            for (int ii = 0; ii < M; ++ii) {
+                const int i = i0 + ii < upl ? i0 + ii : upl - 1;
+                wp[ii].load(a.w, row_ld, t + G * i);
             }
 #pragma unroll
-            for (int i = 0; i < GEMV_UMAX; ++i) {
-                if (base + i >= upl) break;
-                const int u = t + G * (base + i);
+            for (int ii = 0; ii < M; ++ii) {
+                if (i0 + ii >= upl) break;
+                const int u = t + G * (i0 + ii);
 #pragma unroll
-                for (int n = 0; n < NC; ++n)
-                    if (n < a.ncol) acc[n][i % M] = cur[i].dot(x, n, u, acc[n][i % M]);
+                for (int n = 0; n < NC; ++n) {
+                    ActUnit<WT> xa;
+                    xa.load(x, n, u);
+                    acc[n][ii] = dotr(wp[ii], xa, acc[n][ii]);
+                }
             }
         }
     }
-    // butterfly: levels off >= G inside the lane, off < G across the row's lanes
     float v[NC];
 #pragma unroll
     for (int n = 0; n < NC; ++n) {
@@ -452,53 +600,49 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
         for (int h = M / 2; h >= 1; h >>= 1)
 #pragma unroll
             for (int m = 0; m < h; ++m) acc[n][m] = acc[n][m] + acc[n][m + h];
-        float r = acc[n][0];
-#pragma unroll
-        for (int off = G / 2; off >= 1; off >>= 1) r = r + shfl_xor(r, off);
-        v[n] = r;
+        v[n] = fold_to0<G>(acc[n][0]);
     }
-
-    if (a.epi == EPI_GELU_ACT) {
-        // the block's 32 rows (G = 8) -> GELU -> LDS tile -> activation form
+    // 6. epilogue: lane 0 of each row group holds every column's value
+    if constexpr (EPI == EPI_GELU_ACT) {
+        // the block's R rows -> GELU -> LDS tile -> activation form, one 32-row block per wave pass
         const int rb = wave * M + rl;
+        if (t == 0) {
 #pragma unroll
-        for (int n = 0; n < NC; ++n)
-            if (t == n && n < a.ncol) tile[n * 32 + rb] = gelu_erf(v[n]);
-        __syncthreads();
-        const int base = blockIdx.x * 32;
-        if (wave == 0) {
-            for (int n = 0; n < a.ncol; ++n) {
-                const float g = lane < 32 ? tile[n * 32 + lane] : 0.0f;
-                const ActBuf& d = a.dst;
-                if (d.kind == ACT_Q8) {
-                    int8_t qv;
-                    float dv;
-                    quant_q8_lane(g, lane, &qv, &dv);
-                    if (lane < 32) {
-                        d.q[(size_t)n * d.stride + base + lane] = qv;
-                        if (lane == 0) d.d[(size_t)n * (d.stride / 32) + base / 32] = dv;
-                    }
-                } else if (lane < 32) {
-                    if (d.kind == ACT_F16) d.h[(size_t)n * d.stride + base + lane] = f2h(g);
-                    else d.f[(size_t)n * d.stride + base + lane] = g;
+            for (int n = 0; n < NC; ++n) tile[n * R + rb] = gelu_erf(v[n]);
+        }
+        lds_barrier();
+        const ActBuf& d = a.dst;
+        const int base = blockIdx.x * R;
+        for (int pr = wave; pr < ncol * (R / 32); pr += WAVES) {
+            const int n = pr / (R / 32), bk = pr % (R / 32);
+            const float g = lane < 32 ? tile[n * R + bk * 32 + lane] : 0.0f;
+            const int o = base + bk * 32 + lane;
+            if (d.kind == ACT_Q8) {
+                int8_t qv;
+                float dv;
+                quant_q8_lane(g, lane, &qv, &dv);
+                if (lane < 32) {
+                    d.q[(size_t)n * d.stride + o] = qv;
+                    if (lane == 0) d.d[(size_t)n * (d.stride / 32) + o / 32] = dv;
                 }
+            } else if (lane < 32) {
+                if (d.kind == ACT_F16) d.h[(size_t)n * d.stride + o] = f2h(g);
+                else d.f[(size_t)n * d.stride + o] = g;
             }
         }
         return;
     }
-    if (!live) return;
+    if (row >= out || t != 0) return;
 #pragma unroll
     for (int n = 0; n < NC; ++n) {
-        if (t != n || n >= a.ncol) continue;
+        if (n >= ncol) break;
         const float r = v[n];
-        if (a.epi == EPI_STORE) a.y[(size_t)n * a.y_stride + row] = r;
-        else if (a.epi == EPI_RESID) {
-            float* p = a.y + (size_t)n * a.y_stride + row;
-            *p = *p + r;
-        } else {
-            const int sec = row / a.dim, w = row - sec * a.dim, head = w >> 6, dim = w & 63;
-            if (sec == 0) a.y[(size_t)n * a.dim + w] = r;
-            else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + *a.pos) * 64 + dim] = r;
+        if (EPI == EPI_STORE) a.y[(size_t)n * a.y_stride + row] = r;
+        else if (EPI == EPI_RESID) a.y[(size_t)n * a.y_stride + row] = yo[n] + r;
+        else {
+            const int sec = row / a.dim, wi = row - sec * a.dim, head = wi >> 6, dm = wi & 63;
+            if (sec == 0) a.y[(size_t)n * a.dim + wi] = r;
+            else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + *a.pos) * 64 + dm] = r;
         }
     }
 }
@@ -1066,44 +1210,83 @@ void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s) {
     hipLaunchKernelGGL(k_add_bias, dim3((n * ncol + 255) / 256), dim3(256), 0, s, y, b, n, ncol);
 }
 
-// Lanes per row: 8 for the GELU epilogue (32-row blocks quantize inside one workgroup);
-// otherwise the fewest lanes that keep a lane's units within one pass and give >= 160
-// workgroups.
-static int lanes_per_row(const GemvArgs& a) {
-    const int units = a.w.in / ((a.w.type == T_Q8_0 || a.w.type == T_Q4_0) ? 32 : 8);
-    if (a.epi == EPI_GELU_ACT) return 8;
-    for (int G = 16; G < 64; G *= 2)
-        if ((units + G - 1) / G <= GEMV_UMAX && (long)a.w.out * G / 256 >= 160) return G;
-    return 64;
+// ---- GEMV launch: kernel choice by weight type, prologue / epilogue kind and unit count
+template <int WT, int NC, int G, int U, int PRO, int EPI, int W>
+static void gemv_go(const GemvArgs& a, hipStream_t s) {
+    constexpr int R = W * (64 / G);
+    const size_t lds = lds_act_bytes(WT, NC, a.w.in) + (size_t)NC * R * 4 + (PRO == PRO_ACT ? 0 : (size_t)NC * 2 * 256 * 8);
+    hipLaunchKernelGGL((k_gemv<WT, NC, G, U, PRO, EPI, W>), dim3((a.w.out + R - 1) / R), dim3(64 * W), lds, s, a);
 }
 
-template <int WT, int NC, bool LNP> static void gemv_wt_nc_p(const GemvArgs& a, hipStream_t s) {
-    const int G = lanes_per_row(a);
-    const size_t lds = (LNP ? lds_act_bytes(WT, NC, a.w.in) : 0) + (size_t)NC * 32 * sizeof(float);
-    const int rows_per_block = 256 / G;
-    const dim3 grid((a.w.out + rows_per_block - 1) / rows_per_block), block(256);
-    switch (G) {
-    case 8: hipLaunchKernelGGL((k_gemv<WT, NC, 8, LNP>), grid, block, lds, s, a); break;
-    case 16: hipLaunchKernelGGL((k_gemv<WT, NC, 16, LNP>), grid, block, lds, s, a); break;
-    case 32: hipLaunchKernelGGL((k_gemv<WT, NC, 32, LNP>), grid, block, lds, s, a); break;
-    default: hipLaunchKernelGGL((k_gemv<WT, NC, 64, LNP>), grid, block, lds, s, a); break;
+// Tries (G, U, W) = the listed shapes whose G * U matches the row's unit count; else the
+// runtime-loop kernel.
+#define GEMV_TRY(G_, U_, W_) if (units == (G_) * (U_)) return gemv_go<WT, NC, G_, U_, PRO, EPI, W_>(a, s)
+template <int WT, int NC, int PRO, int EPI> static void gemv_pick(const GemvArgs& a, hipStream_t s) {
+    const int units = a.w.in / unit_elems<WT>();
+    if constexpr (PRO == PRO_ACT) {
+        if constexpr (WT == T_Q8_0 || WT == T_Q4_0) {
+            GEMV_TRY(8, 4, 2); GEMV_TRY(8, 6, 2); GEMV_TRY(8, 8, 2);         // in = dim 1024 / 1536 / 2048
+            GEMV_TRY(32, 4, 4); GEMV_TRY(32, 6, 4); GEMV_TRY(32, 8, 4);      // in = ff 4096 / 6144 / 8192
+            GEMV_TRY(8, 2, 2);                                               // in = 512
+        } else if constexpr (WT == T_F16) {
+            GEMV_TRY(8, 16, 2); GEMV_TRY(64, 8, 4); GEMV_TRY(8, 2, 2); GEMV_TRY(8, 8, 2);
+        } else {
+            GEMV_TRY(8, 2, 2); GEMV_TRY(8, 8, 2);
+        }
+    } else if constexpr (PRO == PRO_LN) {
+        if constexpr (WT == T_Q8_0 || WT == T_Q4_0) {
+            GEMV_TRY(8, 4, 4); GEMV_TRY(8, 6, 4); GEMV_TRY(8, 8, 4);
+        } else if constexpr (WT == T_F16) {
+            GEMV_TRY(8, 16, 4); GEMV_TRY(8, 2, 4);
+        } else {
+            GEMV_TRY(8, 2, 4);
+        }
     }
+    gemv_go<WT, NC, 8, 0, PRO, EPI, 4>(a, s);
 }
-template <int WT, int NC> static void gemv_wt_nc(const GemvArgs& a, hipStream_t s) {
-    if (a.pro == PRO_ACT) gemv_wt_nc_p<WT, NC, false>(a, s);
-    else gemv_wt_nc_p<WT, NC, true>(a, s);
+#undef GEMV_TRY
+
+template <int WT, int NC> static void gemv_nc(const GemvArgs& a, hipStream_t s) {
+    if (a.pro == PRO_ACT) gemv_pick<WT, NC, PRO_ACT, EPI_RESID>(a, s);   // every PRO_ACT site adds the residual
+    else if (a.pro == PRO_F32) gemv_pick<WT, NC, PRO_F32, EPI_STORE>(a, s);
+    else if (a.epi == EPI_QKV) gemv_pick<WT, NC, PRO_LN, EPI_QKV>(a, s);
+    else if (a.epi == EPI_GELU_ACT) gemv_pick<WT, NC, PRO_LN, EPI_GELU_ACT>(a, s);
+    else gemv_pick<WT, NC, PRO_LN, EPI_STORE>(a, s);
 }
 template <int WT> static void gemv_wt(const GemvArgs& a, hipStream_t s) {
-    if (a.ncol <= 1) gemv_wt_nc<WT, 1>(a, s);
-    else if (a.ncol <= 2) gemv_wt_nc<WT, 2>(a, s);
-    else gemv_wt_nc<WT, 4>(a, s);
+    if (a.ncol == 1) gemv_nc<WT, 1>(a, s);
+    else gemv_nc<WT, 2>(a, s);
 }
-void launch_gemv(const GemvArgs& a, hipStream_t s) {
-    switch (a.w.type) {
-    case T_Q8_0: gemv_wt<T_Q8_0>(a, s); break;
-    case T_Q4_0: gemv_wt<T_Q4_0>(a, s); break;
-    case T_F16: gemv_wt<T_F16>(a, s); break;
-    default: gemv_wt<T_F32>(a, s); break;
+
+// Columns go in groups of two (every per-column pointer advanced by the group's offset).
+void launch_gemv(const GemvArgs& a0, hipStream_t s) {
+    for (int c0 = 0; c0 < a0.ncol; c0 += 2) {
+        GemvArgs a = a0;
+        a.ncol = a0.ncol - c0 < 2 ? a0.ncol - c0 : 2;
+        if (c0) {
+            a.x = a0.x ? a0.x + (size_t)c0 * a0.x_stride : nullptr;
+            const auto adv = [c0](ActBuf& b) {
+                if (b.q) b.q += (size_t)c0 * b.stride;
+                if (b.d) b.d += (size_t)c0 * (b.stride / 32);
+                if (b.h) b.h += (size_t)c0 * b.stride;
+                if (b.f) b.f += (size_t)c0 * b.stride;
+            };
+            adv(a.src);
+            adv(a.dst);
+            if (a0.epi == EPI_QKV) {
+                a.y = a0.y + (size_t)c0 * a0.dim;
+                a.k = a0.k + (size_t)c0 * a0.heads * a0.cap * 64;
+                a.v = a0.v + (size_t)c0 * a0.heads * a0.cap * 64;
+            } else if (a0.y) {
+                a.y = a0.y + (size_t)c0 * a0.y_stride;
+            }
+        }
+        switch (a.w.type) {
+        case T_Q8_0: gemv_wt<T_Q8_0>(a, s); break;
+        case T_Q4_0: gemv_wt<T_Q4_0>(a, s); break;
+        case T_F16: gemv_wt<T_F16>(a, s); break;
+        default: gemv_wt<T_F32>(a, s); break;
+        }
     }
 }
 void launch_attention(const AttnArgs& a, hipStream_t s) {

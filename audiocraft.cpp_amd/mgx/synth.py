@@ -18,6 +18,10 @@ SYNTH_PATH = os.path.join(os.path.dirname(_HERE), "libmgx_synth.so")
 # MusicGen LM shapes (hd 64, n_q 4, card 2048, T5-base memory width 768) plus a tiny one.
 SHAPES = {
     "tiny": dict(dim=128, layers=2, heads=2, ff_dim=512, card=256, n_ctx=5),
+    # one or two layers at the real widths: the GEMV shapes of the small / medium / large LMs
+    "mini1024": dict(dim=1024, layers=2, heads=16, ff_dim=4096, card=256, n_ctx=6),
+    "mini1536": dict(dim=1536, layers=1, heads=24, ff_dim=6144, card=256, n_ctx=7),
+    "mini2048": dict(dim=2048, layers=1, heads=32, ff_dim=8192, card=256, n_ctx=9),
     "small": dict(dim=1024, layers=24, heads=16, ff_dim=4096, card=2048, n_ctx=12),
     "medium": dict(dim=1536, layers=48, heads=24, ff_dim=6144, card=2048, n_ctx=24),
     "large": dict(dim=2048, layers=48, heads=32, ff_dim=8192, card=2048, n_ctx=32),

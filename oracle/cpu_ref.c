@@ -38,9 +38,9 @@
  *   mul_mat, F16 weights: the activation is rounded to fp16 (RNE); products are exact in
  *     f32; 8-element chunks, chunk c -> partial c mod 64, fmaf in increasing element
  *     order inside a partial, same butterfly. F32 weights: same, without the rounding.
- *   norm: mean and variance as double sums, element i -> partial (i/32) mod 64 accumulated
- *     in increasing i, folded by the same butterfly; result (x - mean) * (1.0f / sqrtf(var +
- *     eps)), then * w, then + b, each rounded in f32.
+ *   norm: mean and variance as double sums, element i -> partial (i/4) mod 256 accumulated
+ *     in increasing i, folded by a 256-wide butterfly (off = 128,..,1); result (x - mean) *
+ *     (1.0f / sqrtf(var + eps)), then * w, then + b, each rounded in f32.
  *   soft_max_ext: x*scale (+mask); max; e = expf(x - max); sum of e in double over chunks
  *     of 256 keys (butterfly inside a chunk, chunks added in order); p = e * (float)(1/sum).
  *   attention matmuls (f32 x f32): q.k as 16 partials (dim i -> partial (i/4) mod 16,
@@ -433,17 +433,17 @@ static void matmul(const mat_t* W, const adapter_t* ad, const float* X, int ncol
 /* layer norm (transformer.h:28-38)                                                     */
 /* ------------------------------------------------------------------------------------ */
 REF_API void ref_layer_norm(const float* x, int n, const float* w, const float* b, float eps, float* y) {
-    double part[64];
-    for (int l = 0; l < 64; ++l) part[l] = 0.0;
-    for (int i = 0; i < n; ++i) part[(i >> 5) & 63] = part[(i >> 5) & 63] + (double)x[i];
-    const float mean = (float)(fold_d(part, 64) / (double)n);
-    for (int l = 0; l < 64; ++l) part[l] = 0.0;
+    double part[256];
+    for (int l = 0; l < 256; ++l) part[l] = 0.0;
+    for (int i = 0; i < n; ++i) part[(i >> 2) & 255] = part[(i >> 2) & 255] + (double)x[i];
+    const float mean = (float)(fold_d(part, 256) / (double)n);
+    for (int l = 0; l < 256; ++l) part[l] = 0.0;
     for (int i = 0; i < n; ++i) {
         const float v = x[i] - mean;
         y[i] = v;
-        part[(i >> 5) & 63] = part[(i >> 5) & 63] + (double)(v * v);
+        part[(i >> 2) & 255] = part[(i >> 2) & 255] + (double)(v * v);
     }
-    const float var = (float)(fold_d(part, 64) / (double)n);
+    const float var = (float)(fold_d(part, 256) / (double)n);
     const float scale = 1.0f / sqrtf(var + eps);
     for (int i = 0; i < n; ++i) {
         float v = y[i] * scale;
@@ -1148,7 +1148,7 @@ REF_API int ref_generate(const ref_model* m, const float* t5_hidden, int n_ctx, 
 }
 
 /* Bumped whenever a documented reduction order changes; fixtures record it. */
-REF_API int ref_convention(void) { return 2; }
+REF_API int ref_convention(void) { return 3; }
 
 REF_API void ref_set_threads(int n) {
 #ifdef _OPENMP

@@ -33,3 +33,42 @@ def test_tiny_forward_matches_oracle(mgx, wtype):
         want = rd.forward(ids[:, t:t + 1])
         assert np.array_equal(got, want), f"step {t}: max {np.abs(got - want).max()}"
     assert gs.used() == 12 and gs.forwards() == 5
+
+
+@pytest.mark.parametrize("shape,wtype", [("mini1024", 8), ("mini1024", 2), ("mini1024", 1), ("mini1536", 8),
+                                         ("mini2048", 2), ("mini2048", 8)])
+@pytest.mark.parametrize("n_seq", [1, 2, 3])
+def test_width_forward_matches_oracle(mgx, shape, wtype, n_seq):
+    """The specialised GEMV shapes (dims 1024 / 1536 / 2048, ff 4x) and the column groups."""
+    from oracle import cpu_ref as R
+    m = H.model(shape, wtype, 4)
+    c = m.config
+    from mgx import synth
+    t5 = H.memory(5, synth.SHAPES[shape]["n_ctx"])
+    ids = H.codes(6, 4, 6, c.card)
+    gm = mgx.Model(c, m.tensors)
+    gs = mgx.Stream(gm, 16, n_seq, t5, True)
+    rd = R.RefDecoder(H.ref_model(shape, wtype, 4), 16, n_seq, t5, True)
+    print(f"{shape} wtype={wtype} n_seq={n_seq}: prefill 4 then 2 steps", flush=True)
+    got = gs.forward(ids[:, :4])
+    want = rd.forward(ids[:, :4])
+    assert np.array_equal(got, want), f"prefill logits differ: max {np.abs(got - want).max()}"
+    for t in range(4, 6):
+        got = gs.forward(ids[:, t:t + 1])
+        want = rd.forward(ids[:, t:t + 1])
+        assert np.array_equal(got, want), f"step {t}: max {np.abs(got - want).max()}"
+
+
+def test_many_streams_forward_matches_oracle(mgx):
+    """Five streams: column groups 2 + 2 + 1 in every projection."""
+    from oracle import cpu_ref as R
+    m = H.model("tiny", 8, 3)
+    c = m.config
+    t5 = H.memory(1, 5)
+    ids = H.codes(7, 4, 6, c.card)
+    gs = mgx.Stream(mgx.Model(c, m.tensors), 16, 5, t5, True)
+    rd = R.RefDecoder(H.ref_model("tiny", 8, 3), 16, 5, t5, True)
+    print("tiny 5 streams", flush=True)
+    assert np.array_equal(gs.forward(ids[:, :4]), rd.forward(ids[:, :4]))
+    for t in range(4, 6):
+        assert np.array_equal(gs.forward(ids[:, t:t + 1]), rd.forward(ids[:, t:t + 1]))
