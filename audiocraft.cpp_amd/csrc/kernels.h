@@ -15,6 +15,8 @@ enum { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GELU_ACT = 3 };
 
 constexpr int ATT_CHUNK = 256;   // keys per attention chunk (fixes the reduction order)
 constexpr int ATT_MAX_CHUNKS = 16;  // capacity up to 4096 positions
+constexpr int ATT_SUB = 64;         // keys per score block
+constexpr int ATT_SUBS = ATT_CHUNK / ATT_SUB;
 constexpr int MAX_CARD = 2048;   // sampler's LDS rows
 
 // A weight matrix in device layout: `out` rows of `in`. Q8_0: int8 q[out][in] + fp16
@@ -71,7 +73,7 @@ struct AttnArgs {
     const float* v;       // [col][heads][cap][64]
     float* scores;        // [col][heads][cap]
     float* opart;         // [col][heads][max_chunks][64]
-    float* cmax;          // [col][heads][max_chunks]
+    float* cmax;          // [col][heads][max_chunks * ATT_SUBS] score-block maxima
     int dim, heads, cap, max_chunks, ncol;
     float scale;
     const int* pos;       // device position: keys [0, pos]
@@ -106,7 +108,8 @@ struct SampleArgs {
 
 void launch_embed(const EmbedArgs& a, hipStream_t s);
 void launch_gemv(const GemvArgs& a, hipStream_t s);
-void launch_attention(const AttnArgs& a, hipStream_t s);
+// nch: the 256-key chunks of the position the launch runs at (the grid covers exactly these)
+void launch_attention(const AttnArgs& a, int nch, hipStream_t s);
 void launch_xattn(const XAttnArgs& a, int heads, hipStream_t s);
 void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s);
 void launch_xkv_split(const float* kv, int n_ctx, int dim, float* k, float* v, hipStream_t s);

@@ -91,9 +91,11 @@ __device__ double derf(double x) {
     return x > 0 ? r : -r;
 }
 
-// ggml_gelu_erf: 0.5*x*(1+erf(x/sqrt 2)) in f32 (lm.h:203).
+// ggml_gelu_erf: 0.5*x*(1+erf(x/sqrt 2)) in f32 (lm.h:203). For |a| >= 4, 1 - |erf(a)| <
+// 1.6e-8 is below half an ulp of 1.0f, so the f32 erf is exactly +-1 and derf is skipped.
 __device__ __forceinline__ float gelu_erf(float x) {
-    const float e = (float)derf((double)(x * 0.70710678118654752440f));
+    const float a = x * 0.70710678118654752440f;
+    const float e = __builtin_fabsf(a) >= 4.0f ? (a > 0.0f ? 1.0f : -1.0f) : (float)derf((double)a);
     return 0.5f * x * (1.0f + e);
 }
 
@@ -604,12 +606,17 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
     }
     // 6. epilogue: lane 0 of each row group holds every column's value
     if constexpr (EPI == EPI_GELU_ACT) {
-        // the block's R rows -> GELU -> LDS tile -> activation form, one 32-row block per wave pass
+        // the block's R rows -> LDS tile -> GELU (one value per lane, spread over the waves)
+        // -> activation form, one 32-row block per wave pass
         const int rb = wave * M + rl;
         if (t == 0) {
 #pragma unroll
-            for (int n = 0; n < NC; ++n) tile[n * R + rb] = gelu_erf(v[n]);
+            for (int n = 0; n < NC; ++n) tile[n * R + rb] = v[n];
         }
+        lds_barrier();
+        constexpr int STRIDE = NT / (NC * R) > 0 ? NT / (NC * R) : 1;
+        for (int i = tid; i < NC * R * STRIDE; i += NT)
+            if (i % STRIDE == 0) tile[i / STRIDE] = gelu_erf(tile[i / STRIDE]);
         lds_barrier();
         const ActBuf& d = a.dst;
         const int base = blockIdx.x * R;
@@ -680,149 +687,135 @@ __device__ __forceinline__ float halving16(float (&p)[16], int t) {
     return (lo ? c[0] : c[1]) + recv;
 }
 
-// Scores of one 256-key chunk (16 lanes per key, four dims each) and the chunk's max.
+// Sum over the 16 lanes of a lane group of 4 values per lane: levels 8 and 4 halve the values,
+// 2 and 1 add in place. Lane t ends with value 2*((t>>3)&1) + ((t>>2)&1); each value's
+// additions follow the butterfly p[l] + p[l+off], off = 8, 4, 2, 1.
+__device__ __forceinline__ float halving4(const float (&p)[4], int t) {
+    const bool lo8 = (t & 8) == 0;
+    const float a0 = (lo8 ? p[0] : p[2]) + shfl_xor(lo8 ? p[2] : p[0], 8);
+    const float a1 = (lo8 ? p[1] : p[3]) + shfl_xor(lo8 ? p[3] : p[1], 8);
+    const bool lo4 = (t & 4) == 0;
+    float b = (lo4 ? a0 : a1) + shfl_xor(lo4 ? a1 : a0, 4);
+    b = b + shfl_xor(b, 2);
+    return b + shfl_xor(b, 1);
+}
+
+// Scores of one 64-key block (16 lanes per key, four dims each; 16 keys per pass) and the
+// block's max (-inf when it holds no key yet), into cmax[head][block].
 __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
-    const int c = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
+    const int b = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
     const int u = *a.pos + 1;
-    if (c * ATT_CHUNK >= u) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, t = lane & 15;
     const size_t head = (size_t)n * a.heads + h;
     const float* K = a.k + head * a.cap * 64;
     float* S = a.scores + head * a.cap;
     __shared__ float red_f[4];
     const float4 q = ((const float4*)(a.q + (size_t)n * a.dim + h * 64))[t];
-    float4 kv[16];
+    float4 kv[4];
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
-        const int j = c * ATT_CHUNK + it * 16 + wave * 4 + g;
-        kv[it] = j < u ? ((const float4*)(K + (size_t)j * 64))[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int it = 0; it < 4; ++it) {
+        const int j = b * ATT_SUB + it * 16 + wave * 4 + g;
+        kv[it] = ((const float4*)(K + (size_t)(j < u ? j : u - 1) * 64))[t];
     }
-    float p[16];
+    float p[4];
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
+    for (int it = 0; it < 4; ++it) {
         float v = __builtin_fmaf(q.x, kv[it].x, 0.0f);
         v = __builtin_fmaf(q.y, kv[it].y, v);
         v = __builtin_fmaf(q.z, kv[it].z, v);
         p[it] = __builtin_fmaf(q.w, kv[it].w, v);
     }
-    const int jt = c * ATT_CHUNK + t * 16 + wave * 4 + g;   // lane t now holds key jt
-    const float sc = halving16(p, t) * a.scale;
+    const int jt = b * ATT_SUB + (2 * ((t >> 3) & 1) + ((t >> 2) & 1)) * 16 + wave * 4 + g;
+    const float sc = halving4(p, t) * a.scale;
     float mx = -__builtin_inff();
-    if (jt < u) { S[jt] = sc; mx = sc; }
+    if (jt < u) {
+        if ((t & 3) == 0) S[jt] = sc;
+        mx = sc;
+    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(mx, off); mx = mx > o ? mx : o; }
     if (lane == 0) red_f[wave] = mx;
-    __syncthreads();
+    lds_barrier();
     if (tid == 0) {
         float m = red_f[0];
         for (int w = 1; w < 4; ++w) m = m > red_f[w] ? m : red_f[w];
-        a.cmax[head * a.max_chunks + c] = m;
+        a.cmax[head * a.max_chunks * ATT_SUBS + b] = m;
     }
 }
 
-// Softmax of one head's scores into probabilities: global max, exps, chunk sums in double
-// (butterfly over each chunk's 256 keys), chunks added in order, p = e * (float)(1/sum).
-__global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
-    const int h = blockIdx.x, n = blockIdx.y;
-    const int tid = threadIdx.x;
-    const int u = *a.pos + 1, nch = (u + ATT_CHUNK - 1) / ATT_CHUNK;
-    const size_t head = (size_t)n * a.heads + h;
-    float* S = a.scores + head * a.cap;
-    __shared__ double red_d[ATT_MAX_CHUNKS][128];
-    __shared__ double csum[ATT_MAX_CHUNKS];
-    __shared__ float inv_sh;
-    float s[ATT_MAX_CHUNKS];
-#pragma unroll
-    for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc) {
-        const int j = cc * ATT_CHUNK + tid;
-        s[cc] = (cc < nch && j < u) ? S[j] : 0.0f;
-    }
-    float M = a.cmax[head * a.max_chunks];
-    for (int cc = 1; cc < nch; ++cc) { const float o = a.cmax[head * a.max_chunks + cc]; M = M > o ? M : o; }
-    float e[ATT_MAX_CHUNKS];
-#pragma unroll
-    for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc) {
-        const int j = cc * ATT_CHUNK + tid;
-        e[cc] = (cc < nch && j < u) ? dexpf(s[cc] - M) : 0.0f;
-    }
-    // every chunk's 256-key butterfly at once: off 128 through LDS, 64..1 in wave 0
-#pragma unroll
-    for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc)
-        if (cc < nch && tid >= 128) red_d[cc][tid - 128] = (double)e[cc];
-    __syncthreads();
-    if (tid < 128) {
-#pragma unroll
-        for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc)
-            if (cc < nch) red_d[cc][tid] = (double)e[cc] + red_d[cc][tid];
-    }
-    __syncthreads();
-    if (tid < 64) {
-        for (int cc = 0; cc < nch; ++cc) {
-            double v = red_d[cc][tid] + red_d[cc][tid + 64];
-            v = fold64d(v);
-            if (tid == 0) csum[cc] = v;
-        }
-        if (tid == 0) {
-            double total = 0.0;
-            for (int cc = 0; cc < nch; ++cc) total = total + csum[cc];
-            inv_sh = (float)(1.0 / total);
-        }
-    }
-    __syncthreads();
-    const float inv = inv_sh;
-#pragma unroll
-    for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc) {
-        const int j = cc * ATT_CHUNK + tid;
-        if (cc < nch && j < u) S[j] = e[cc] * inv;
-    }
-}
-
-// This chunk's share of V^T p: partial g = key mod 16 (g = 4*wave + lane/16), lane%16 ->
-// dims 4*(lane%16)..+3, keys in increasing order, then the 16 partials folded.
-__global__ __launch_bounds__(256) void k_attn_v(AttnArgs a) {
+// Softmax + this chunk's share of V^T p, one block per (chunk, head, stream); NCH = the
+// position's chunk count. Every block rebuilds the head's normalizer: global max from the
+// block maxima, e = expf(s - max) for every key, per-chunk double sums in the 256-key
+// butterfly, chunks added in order, p = e * (float)(1/sum). V partials: partial g = key mod
+// 16 (g = 4*wave + lane/16), lane%16 -> dims 4*(lane%16)..+3, keys in increasing order, then
+// the 16 partials folded. Every load is issued before the first use.
+template <int NCH>
+__global__ __launch_bounds__(256) void k_attn_pv(AttnArgs a) {
     const int c = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
     const int u = *a.pos + 1;
-    if (c * ATT_CHUNK >= u) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const size_t head = (size_t)n * a.heads + h;
-    const float* P = a.scores + head * a.cap;
+    const float* S = a.scores + head * a.cap;
+    __shared__ float el[NCH][ATT_CHUNK];
     __shared__ float4 vred[16][16];
+    float s[NCH];
+#pragma unroll
+    for (int cc = 0; cc < NCH; ++cc) {
+        const int j = cc * ATT_CHUNK + tid;
+        s[cc] = S[j < u ? j : u - 1];
+    }
+    float cm[NCH * ATT_SUBS];
+#pragma unroll
+    for (int i = 0; i < NCH * ATT_SUBS; ++i) cm[i] = a.cmax[head * a.max_chunks * ATT_SUBS + i];
     const int g = wave * 4 + (lane >> 4), dq = lane & 15;
     const float* V = a.v + head * a.cap * 64;
     float4 vv[16];
-    float pp[16];
 #pragma unroll
     for (int m = 0; m < 16; ++m) {
         const int j = c * ATT_CHUNK + g + 16 * m;
-        const bool in = j < u;
-        vv[m] = in ? ((const float4*)(V + (size_t)j * 64))[dq] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        pp[m] = in ? P[j] : 0.0f;
+        vv[m] = ((const float4*)(V + (size_t)(j < u ? j : u - 1) * 64))[dq];
     }
+    float M = cm[0];
+#pragma unroll
+    for (int i = 1; i < NCH * ATT_SUBS; ++i) M = M > cm[i] ? M : cm[i];
+#pragma unroll
+    for (int cc = 0; cc < NCH; ++cc) el[cc][tid] = cc * ATT_CHUNK + tid < u ? dexpf(s[cc] - M) : 0.0f;
+    lds_barrier();
+    // every wave folds every chunk (off 128, 64 from LDS, 32..1 in-wave) and adds them in order
+    double cs[NCH];
+#pragma unroll
+    for (int cc = 0; cc < NCH; ++cc)
+        cs[cc] = fold64d_b(((double)el[cc][lane] + (double)el[cc][lane + 128]) + ((double)el[cc][lane + 64] + (double)el[cc][lane + 192]));
+    double total = 0.0;
+#pragma unroll
+    for (int cc = 0; cc < NCH; ++cc) total = total + cs[cc];
+    const float inv = (float)(1.0 / total);
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int m = 0; m < 16; ++m) {
-        if (c * ATT_CHUNK + g + 16 * m < u) {
-            acc.x = __builtin_fmaf(pp[m], vv[m].x, acc.x);
-            acc.y = __builtin_fmaf(pp[m], vv[m].y, acc.y);
-            acc.z = __builtin_fmaf(pp[m], vv[m].z, acc.z);
-            acc.w = __builtin_fmaf(pp[m], vv[m].w, acc.w);
+        const int jj = g + 16 * m;
+        if (c * ATT_CHUNK + jj < u) {
+            const float pm = el[c][jj] * inv;
+            acc.x = __builtin_fmaf(pm, vv[m].x, acc.x);
+            acc.y = __builtin_fmaf(pm, vv[m].y, acc.y);
+            acc.z = __builtin_fmaf(pm, vv[m].z, acc.z);
+            acc.w = __builtin_fmaf(pm, vv[m].w, acc.w);
         }
     }
     vred[g][dq] = acc;
-    __syncthreads();
+    lds_barrier();
     if (g < 8) {
         const float4 o = vred[g + 8][dq];
         vred[g][dq] = make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
     }
-    __syncthreads();
-    if (g < 4) {
+    lds_barrier();
+    if (wave == 0) {
+        // g = lane/16 here: level 4 from LDS, levels 2 and 1 are lanes 32 and 16 apart
         const float4 sv = vred[g][dq], o = vred[g + 4][dq];
         float4 r = make_float4(sv.x + o.x, sv.y + o.y, sv.z + o.z, sv.w + o.w);
-        r.x = r.x + shfl_xor(r.x, 32); r.y = r.y + shfl_xor(r.y, 32);
-        r.z = r.z + shfl_xor(r.z, 32); r.w = r.w + shfl_xor(r.w, 32);
-        r.x = r.x + shfl_xor(r.x, 16); r.y = r.y + shfl_xor(r.y, 16);
-        r.z = r.z + shfl_xor(r.z, 16); r.w = r.w + shfl_xor(r.w, 16);
-        if (g == 0) ((float4*)(a.opart + (head * a.max_chunks + c) * 64))[dq] = r;
+        r.x = r.x + take_up<32>(r.x); r.y = r.y + take_up<32>(r.y); r.z = r.z + take_up<32>(r.z); r.w = r.w + take_up<32>(r.w);
+        r.x = r.x + take_up<16>(r.x); r.y = r.y + take_up<16>(r.y); r.z = r.z + take_up<16>(r.z); r.w = r.w + take_up<16>(r.w);
+        if (lane < 16) ((float4*)(a.opart + (head * a.max_chunks + c) * 64))[dq] = r;
     }
 }
 
@@ -847,84 +840,82 @@ __global__ __launch_bounds__(64) void k_attn_reduce(AttnArgs a) {
 // The null stream's memory is zero, so its block output is exactly zero and is skipped.
 // ------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_xattn(XAttnArgs a) {
+    // One block per head, n_ctx <= 256 keys (one chunk). Scores: 16 lanes per key (four dims
+    // each), 16 keys per pass; after the halving reduce thread (wave, g, t) holds key
+    // 16t + 4*wave + g. V: partial g16 = key mod 16, lane%16 -> dims 4*(lane%16)..+3.
     const int h = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, t = lane & 15;
     const int nc = a.n_ctx;
     const float* K = a.k + (size_t)h * nc * 64;
     const float* V = a.v + (size_t)h * nc * 64;
-    __shared__ float s[256];
+    __shared__ float el[256];
     __shared__ float red_f[4];
-    __shared__ double red_d[256];
     __shared__ float4 vred[16][16];
-    __shared__ float inv_sh;
+    __shared__ float ol[64];
     const float4 q = ((const float4*)(a.q + h * 64))[t];
-    for (int it = 0; it * 16 < nc; ++it) {
+    float4 kv[16];
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
         const int j = it * 16 + wave * 4 + g;
-        float p = 0.0f;
-        if (j < nc) {
-            const float4 k = ((const float4*)(K + (size_t)j * 64))[t];
-            p = __builtin_fmaf(q.x, k.x, 0.0f);
-            p = __builtin_fmaf(q.y, k.y, p);
-            p = __builtin_fmaf(q.z, k.z, p);
-            p = __builtin_fmaf(q.w, k.w, p);
-        }
-        p = p + shfl_xor(p, 8);
-        p = p + shfl_xor(p, 4);
-        p = p + shfl_xor(p, 2);
-        p = p + shfl_xor(p, 1);
-        if (t == 0 && j < nc) s[j] = p * a.scale;
+        kv[it] = j < nc ? ((const float4*)(K + (size_t)j * 64))[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    __syncthreads();
-    float mx = -__builtin_inff();
-    for (int j = tid; j < nc; j += 256) mx = mx > s[j] ? mx : s[j];
+    const int g16 = wave * 4 + g, dq = lane & 15;
+    float4 vv[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+        const int j = g16 + 16 * m;
+        vv[m] = j < nc ? ((const float4*)(V + (size_t)j * 64))[dq] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float p[16];
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+        float v = __builtin_fmaf(q.x, kv[it].x, 0.0f);
+        v = __builtin_fmaf(q.y, kv[it].y, v);
+        v = __builtin_fmaf(q.z, kv[it].z, v);
+        p[it] = __builtin_fmaf(q.w, kv[it].w, v);
+    }
+    const int jt = t * 16 + wave * 4 + g;
+    const float sc = halving16(p, t) * a.scale;
+    float mx = jt < nc ? sc : -__builtin_inff();
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(mx, off); mx = mx > o ? mx : o; }
     if (lane == 0) red_f[wave] = mx;
-    __syncthreads();
-    mx = red_f[0];
-    for (int w = 1; w < 4; ++w) mx = mx > red_f[w] ? mx : red_f[w];
-    const float e = tid < nc ? dexpf(s[tid] - mx) : 0.0f;
-    red_d[tid] = tid < nc ? (double)e : 0.0;
-    __syncthreads();
-    if (tid < 128) red_d[tid] = red_d[tid] + red_d[tid + 128];
-    __syncthreads();
-    if (tid < 64) {
-        double v = red_d[tid] + red_d[tid + 64];
-        v = fold64d(v);
-        if (tid == 0) inv_sh = (float)(1.0 / (0.0 + v));
-    }
-    __syncthreads();
-    if (tid < nc) s[tid] = e * inv_sh;
-    __syncthreads();
-    const int gg = wave * 4 + g, dq = lane & 15;
+    lds_barrier();
+    float M = red_f[0];
+    for (int w = 1; w < 4; ++w) M = M > red_f[w] ? M : red_f[w];
+    el[jt] = jt < nc ? dexpf(sc - M) : 0.0f;
+    lds_barrier();
+    // the 256-key sum in double (butterfly), every wave; p = e * (float)(1/sum)
+    const double r = ((double)el[lane] + (double)el[lane + 128]) + ((double)el[lane + 64] + (double)el[lane + 192]);
+    const float inv = (float)(1.0 / (0.0 + fold64d_b(r)));
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int m = 0; gg + 16 * m < nc; ++m) {
-        const int j = gg + 16 * m;
-        const float p = s[j];
-        const float4 v = ((const float4*)(V + (size_t)j * 64))[dq];
-        acc.x = __builtin_fmaf(p, v.x, acc.x);
-        acc.y = __builtin_fmaf(p, v.y, acc.y);
-        acc.z = __builtin_fmaf(p, v.z, acc.z);
-        acc.w = __builtin_fmaf(p, v.w, acc.w);
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+        const int j = g16 + 16 * m;
+        if (j < nc) {
+            const float pm = el[j] * inv;
+            acc.x = __builtin_fmaf(pm, vv[m].x, acc.x);
+            acc.y = __builtin_fmaf(pm, vv[m].y, acc.y);
+            acc.z = __builtin_fmaf(pm, vv[m].z, acc.z);
+            acc.w = __builtin_fmaf(pm, vv[m].w, acc.w);
+        }
     }
-    vred[gg][dq] = acc;
-    __syncthreads();
-    if (gg < 8) {
-        const float4 o = vred[gg + 8][dq];
-        vred[gg][dq] = make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
+    vred[g16][dq] = acc;
+    lds_barrier();
+    if (g16 < 8) {
+        const float4 o = vred[g16 + 8][dq];
+        vred[g16][dq] = make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
     }
-    __syncthreads();
-    if (gg < 4) {
-        const float4 sv = vred[gg][dq], o = vred[gg + 4][dq];
-        float4 r = make_float4(sv.x + o.x, sv.y + o.y, sv.z + o.z, sv.w + o.w);
-        r.x = r.x + shfl_xor(r.x, 32); r.y = r.y + shfl_xor(r.y, 32);
-        r.z = r.z + shfl_xor(r.z, 32); r.w = r.w + shfl_xor(r.w, 32);
-        r.x = r.x + shfl_xor(r.x, 16); r.y = r.y + shfl_xor(r.y, 16);
-        r.z = r.z + shfl_xor(r.z, 16); r.w = r.w + shfl_xor(r.w, 16);
-        if (gg == 0) ((float4*)s)[dq] = make_float4(0.0f + r.x, 0.0f + r.y, 0.0f + r.z, 0.0f + r.w);
+    lds_barrier();
+    if (wave == 0) {
+        // g16 = lane/16 here: levels 4 (LDS), 2 and 1 (lanes 32 and 16 apart)
+        const float4 sv = vred[g16][dq], o = vred[g16 + 4][dq];
+        float4 rr = make_float4(sv.x + o.x, sv.y + o.y, sv.z + o.z, sv.w + o.w);
+        rr.x = rr.x + take_up<32>(rr.x); rr.y = rr.y + take_up<32>(rr.y); rr.z = rr.z + take_up<32>(rr.z); rr.w = rr.w + take_up<32>(rr.w);
+        rr.x = rr.x + take_up<16>(rr.x); rr.y = rr.y + take_up<16>(rr.y); rr.z = rr.z + take_up<16>(rr.z); rr.w = rr.w + take_up<16>(rr.w);
+        if (lane < 16) ((float4*)ol)[dq] = make_float4(0.0f + rr.x, 0.0f + rr.y, 0.0f + rr.z, 0.0f + rr.w);
+        put_act(a.out, 0, h * 64 + lane, ol[lane], lane);
     }
-    __syncthreads();
-    if (tid < 64) put_act(a.out, 0, h * 64 + tid, s[tid], tid);
 }
 
 // The hoisted cross K/V: projected [n_ctx][2*dim] -> K [H][n_ctx][64], V [H][n_ctx][64].
@@ -1289,11 +1280,29 @@ void launch_gemv(const GemvArgs& a0, hipStream_t s) {
         }
     }
 }
-void launch_attention(const AttnArgs& a, hipStream_t s) {
-    const dim3 grid(a.max_chunks, a.heads, a.ncol);
-    hipLaunchKernelGGL(k_attn_scores, grid, dim3(256), 0, s, a);
-    hipLaunchKernelGGL(k_attn_softmax, dim3(a.heads, a.ncol), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(k_attn_v, grid, dim3(256), 0, s, a);
+template <int NCH> static void attn_pv(const AttnArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(k_attn_pv<NCH>, dim3(NCH, a.heads, a.ncol), dim3(256), 0, s, a);
+}
+void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
+    hipLaunchKernelGGL(k_attn_scores, dim3(nch * ATT_SUBS, a.heads, a.ncol), dim3(256), 0, s, a);
+    switch (nch) {
+    case 1: attn_pv<1>(a, s); break;
+    case 2: attn_pv<2>(a, s); break;
+    case 3: attn_pv<3>(a, s); break;
+    case 4: attn_pv<4>(a, s); break;
+    case 5: attn_pv<5>(a, s); break;
+    case 6: attn_pv<6>(a, s); break;
+    case 7: attn_pv<7>(a, s); break;
+    case 8: attn_pv<8>(a, s); break;
+    case 9: attn_pv<9>(a, s); break;
+    case 10: attn_pv<10>(a, s); break;
+    case 11: attn_pv<11>(a, s); break;
+    case 12: attn_pv<12>(a, s); break;
+    case 13: attn_pv<13>(a, s); break;
+    case 14: attn_pv<14>(a, s); break;
+    case 15: attn_pv<15>(a, s); break;
+    default: attn_pv<16>(a, s); break;
+    }
     hipLaunchKernelGGL(k_attn_reduce, dim3(a.heads, a.ncol), dim3(64), 0, s, a);
 }
 void launch_xattn(const XAttnArgs& a, int heads, hipStream_t s) {

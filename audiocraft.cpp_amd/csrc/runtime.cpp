@@ -122,7 +122,7 @@ struct mgx_stream {
     float *xk = nullptr, *xv = nullptr;      // per layer [H][n_ctx][64], stream 0
     float* table = nullptr;                  // sinusoid [cap][dim]
     int* dpos = nullptr;                     // the position the next step processes
-    float* cmax = nullptr;                   // [n_seq][H][max_chunks] attention chunk maxima
+    float* cmax = nullptr;                   // [n_seq][H][max_chunks * ATT_SUBS] attention score-block maxima
     float *x = nullptr, *qb = nullptr, *scores = nullptr, *opart = nullptr, *logits = nullptr;
     float* qc = nullptr;                     // cross q [dim]
     ActStore act_o, act_c, act_f;            // attention out, cross-attention out, GELU out
@@ -317,8 +317,12 @@ mgx::GemvArgs& epi_store(mgx::GemvArgs& a, float* y, int stride, bool resid = fa
 
 // One sequence step at the device position *s->dpos for every stream (codebook q's id at
 // ids[q * ids_stride + pos - ids_base]); with `heads`, the step's logits land in s->logits.
-// Ends by advancing the device position unless `advance` is false.
-void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, bool heads, const mgx::SampleArgs* sample) {
+// `position` is the host's view of *s->dpos: it sizes the attention grids (the kernels read
+// the exact key count on the device). Ends by advancing the device position.
+int att_chunks(int position) { return position / mgx::ATT_CHUNK + 1; }
+
+void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, bool heads, const mgx::SampleArgs* sample,
+          int position) {
     const mgx_model* m = s->m;
     const mgx_lm_config& c = m->c;
     const int N = s->n_seq, D = c.dim;
@@ -348,7 +352,7 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, bool 
             // f32 K and V of every key attended, both streams (bytes known only on device: the
             // profile records the host's view of the position)
             ProfScope ps(s, PROF_ATTN, 2.0 * N * c.heads * (s->prof_pos + 1) * 64 * 4);
-            mgx::launch_attention(at, s->hs);
+            mgx::launch_attention(at, att_chunks(position), s->hs);
         }
         {
             mgx::GemvArgs a = ga(L.w[P_OUT], N);
@@ -458,7 +462,7 @@ void make_stream(mgx_model* m, int capacity, int n_seq, const float* t5, int n_c
     s->dpos = s->mem.alloc<int>(1);
     HIP_OK(hipMemsetAsync(s->dpos, 0, sizeof(int), s->hs));
     if (s->max_chunks > mgx::ATT_MAX_CHUNKS) throw Error(MGX_ERR_INVALID, "capacity above 4096 positions");
-    s->cmax = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks);
+    s->cmax = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * mgx::ATT_SUBS);
     s->x = s->mem.alloc<float>((size_t)n_seq * c.dim);
     s->qb = s->mem.alloc<float>((size_t)n_seq * c.dim);
     s->scores = s->mem.alloc<float>((size_t)n_seq * c.heads * capacity);
@@ -592,7 +596,7 @@ int mgx_forward(mgx_stream* s, const int32_t* ids, int32_t n_tokens, float* logi
         HIP_OK(hipMemcpyAsync(s->dpos, &used, sizeof(int), hipMemcpyHostToDevice, s->hs));
         // A prefill is the same per-position arithmetic as single steps (its causal mask only
         // adds exact zeros), so the tokens run one position at a time.
-        for (int t = 0; t < n_tokens; ++t) step(s, s->ids, n_tokens, used, t == n_tokens - 1, nullptr);
+        for (int t = 0; t < n_tokens; ++t) step(s, s->ids, n_tokens, used, t == n_tokens - 1, nullptr, used + t);
         HIP_OK(hipGetLastError());
         if (logits_out)
             HIP_OK(hipMemcpyAsync(logits_out, s->logits, sizeof(float) * (size_t)s->n_seq * c.n_q * c.card,
@@ -633,17 +637,19 @@ struct mgx_session {
     mgx::SampleArgs sa{};
     double prefill_seconds = 0.0, decode_seconds = 0.0;
     int prof_every = 0;
-    // One captured prefill position (no heads) and one captured decode step (heads, CFG
-    // mix, sampling, position advance): every kernel reads the position from the device, so
-    // the same graphs replay for every step.
-    hipGraphExec_t g_body = nullptr, g_step = nullptr;
+    // Captured prefill positions (no heads) and decode steps (heads, CFG mix, sampling,
+    // position advance), one pair per attention chunk count: every kernel reads the position
+    // from the device, so a graph replays for every position with that many 256-key chunks.
+    hipGraphExec_t g_body[mgx::ATT_MAX_CHUNKS] = {}, g_step[mgx::ATT_MAX_CHUNKS] = {};
     // MGX_GRAPHS=0 launches the same kernels one by one (for tools that do not follow
     // stream capture, such as kernel tracers).
     bool use_graphs = true;
     ~mgx_session() {
         if (s && s->hs) (void)hipStreamSynchronize(s->hs);
-        if (g_body) (void)hipGraphExecDestroy(g_body);
-        if (g_step) (void)hipGraphExecDestroy(g_step);
+        for (int i = 0; i < mgx::ATT_MAX_CHUNKS; ++i) {
+            if (g_body[i]) (void)hipGraphExecDestroy(g_body[i]);
+            if (g_step[i]) (void)hipGraphExecDestroy(g_step[i]);
+        }
         mem.release();
     }
     int pattern_t(int q, int step) const { const int t = step - 1 - q; return (step > 0 && t >= 0 && t < T) ? t : -1; }
@@ -714,12 +720,12 @@ void session_create(mgx_model* m, const float* t5_hidden, int32_t n_ctx, int32_t
     *out = ss.release();
 }
 
-hipGraphExec_t capture(mgx_session* ss, bool full) {
+hipGraphExec_t capture(mgx_session* ss, bool full, int position) {
     mgx_stream* s = ss->s.get();
     hipGraph_t g = nullptr;
     hipGraphExec_t e = nullptr;
     HIP_OK(hipStreamBeginCapture(s->hs, hipStreamCaptureModeThreadLocal));
-    step(s, ss->dseq, ss->S, 0, full, full ? &ss->sa : nullptr);
+    step(s, ss->dseq, ss->S, 0, full, full ? &ss->sa : nullptr, position);
     HIP_OK(hipStreamEndCapture(s->hs, &g));
     const hipError_t rc = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
@@ -733,16 +739,16 @@ void run_position(mgx_session* ss, bool full, bool profiled, int position) {
     if (profiled) {
         s->prof_on = true;
         s->prof_pos = position;
-        step(s, ss->dseq, ss->S, 0, full, full ? &ss->sa : nullptr);
+        step(s, ss->dseq, ss->S, 0, full, full ? &ss->sa : nullptr, position);
         s->prof_on = false;
         return;
     }
     if (!ss->use_graphs) {
-        step(s, ss->dseq, ss->S, 0, full, full ? &ss->sa : nullptr);
+        step(s, ss->dseq, ss->S, 0, full, full ? &ss->sa : nullptr, position);
         return;
     }
-    hipGraphExec_t& g = full ? ss->g_step : ss->g_body;
-    if (!g) g = capture(ss, full);
+    hipGraphExec_t& g = (full ? ss->g_step : ss->g_body)[att_chunks(position) - 1];
+    if (!g) g = capture(ss, full, position);
     HIP_OK(hipGraphLaunch(g, s->hs));
 }
 

@@ -50,6 +50,17 @@ def test_tiny_generate_matches_oracle(M, wtype, sampling, top_k):
     assert grep.cache_bytes == rrep.cache_bytes
 
 
+@pytest.mark.parametrize("wtype", [8, 1])
+def test_tiny_long_generate_crosses_attention_chunks(M, wtype):
+    """700 positions: three 256-key attention chunks, a graph per chunk count, prefill across a
+    chunk boundary."""
+    print(f"tiny long generate wtype={wtype}: prompt 300, 700 frames", flush=True)
+    (gc, gf, _, gs), (rc, rf, _, rs) = run_both(M, "tiny", wtype, 11, 300, 700, True, 250)
+    step = H.first_diff(gs, rs)
+    assert step is None, f"mixed logits part at flat index {step} (step {step // gs[0].size})"
+    assert np.array_equal(gf, rf) and np.array_equal(gc, rc)
+
+
 def test_tiny_unguided_and_no_prompt(M):
     print("tiny generate: empty description (unguided), then no prompt", flush=True)
     (gc, gf, _, gs), (rc, rf, _, rs) = run_both(M, "tiny", 8, 6, 7, 30, True, 250, description_empty=True)
