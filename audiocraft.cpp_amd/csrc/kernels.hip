@@ -380,96 +380,80 @@ __device__ __forceinline__ double fold256(const double* red, int lane) {
     return fold64d_b(r);
 }
 
-// LayerNorm (transformer.h:28-38) or plain conversion of NC f32 columns into the activation
-// form, in LDS, by the block's 256 threads. Thread i owns partial i: float4 groups i, i+256,
-// ... of each column, summed in element order in double; the 256 partials are folded by the
-// butterfly. Then (x - mean) * (1/sqrtf(var + eps)) * w + b per element, and quantization
-// (each 32-element block is 8 consecutive lanes).
-template <int WT, int NC, int KG, bool LN>
-__device__ __forceinline__ void prologue(const GemvArgs& a, const LdsAct& x, double* red, int tid, int lane,
-                                         const float4 (&xr)[NC][KG], const float4 (&wr)[KG], const float4 (&br)[KG]) {
+// LayerNorm (transformer.h:28-38) or plain conversion of one f32 column into the activation
+// form, in LDS, by a group of 256 threads (column n of the launch; each column has its own
+// group). Thread i owns partial i: float4 groups i, i+256, ... of the column, summed in
+// element order in double; the 256 partials are folded by the butterfly. Then (x - mean) *
+// (1/sqrtf(var + eps)) * w + b per element, and quantization (each 32-element block is 8
+// consecutive lanes). red: 512 doubles of LDS for this column.
+template <int WT, int KG, bool LN>
+__device__ __forceinline__ void prologue(const GemvArgs& a, const LdsAct& x, double* red, int n, int tid, int lane,
+                                         const float4 (&xr)[KG], const float4 (&wr)[KG], const float4 (&br)[KG]) {
     const int in = a.w.in, nf = in / 4, nb = in / 32;
-    float4 u[NC][KG];
+    float4 u[KG];
 #pragma unroll
-    for (int n = 0; n < NC; ++n)
-#pragma unroll
-        for (int j = 0; j < KG; ++j) u[n][j] = tid + 256 * j < nf ? xr[n][j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int j = 0; j < KG; ++j) u[j] = tid + 256 * j < nf ? xr[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (LN) {
-        float mean[NC];
+        double s = 0.0;
 #pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            double s = 0.0;
-#pragma unroll
-            for (int j = 0; j < KG; ++j) {
-                s = s + (double)u[n][j].x; s = s + (double)u[n][j].y; s = s + (double)u[n][j].z; s = s + (double)u[n][j].w;
-            }
-            red[n * 256 + tid] = s;
+        for (int j = 0; j < KG; ++j) {
+            s = s + (double)u[j].x; s = s + (double)u[j].y; s = s + (double)u[j].z; s = s + (double)u[j].w;
         }
+        red[tid] = s;
         lds_barrier();
+        const float mean = (float)(fold256(red, lane) / (double)in);
+        double s2 = 0.0;
 #pragma unroll
-        for (int n = 0; n < NC; ++n) mean[n] = (float)(fold256(red + n * 256, lane) / (double)in);
-        double* red2 = red + NC * 256;
-#pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            double s2 = 0.0;
-#pragma unroll
-            for (int j = 0; j < KG; ++j) {
-                float4 d = u[n][j];
-                d.x = d.x - mean[n]; d.y = d.y - mean[n]; d.z = d.z - mean[n]; d.w = d.w - mean[n];
-                u[n][j] = d;
-                if (tid + 256 * j < nf) {
-                    s2 = s2 + (double)(d.x * d.x); s2 = s2 + (double)(d.y * d.y);
-                    s2 = s2 + (double)(d.z * d.z); s2 = s2 + (double)(d.w * d.w);
-                }
+        for (int j = 0; j < KG; ++j) {
+            float4 d = u[j];
+            d.x = d.x - mean; d.y = d.y - mean; d.z = d.z - mean; d.w = d.w - mean;
+            u[j] = d;
+            if (tid + 256 * j < nf) {
+                s2 = s2 + (double)(d.x * d.x); s2 = s2 + (double)(d.y * d.y);
+                s2 = s2 + (double)(d.z * d.z); s2 = s2 + (double)(d.w * d.w);
             }
-            red2[n * 256 + tid] = s2;
         }
+        red[256 + tid] = s2;
         lds_barrier();
+        const float var = (float)(fold256(red + 256, lane) / (double)in);
+        const float scale = 1.0f / __builtin_sqrtf(var + a.eps);
 #pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            const float var = (float)(fold256(red2 + n * 256, lane) / (double)in);
-            const float scale = 1.0f / __builtin_sqrtf(var + a.eps);
-#pragma unroll
-            for (int j = 0; j < KG; ++j) {
-                float4 t = u[n][j];
-                t.x = t.x * scale; t.y = t.y * scale; t.z = t.z * scale; t.w = t.w * scale;
-                t.x = t.x * wr[j].x; t.y = t.y * wr[j].y; t.z = t.z * wr[j].z; t.w = t.w * wr[j].w;
-                t.x = t.x + br[j].x; t.y = t.y + br[j].y; t.z = t.z + br[j].z; t.w = t.w + br[j].w;
-                u[n][j] = t;
-            }
+        for (int j = 0; j < KG; ++j) {
+            float4 t = u[j];
+            t.x = t.x * scale; t.y = t.y * scale; t.z = t.z * scale; t.w = t.w * scale;
+            t.x = t.x * wr[j].x; t.y = t.y * wr[j].y; t.z = t.z * wr[j].z; t.w = t.w * wr[j].w;
+            t.x = t.x + br[j].x; t.y = t.y + br[j].y; t.z = t.z + br[j].z; t.w = t.w + br[j].w;
+            u[j] = t;
         }
     }
 #pragma unroll
-    for (int n = 0; n < NC; ++n) {
-#pragma unroll
-        for (int j = 0; j < KG; ++j) {
-            const int f = tid + 256 * j;
-            const float4 t = u[n][j];
-            if (WT == T_Q8_0 || WT == T_Q4_0) {
-                float amax = __builtin_fabsf(t.x);
-                amax = amax > __builtin_fabsf(t.y) ? amax : __builtin_fabsf(t.y);
-                amax = amax > __builtin_fabsf(t.z) ? amax : __builtin_fabsf(t.z);
-                amax = amax > __builtin_fabsf(t.w) ? amax : __builtin_fabsf(t.w);
-                amax = grp8_bcast(grp8_max_to0(amax), lane);
-                const float d = amax / 127.0f;
-                const float id = d != 0.0f ? 1.0f / d : 0.0f;
-                const uint32_t word = (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.x * id)
-                                    | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.y * id) << 8
-                                    | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.z * id) << 16
-                                    | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.w * id) << 24;
-                if (f < nf) {
-                    *(uint32_t*)(x.q + (size_t)n * in + 4 * f) = word;
-                    if ((lane & 7) == 0) x.d[(size_t)n * nb + f / 8] = h2f(f2h(d));
-                }
-            } else if (WT == T_F16) {
-                if (f < nf) {
-                    const uint32_t lo = (uint32_t)f2h(t.x) | (uint32_t)f2h(t.y) << 16;
-                    const uint32_t hi = (uint32_t)f2h(t.z) | (uint32_t)f2h(t.w) << 16;
-                    *(uint2*)(x.h + (size_t)n * in + 4 * f) = make_uint2(lo, hi);
-                }
-            } else if (f < nf) {
-                *(float4*)(x.f + (size_t)n * in + 4 * f) = t;
+    for (int j = 0; j < KG; ++j) {
+        const int f = tid + 256 * j;
+        const float4 t = u[j];
+        if (WT == T_Q8_0 || WT == T_Q4_0) {
+            float amax = __builtin_fabsf(t.x);
+            amax = amax > __builtin_fabsf(t.y) ? amax : __builtin_fabsf(t.y);
+            amax = amax > __builtin_fabsf(t.z) ? amax : __builtin_fabsf(t.z);
+            amax = amax > __builtin_fabsf(t.w) ? amax : __builtin_fabsf(t.w);
+            amax = grp8_bcast(grp8_max_to0(amax), lane);
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            const uint32_t word = (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.x * id)
+                                | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.y * id) << 8
+                                | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.z * id) << 16
+                                | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.w * id) << 24;
+            if (f < nf) {
+                *(uint32_t*)(x.q + (size_t)n * in + 4 * f) = word;
+                if ((lane & 7) == 0) x.d[(size_t)n * nb + f / 8] = h2f(f2h(d));
             }
+        } else if (WT == T_F16) {
+            if (f < nf) {
+                const uint32_t lo = (uint32_t)f2h(t.x) | (uint32_t)f2h(t.y) << 16;
+                const uint32_t hi = (uint32_t)f2h(t.z) | (uint32_t)f2h(t.w) << 16;
+                *(uint2*)(x.h + (size_t)n * in + 4 * f) = make_uint2(lo, hi);
+            }
+        } else if (f < nf) {
+            *(float4*)(x.f + (size_t)n * in + 4 * f) = t;
         }
     }
 }
@@ -481,7 +465,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
     constexpr int M = 64 / G, R = WAVES * M, NT = 64 * WAVES;
     constexpr int IN = U > 0 ? unit_elems<WT>() * G * U : 2048;   // prologue size bound
     constexpr int KG = (IN + 1023) / 1024;
-    static_assert(PRO == PRO_ACT || WAVES == 4, "the prologue has 256 partials, one per thread");
+    static_assert(PRO == PRO_ACT || WAVES == 4 * NC, "the prologue gives each column 256 threads (256 partials)");
     static_assert(U > 0 || G == 8, "the runtime unit loop folds 8 units per lane per pass");
     static_assert(EPI != EPI_GELU_ACT || R % 32 == 0, "GELU blocks quantize whole 32-row blocks");
     extern __shared__ __align__(16) uint8_t lds[];
@@ -496,17 +480,18 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
     float* tile = (float*)(lds + lds_act_bytes(WT, NC, in));
     double* red = (double*)(lds + lds_act_bytes(WT, NC, in) + (size_t)NC * R * 4);
 
-    // 1. activation source
-    float4 xr[NC][PRO == PRO_ACT ? 1 : KG], wr[PRO == PRO_ACT ? 1 : KG], br[PRO == PRO_ACT ? 1 : KG];
+    // 1. activation source (prologue: thread group pcol = tid / 256 builds column pcol)
+    const int pcol = tid >> 8, ptid = tid & 255;
+    float4 xr[PRO == PRO_ACT ? 1 : KG], wr[PRO == PRO_ACT ? 1 : KG], br[PRO == PRO_ACT ? 1 : KG];
     int4 ch[GEMV_KA];
     int nchunks = 0, cq = 0;
     if constexpr (PRO != PRO_ACT) {
         const int nf = in / 4;
+        const float4* xs = (const float4*)(a.x + (size_t)(pcol < ncol ? pcol : ncol - 1) * a.x_stride);
 #pragma unroll
         for (int j = 0; j < KG; ++j) {
-            const int f = tid + 256 * j < nf ? tid + 256 * j : nf - 1;
-#pragma unroll
-            for (int n = 0; n < NC; ++n) xr[n][j] = ((const float4*)(a.x + (size_t)(n < ncol ? n : ncol - 1) * a.x_stride))[f];
+            const int f = ptid + 256 * j < nf ? ptid + 256 * j : nf - 1;
+            xr[j] = xs[f];
             if (PRO == PRO_LN) { wr[j] = ((const float4*)a.ln_w)[f]; br[j] = ((const float4*)a.ln_b)[f]; }
         }
     } else {
@@ -543,7 +528,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
     if constexpr (PRO != PRO_ACT) __builtin_amdgcn_sched_barrier(0);
     // 4. activation -> LDS
     if constexpr (PRO != PRO_ACT) {
-        prologue<WT, NC, KG, PRO == PRO_LN>(a, x, red, tid, lane, xr, wr, br);
+        prologue<WT, KG, PRO == PRO_LN>(a, x, red + pcol * 512, pcol, ptid, lane, xr, wr, br);
     } else {
         // a clamped index loaded the last chunk, so its store rewrites that chunk's own bytes
 #pragma unroll
@@ -715,7 +700,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int j = b * ATT_SUB + it * 16 + wave * 4 + g;
-        kv[it] = ((const float4*)(K + (size_t)(j < u ? j : u - 1) * 64))[t];
+        kv[it] = ((const float4*)(K + (size_t)j * 64))[t];   // rows up to the chunk end exist
     }
     float p[4];
 #pragma unroll
@@ -743,76 +728,85 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
     }
 }
 
-// Softmax + this chunk's share of V^T p, one block per (chunk, head, stream); NCH = the
-// position's chunk count. Every block rebuilds the head's normalizer: global max from the
-// block maxima, e = expf(s - max) for every key, per-chunk double sums in the 256-key
-// butterfly, chunks added in order, p = e * (float)(1/sum). V partials: partial g = key mod
-// 16 (g = 4*wave + lane/16), lane%16 -> dims 4*(lane%16)..+3, keys in increasing order, then
-// the 16 partials folded. Every load is issued before the first use.
-template <int NCH>
-__global__ __launch_bounds__(256) void k_attn_pv(AttnArgs a) {
+// Softmax + this chunk's share of V^T p, one block of 64*WAVES threads per (chunk, head,
+// stream); NCH = the position's chunk count. Every block rebuilds the head's normalizer:
+// global max from the score-block maxima, e = expf(s - max) for every key (spread over all
+// the block's threads), per-chunk double sums in the 256-key butterfly, chunks added in
+// order, p = e * (float)(1/sum). V (waves 0-3): partial g = key mod 16 (g = 4*wave +
+// lane/16), lane%16 -> dims 4*(lane%16)..+3, keys in increasing order, then the 16 partials
+// folded. Every load is issued before the first use (cache rows exist up to the chunk end).
+template <int NCH, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_attn_pv(AttnArgs a) {
+    constexpr int NT = 64 * WAVES, PER = (NCH * ATT_CHUNK + NT - 1) / NT;
     const int c = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
-    const int u = *a.pos + 1;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const size_t head = (size_t)n * a.heads + h;
     const float* S = a.scores + head * a.cap;
-    __shared__ float el[NCH][ATT_CHUNK];
+    __shared__ float el[NCH * ATT_CHUNK];
     __shared__ float4 vred[16][16];
-    float s[NCH];
+    float sv[PER];
 #pragma unroll
-    for (int cc = 0; cc < NCH; ++cc) {
-        const int j = cc * ATT_CHUNK + tid;
-        s[cc] = S[j < u ? j : u - 1];
+    for (int i = 0; i < PER; ++i) {
+        const int j = tid + NT * i;
+        sv[i] = S[j < NCH * ATT_CHUNK ? j : 0];
     }
     float cm[NCH * ATT_SUBS];
 #pragma unroll
     for (int i = 0; i < NCH * ATT_SUBS; ++i) cm[i] = a.cmax[head * a.max_chunks * ATT_SUBS + i];
-    const int g = wave * 4 + (lane >> 4), dq = lane & 15;
+    const int g = (wave & 3) * 4 + (lane >> 4), dq = lane & 15;
     const float* V = a.v + head * a.cap * 64;
     float4 vv[16];
+    if (wave < 4) {
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
-        const int j = c * ATT_CHUNK + g + 16 * m;
-        vv[m] = ((const float4*)(V + (size_t)(j < u ? j : u - 1) * 64))[dq];
+        for (int m = 0; m < 16; ++m) vv[m] = ((const float4*)(V + (size_t)(c * ATT_CHUNK + g + 16 * m) * 64))[dq];
     }
+    const int u = *a.pos + 1;
     float M = cm[0];
 #pragma unroll
     for (int i = 1; i < NCH * ATT_SUBS; ++i) M = M > cm[i] ? M : cm[i];
 #pragma unroll
-    for (int cc = 0; cc < NCH; ++cc) el[cc][tid] = cc * ATT_CHUNK + tid < u ? dexpf(s[cc] - M) : 0.0f;
-    lds_barrier();
-    // every wave folds every chunk (off 128, 64 from LDS, 32..1 in-wave) and adds them in order
-    double cs[NCH];
-#pragma unroll
-    for (int cc = 0; cc < NCH; ++cc)
-        cs[cc] = fold64d_b(((double)el[cc][lane] + (double)el[cc][lane + 128]) + ((double)el[cc][lane + 64] + (double)el[cc][lane + 192]));
-    double total = 0.0;
-#pragma unroll
-    for (int cc = 0; cc < NCH; ++cc) total = total + cs[cc];
-    const float inv = (float)(1.0 / total);
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-    for (int m = 0; m < 16; ++m) {
-        const int jj = g + 16 * m;
-        if (c * ATT_CHUNK + jj < u) {
-            const float pm = el[c][jj] * inv;
-            acc.x = __builtin_fmaf(pm, vv[m].x, acc.x);
-            acc.y = __builtin_fmaf(pm, vv[m].y, acc.y);
-            acc.z = __builtin_fmaf(pm, vv[m].z, acc.z);
-            acc.w = __builtin_fmaf(pm, vv[m].w, acc.w);
-        }
+    for (int i = 0; i < PER; ++i) {
+        const int j = tid + NT * i;
+        if (j < NCH * ATT_CHUNK) el[j] = j < u ? dexpf(sv[i] - M) : 0.0f;
     }
-    vred[g][dq] = acc;
     lds_barrier();
-    if (g < 8) {
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (wave < 4) {
+        // every V wave folds every chunk (off 128, 64 from LDS, 32..1 in-wave), chunks added in order
+        double cs[NCH];
+#pragma unroll
+        for (int cc = 0; cc < NCH; ++cc) {
+            const float* e = el + cc * ATT_CHUNK;
+            cs[cc] = fold64d_b(((double)e[lane] + (double)e[lane + 128]) + ((double)e[lane + 64] + (double)e[lane + 192]));
+        }
+        double total = 0.0;
+#pragma unroll
+        for (int cc = 0; cc < NCH; ++cc) total = total + cs[cc];
+        const float inv = (float)(1.0 / total);
+        const int u_c = u - c * ATT_CHUNK;   // keys of this chunk that exist
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            const int jj = g + 16 * m;
+            if (jj < u_c) {
+                const float pm = el[c * ATT_CHUNK + jj] * inv;
+                acc.x = __builtin_fmaf(pm, vv[m].x, acc.x);
+                acc.y = __builtin_fmaf(pm, vv[m].y, acc.y);
+                acc.z = __builtin_fmaf(pm, vv[m].z, acc.z);
+                acc.w = __builtin_fmaf(pm, vv[m].w, acc.w);
+            }
+        }
+        vred[g][dq] = acc;
+    }
+    lds_barrier();
+    if (wave < 2) {
         const float4 o = vred[g + 8][dq];
         vred[g][dq] = make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
     }
     lds_barrier();
     if (wave == 0) {
         // g = lane/16 here: level 4 from LDS, levels 2 and 1 are lanes 32 and 16 apart
-        const float4 sv = vred[g][dq], o = vred[g + 4][dq];
-        float4 r = make_float4(sv.x + o.x, sv.y + o.y, sv.z + o.z, sv.w + o.w);
+        const float4 sv4 = vred[g][dq], o = vred[g + 4][dq];
+        float4 r = make_float4(sv4.x + o.x, sv4.y + o.y, sv4.z + o.z, sv4.w + o.w);
         r.x = r.x + take_up<32>(r.x); r.y = r.y + take_up<32>(r.y); r.z = r.z + take_up<32>(r.z); r.w = r.w + take_up<32>(r.w);
         r.x = r.x + take_up<16>(r.x); r.y = r.y + take_up<16>(r.y); r.z = r.z + take_up<16>(r.z); r.w = r.w + take_up<16>(r.w);
         if (lane < 16) ((float4*)(a.opart + (head * a.max_chunks + c) * 64))[dq] = r;
@@ -1201,11 +1195,13 @@ void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s) {
     hipLaunchKernelGGL(k_add_bias, dim3((n * ncol + 255) / 256), dim3(256), 0, s, y, b, n, ncol);
 }
 
+constexpr int PV_WAVES = 8;   // softmax + V block: 8 waves share the exps, 4 do V
+
 // ---- GEMV launch: kernel choice by weight type, prologue / epilogue kind and unit count
 template <int WT, int NC, int G, int U, int PRO, int EPI, int W>
 static void gemv_go(const GemvArgs& a, hipStream_t s) {
     constexpr int R = W * (64 / G);
-    const size_t lds = lds_act_bytes(WT, NC, a.w.in) + (size_t)NC * R * 4 + (PRO == PRO_ACT ? 0 : (size_t)NC * 2 * 256 * 8);
+    const size_t lds = lds_act_bytes(WT, NC, a.w.in) + (size_t)NC * R * 4 + (PRO == PRO_ACT ? 0 : (size_t)NC * 512 * 8);
     hipLaunchKernelGGL((k_gemv<WT, NC, G, U, PRO, EPI, W>), dim3((a.w.out + R - 1) / R), dim3(64 * W), lds, s, a);
 }
 
@@ -1225,15 +1221,19 @@ template <int WT, int NC, int PRO, int EPI> static void gemv_pick(const GemvArgs
             GEMV_TRY(8, 2, 2); GEMV_TRY(8, 8, 2);
         }
     } else if constexpr (PRO == PRO_LN) {
+        // 256 threads per column: 4 waves at one column, 8 at two; the GELU epilogue needs
+        // 32-row blocks, so a one-column GELU launch takes 8 lanes a row
+        constexpr int GL = (EPI == EPI_GELU_ACT && NC == 1) ? 8 : 16;
         if constexpr (WT == T_Q8_0 || WT == T_Q4_0) {
-            GEMV_TRY(8, 4, 4); GEMV_TRY(8, 6, 4); GEMV_TRY(8, 8, 4);
+            GEMV_TRY(GL, 32 / GL, 4 * NC); GEMV_TRY(GL, 48 / GL, 4 * NC); GEMV_TRY(GL, 64 / GL, 4 * NC);
         } else if constexpr (WT == T_F16) {
-            GEMV_TRY(8, 16, 4); GEMV_TRY(8, 2, 4);
+            GEMV_TRY(GL, 128 / GL, 4 * NC); GEMV_TRY(8, 2, 4 * NC);
         } else {
-            GEMV_TRY(8, 2, 4);
+            GEMV_TRY(8, 2, 4 * NC);
         }
     }
-    gemv_go<WT, NC, 8, 0, PRO, EPI, 4>(a, s);
+    if constexpr (PRO == PRO_ACT) gemv_go<WT, NC, 8, 0, PRO, EPI, 4>(a, s);
+    else gemv_go<WT, NC, 8, 0, PRO, EPI, 4 * NC>(a, s);
 }
 #undef GEMV_TRY
 
@@ -1281,7 +1281,7 @@ void launch_gemv(const GemvArgs& a0, hipStream_t s) {
     }
 }
 template <int NCH> static void attn_pv(const AttnArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_attn_pv<NCH>, dim3(NCH, a.heads, a.ncol), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((k_attn_pv<NCH, PV_WAVES>), dim3(NCH, a.heads, a.ncol), dim3(64 * PV_WAVES), 0, s, a);
 }
 void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
     hipLaunchKernelGGL(k_attn_scores, dim3(nch * ATT_SUBS, a.heads, a.ncol), dim3(256), 0, s, a);

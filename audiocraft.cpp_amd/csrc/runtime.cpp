@@ -116,9 +116,10 @@ struct ActStore {
 struct mgx_stream {
     mgx_model* m = nullptr;
     int cap = 0, n_seq = 0, cross = 0, n_ctx = 0, used = 0, forwards = 0, max_chunks = 0;
+    int kv_rows = 0;                         // cache rows per head: cap rounded up to whole 256-key chunks
     hipStream_t hs = nullptr;
     DevArena mem;
-    float *K = nullptr, *V = nullptr;        // per layer [n_seq][H][cap][64]
+    float *K = nullptr, *V = nullptr;        // per layer [n_seq][H][kv_rows][64]
     float *xk = nullptr, *xv = nullptr;      // per layer [H][n_ctx][64], stream 0
     float* table = nullptr;                  // sinusoid [cap][dim]
     int* dpos = nullptr;                     // the position the next step processes
@@ -149,7 +150,7 @@ struct mgx_stream {
         }
         return event_pool[event_next++];
     }
-    size_t layer_kv() const { return (size_t)n_seq * m->c.heads * cap * 64; }
+    size_t layer_kv() const { return (size_t)n_seq * m->c.heads * kv_rows * 64; }
     void alloc_act(ActStore& a, int cols, int stride) {
         a.stride = stride;
         a.q = mem.alloc<int8_t>((size_t)cols * stride);
@@ -340,14 +341,14 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, bool 
         {
             mgx::GemvArgs a = ga(L.w[P_QKV], N);
             pro_ln(a, s->x, D, L.n1w, L.n1b, c.norm_eps);
-            a.epi = mgx::EPI_QKV; a.y = s->qb; a.k = Kl; a.v = Vl; a.dim = D; a.heads = c.heads; a.cap = s->cap;
+            a.epi = mgx::EPI_QKV; a.y = s->qb; a.k = Kl; a.v = Vl; a.dim = D; a.heads = c.heads; a.cap = s->kv_rows;
             a.pos = s->dpos;
             gemv(s, a);
         }
         {
             mgx::AttnArgs at{};
             at.q = s->qb; at.k = Kl; at.v = Vl; at.scores = s->scores; at.opart = s->opart; at.cmax = s->cmax;
-            at.dim = D; at.heads = c.heads; at.cap = s->cap; at.max_chunks = s->max_chunks; at.ncol = N;
+            at.dim = D; at.heads = c.heads; at.cap = s->kv_rows; at.max_chunks = s->max_chunks; at.ncol = N;
             at.scale = scale; at.pos = s->dpos; at.out = s->act_o.view(L.w[P_OUT].type);
             // f32 K and V of every key attended, both streams (bytes known only on device: the
             // profile records the host's view of the position)
@@ -450,6 +451,7 @@ void make_stream(mgx_model* m, int capacity, int n_seq, const float* t5, int n_c
     auto s = std::make_unique<mgx_stream>();
     s->m = m; s->cap = capacity; s->n_seq = n_seq; s->cross = cross ? 1 : 0; s->n_ctx = cross ? n_ctx : 0;
     s->max_chunks = (capacity + mgx::ATT_CHUNK - 1) / mgx::ATT_CHUNK;
+    s->kv_rows = s->max_chunks * mgx::ATT_CHUNK;
     HIP_OK(hipStreamCreateWithFlags(&s->hs, hipStreamNonBlocking));
     const size_t kv = s->layer_kv() * c.layers;
     s->K = s->mem.alloc<float>(kv);
@@ -465,7 +467,7 @@ void make_stream(mgx_model* m, int capacity, int n_seq, const float* t5, int n_c
     s->cmax = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * mgx::ATT_SUBS);
     s->x = s->mem.alloc<float>((size_t)n_seq * c.dim);
     s->qb = s->mem.alloc<float>((size_t)n_seq * c.dim);
-    s->scores = s->mem.alloc<float>((size_t)n_seq * c.heads * capacity);
+    s->scores = s->mem.alloc<float>((size_t)n_seq * c.heads * s->kv_rows);
     s->opart = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * 64);
     s->logits = s->mem.alloc<float>((size_t)n_seq * c.n_q * c.card);
     s->qc = s->mem.alloc<float>((size_t)c.dim);
