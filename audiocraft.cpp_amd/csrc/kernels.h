@@ -65,6 +65,7 @@ struct GemvArgs {
     int dim, heads, cap;
     const int* pos;       // QKV: device position
     ActBuf dst;           // GELU_ACT destination
+    unsigned long long* stamp;   // optional [64][2]: per-sub-slot earliest start, latest end (GPU wall clock)
 };
 
 struct AttnArgs {
@@ -78,6 +79,7 @@ struct AttnArgs {
     float scale;
     const int* pos;       // device position: keys [0, pos]
     ActBuf out;           // the out-projection's activation
+    unsigned long long* stamp;   // optional [64][2]: scores' earliest starts, reduce's latest ends
 };
 
 struct XAttnArgs {
@@ -115,6 +117,8 @@ void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s);
 void launch_xkv_split(const float* kv, int n_ctx, int dim, float* k, float* v, hipStream_t s);
 void launch_sample(const SampleArgs& a, hipStream_t s);
 void launch_advance(int* pos, hipStream_t s);
+// fills n launch-timing slots (64 sub-slots each) with {UINT64_MAX, 0}
+void launch_stamp_init(unsigned long long* p, int n, hipStream_t s);
 void launch_repack(int type, const uint8_t* raw, int64_t rows, int in, void* q, uint16_t* d, hipStream_t s);
 
 }  // namespace mgx

@@ -252,6 +252,29 @@ __device__ __forceinline__ float grp8_bcast(float v, int lane) {
 // Workgroup barrier for LDS traffic only: global loads in flight are not waited for.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Launch timing (profiled launches only): a launch's slot holds 64 sub-slots of {earliest
+// start, latest end} on the GPU's constant-rate wall clock; block b publishes into sub-slot
+// b mod 64 once its waves are done (spreading the atomics keeps them off the kernel's own
+// memory traffic). The host takes the min / max over the sub-slots: the span a kernel tracer
+// reports as the launch's duration.
+constexpr int STAMP_SUB = 64;
+__device__ __forceinline__ unsigned long long stamp_begin(const unsigned long long* p) {
+    return p ? (unsigned long long)wall_clock64() : 0ull;
+}
+__device__ __forceinline__ unsigned long long* stamp_sub(unsigned long long* p) {
+    const unsigned b = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    return p + 2 * (b % STAMP_SUB);
+}
+__device__ __forceinline__ void stamp_end(unsigned long long* p, unsigned long long t0) {
+    if (!p) return;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long* q = stamp_sub(p);
+        atomicMin(q, t0);
+        atomicMax(q + 1, (unsigned long long)wall_clock64());
+    }
+}
+
 struct LdsAct {
     int8_t* q;     // Q8 [col][in]
     float* d;      // Q8 [col][in/32]
@@ -461,7 +484,7 @@ __device__ __forceinline__ void prologue(const GemvArgs& a, const LdsAct& x, dou
 // U > 0: every lane owns exactly U units (units == G * U). U == 0: any unit count, a runtime
 // loop in passes of 8 units per lane (needs G == 8 so a pass covers each partial once).
 template <int WT, int NC, int G, int U, int PRO, int EPI, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
+__device__ __forceinline__ void gemv_body(const GemvArgs& a) {
     constexpr int M = 64 / G, R = WAVES * M, NT = 64 * WAVES;
     constexpr int IN = U > 0 ? unit_elems<WT>() * G * U : 2048;   // prologue size bound
     constexpr int KG = (IN + 1023) / 1024;
@@ -688,6 +711,7 @@ __device__ __forceinline__ float halving4(const float (&p)[4], int t) {
 // Scores of one 64-key block (16 lanes per key, four dims each; 16 keys per pass) and the
 // block's max (-inf when it holds no key yet), into cmax[head][block].
 __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
+    const unsigned long long t0 = stamp_begin(a.stamp);
     const int b = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
     const int u = *a.pos + 1;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, t = lane & 15;
@@ -726,6 +750,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
         for (int w = 1; w < 4; ++w) m = m > red_f[w] ? m : red_f[w];
         a.cmax[head * a.max_chunks * ATT_SUBS + b] = m;
     }
+    if (a.stamp && threadIdx.x == 0) atomicMin(stamp_sub(a.stamp), t0);
 }
 
 // Softmax + this chunk's share of V^T p, one block of 64*WAVES threads per (chunk, head,
@@ -827,6 +852,7 @@ __global__ __launch_bounds__(64) void k_attn_reduce(AttnArgs a) {
     for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc)
         if (cc < nch) r = r + part[cc];
     put_act(a.out, n, h * 64 + lane, r, lane);
+    if (a.stamp && lane == 0) atomicMax(stamp_sub(a.stamp) + 1, (unsigned long long)wall_clock64());
 }
 
 // ------------------------------------------------------------------------------------
@@ -1195,6 +1221,13 @@ void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s) {
     hipLaunchKernelGGL(k_add_bias, dim3((n * ncol + 255) / 256), dim3(256), 0, s, y, b, n, ncol);
 }
 
+template <int WT, int NC, int G, int U, int PRO, int EPI, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
+    const unsigned long long t0 = stamp_begin(a.stamp);
+    gemv_body<WT, NC, G, U, PRO, EPI, WAVES>(a);
+    stamp_end(a.stamp, t0);
+}
+
 constexpr int PV_WAVES = 8;   // softmax + V block: 8 waves share the exps, 4 do V
 
 // ---- GEMV launch: kernel choice by weight type, prologue / epilogue kind and unit count
@@ -1313,6 +1346,13 @@ void launch_xkv_split(const float* kv, int n_ctx, int dim, float* k, float* v, h
 }
 void launch_sample(const SampleArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(k_sample, dim3(a.n_q), dim3(256), 0, s, a);
+}
+__global__ void k_stamp_init(unsigned long long* p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n * STAMP_SUB) { p[2 * i] = ~0ull; p[2 * i + 1] = 0ull; }
+}
+void launch_stamp_init(unsigned long long* p, int n, hipStream_t s) {
+    hipLaunchKernelGGL(k_stamp_init, dim3((n * STAMP_SUB + 255) / 256), dim3(256), 0, s, p, n);
 }
 void launch_repack(int type, const uint8_t* raw, int64_t rows, int in, void* q, uint16_t* d, hipStream_t s) {
     const int64_t nblocks = rows * (in / 32);

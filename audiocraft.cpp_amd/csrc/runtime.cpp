@@ -128,27 +128,25 @@ struct mgx_stream {
     float* qc = nullptr;                     // cross q [dim]
     ActStore act_o, act_c, act_f;            // attention out, cross-attention out, GELU out
     int32_t* ids = nullptr;                  // [n_q][cap] staged ids for mgx_forward
-    // Launch timing: when `prof_on`, every GEMV and attention launch is bracketed by HIP
-    // events on this stream; read back by the session's profile call.
-    struct Mark { hipEvent_t a, b; int kind; double bytes; };
+    // Launch timing: when `prof_on`, every GEMV and attention launch gets a slot in `stamps`
+    // (device [slot][2]: earliest block start, latest wave end on the GPU wall clock).
+    struct Mark { int slot, kind; double bytes; };
+    static constexpr int STAMP_SLOTS = 16384;   // launches; 64 sub-slots of 16 B each
     bool prof_on = false;
     int prof_pos = 0;                        // host view of the position, for profiling
     std::vector<Mark> marks;
-    std::vector<hipEvent_t> event_pool;
-    size_t event_next = 0;
+    unsigned long long* stamps = nullptr;
+    double clock_khz = 0.0;
     ~mgx_stream() {
         if (hs) (void)hipStreamSynchronize(hs);
         mem.release();
-        for (hipEvent_t e : event_pool) (void)hipEventDestroy(e);
         if (hs) (void)hipStreamDestroy(hs);
     }
-    hipEvent_t event() {
-        if (event_next == event_pool.size()) {
-            hipEvent_t e;
-            HIP_OK(hipEventCreate(&e));
-            event_pool.push_back(e);
-        }
-        return event_pool[event_next++];
+    // the next timing slot, or null when profiling is off or the slots are used up
+    unsigned long long* stamp_slot(int kind, double bytes) {
+        if (!prof_on || !stamps || (int)marks.size() >= STAMP_SLOTS) return nullptr;
+        marks.push_back({(int)marks.size(), kind, bytes});
+        return stamps + 2 * 64 * (size_t)marks.back().slot;
     }
     size_t layer_kv() const { return (size_t)n_seq * m->c.heads * kv_rows * 64; }
     void alloc_act(ActStore& a, int cols, int stride) {
@@ -270,27 +268,9 @@ double bytes_per_weight(int type) {
 
 enum { PROF_GEMV = 0, PROF_ATTN = 1 };
 
-struct ProfScope {
-    mgx_stream* s;
-    hipEvent_t b = nullptr;
-    int kind;
-    double bytes;
-    ProfScope(mgx_stream* st, int k, double by) : s(st), kind(k), bytes(by) {
-        if (s->prof_on) {
-            hipEvent_t a = s->event();
-            b = s->event();
-            HIP_OK(hipEventRecord(a, s->hs));
-            s->marks.push_back({a, b, kind, bytes});
-        }
-    }
-    ~ProfScope() {
-        if (b) (void)hipEventRecord(b, s->hs);
-    }
-};
-
 // One projection. Algorithmic bytes of a launch = the weights at their stored precision.
-void gemv(mgx_stream* s, const mgx::GemvArgs& a) {
-    ProfScope ps(s, PROF_GEMV, (double)a.w.in * a.w.out * bytes_per_weight(a.w.type));
+void gemv(mgx_stream* s, mgx::GemvArgs a) {
+    a.stamp = s->stamp_slot(PROF_GEMV, (double)a.w.in * a.w.out * bytes_per_weight(a.w.type));
     mgx::launch_gemv(a, s->hs);
 }
 
@@ -350,9 +330,8 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, bool 
             at.q = s->qb; at.k = Kl; at.v = Vl; at.scores = s->scores; at.opart = s->opart; at.cmax = s->cmax;
             at.dim = D; at.heads = c.heads; at.cap = s->kv_rows; at.max_chunks = s->max_chunks; at.ncol = N;
             at.scale = scale; at.pos = s->dpos; at.out = s->act_o.view(L.w[P_OUT].type);
-            // f32 K and V of every key attended, both streams (bytes known only on device: the
-            // profile records the host's view of the position)
-            ProfScope ps(s, PROF_ATTN, 2.0 * N * c.heads * (s->prof_pos + 1) * 64 * 4);
+            // f32 K and V of every key attended, every stream
+            at.stamp = s->stamp_slot(PROF_ATTN, 2.0 * N * c.heads * (position + 1) * 64 * 4);
             mgx::launch_attention(at, att_chunks(position), s->hs);
         }
         {
@@ -854,6 +833,16 @@ int mgx_session_profile(mgx_session* ss, int32_t every) {
     return guarded([&] {
         if (!ss) throw Error(MGX_ERR_INVALID, "null session");
         if (every < 0) throw Error(MGX_ERR_INVALID, "every must be >= 0");
+        mgx_stream* s = ss->s.get();
+        if (every > 0 && !s->stamps) {
+            HIP_OK(hipSetDevice(ss->m->device));
+            s->stamps = s->mem.alloc<unsigned long long>(2 * 64 * (size_t)mgx_stream::STAMP_SLOTS);
+            mgx::launch_stamp_init(s->stamps, mgx_stream::STAMP_SLOTS, s->hs);
+            HIP_OK(hipGetLastError());
+            int khz = 0;
+            HIP_OK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, ss->m->device));
+            s->clock_khz = khz;
+        }
         ss->prof_every = every;
     });
 }
@@ -865,11 +854,19 @@ int mgx_session_profile_read(mgx_session* ss, int32_t kind, double* ms_total, do
         HIP_OK(hipStreamSynchronize(s->hs));
         double ms = 0.0, by = 0.0;
         int n = 0;
-        for (const auto& mk : s->marks) {
-            if (mk.kind != kind) continue;
-            float e = 0.0f;
-            HIP_OK(hipEventElapsedTime(&e, mk.a, mk.b));
-            ms += e; by += mk.bytes; ++n;
+        if (!s->marks.empty()) {
+            std::vector<unsigned long long> st(2 * 64 * s->marks.size());
+            HIP_OK(hipMemcpy(st.data(), s->stamps, st.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+            for (const auto& mk : s->marks) {
+                if (mk.kind != kind) continue;
+                unsigned long long b = ~0ull, e = 0ull;
+                for (int k = 0; k < 64; ++k) {
+                    b = std::min(b, st[2 * (64 * (size_t)mk.slot + k)]);
+                    e = std::max(e, st[2 * (64 * (size_t)mk.slot + k) + 1]);
+                }
+                if (e <= b) continue;   // a launch that recorded nothing
+                ms += (double)(e - b) / s->clock_khz; by += mk.bytes; ++n;
+            }
         }
         if (ms_total) *ms_total = ms;
         if (bytes_total) *bytes_total = by;

@@ -10,10 +10,14 @@ prompt (prefilled, untimed) and a 1500-frame continuation sampled with top-k 250
 seed 1. W warmup decode steps run untimed, then exactly K decode steps are timed; if the
 continuation runs out, a fresh session is prefilled outside the timed segments.
 
-Prints one JSON line. `value` is decode frames/s; `roofline` is the Q8_0 GEMV family's
-achieved HBM bandwidth (weight bytes at 34/32 B per weight over HIP-event-timed launch
-durations of every 64th timed step); `cpu_baseline` times the oracle's CPU restatement of the
-reference decode step on the host for a bounded sample of the same workload.
+Prints one JSON line. `value` is decode frames/s; `roofline` is the weight-GEMV kernel's
+achieved HBM bandwidth: weight bytes at their stored precision (34/32 B per Q8_0 weight) over
+the GPU-side duration of every GEMV launch of every 64th timed step (earliest block start to
+latest wave end, stamped by the kernels on the GPU wall clock of the session's stream);
+`traffic` is the HBM bytes per GEMV launch that rocprofv3's FETCH_SIZE + WRITE_SIZE counters
+read, scaled by the same counters on a copy of known size (profiles/gemv_traffic_medium_q8.txt,
+when present); `cpu_baseline` times the oracle's CPU restatement of the reference decode step
+on the host for a bounded sample of the same workload.
 """
 import argparse
 import ctypes
@@ -53,11 +57,38 @@ def step_bytes(c, wbpw, n_seq, n_ctx, u):
     return w + kv_read + kv_write + xkv + Q * C * n_seq * 4
 
 
+def gemv_traffic(workload):
+    """HBM bytes per GEMV launch from the committed counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", f"gemv_traffic_{workload.replace('-', '_')}.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
 def hip_sync():
     lib = ctypes.CDLL("libamdhip64.so.7")
     rc = lib.hipDeviceSynchronize()
     if rc:
         raise RuntimeError(f"hipDeviceSynchronize failed: {rc}")
+
+
+def device_copy(mib):
+    """One device-to-device copy of `mib` MiB: the known-size reference a counter run scales by."""
+    lib = ctypes.CDLL("libamdhip64.so.7")
+    n = int(mib) << 20
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    for p in (a, b):
+        if lib.hipMalloc(ctypes.byref(p), ctypes.c_size_t(n)):
+            raise RuntimeError("hipMalloc failed")
+    # the buffers stay allocated until the process ends (a counter tool may still refer to them)
+    if lib.hipMemset(a, 1, ctypes.c_size_t(n)) or lib.hipMemcpy(b, a, ctypes.c_size_t(n), 3):
+        raise RuntimeError("device copy failed")
+    hip_sync()
 
 
 def cpu_baseline(w, model, t5, prompt, seconds):
@@ -93,14 +124,22 @@ def main():
     ap.add_argument("--profile-every", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prompt", type=int, default=None,
+                    help="prompt frames override (counter runs: fewer untimed prefill dispatches)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="run one device-to-device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} requested). "
               "The decode step shards by request; see DESIGN.md.", file=sys.stderr)
         sys.exit(2)
     import mgx
-    w = WORKLOADS[args.workload]
+    w = dict(WORKLOADS[args.workload])
+    if args.prompt is not None:
+        w["prompt"] = args.prompt
     mgx.load()
+    if args.copy_mib:
+        device_copy(args.copy_mib)
     t_build = time.time()
     model = mgx.SyntheticModel(w["shape"], w["wtype"], seed=w["seed"])
     c = model.config
@@ -176,7 +215,7 @@ def main():
         "hbm_gbs_step": round(bytes_total / timed / 1e9, 1),
         "roofline_frac_step": round(bytes_total / timed / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": gemv_traffic(args.workload),
                      "kernel": "k_gemv (Q8_0 weight GEMV, all projections)", "launches_timed": gemv[2],
                      "avg_launch_us": round(1000.0 * gemv[0] / max(gemv[2], 1), 3)},
         "attention": {"achieved": round(attn_gbs, 1), "unit": "GB/s", "launches_timed": attn[2],

@@ -156,9 +156,11 @@ void mgx_session_destroy(mgx_session* session);
 
 /* Launch timing (no reference counterpart; the reference has wall clocks only,
    pipeline.cpp:15-18): with every > 0, each GEMV (kind 0) and self-attention (kind 1) launch
-   of every `every`-th loop iteration is bracketed by HIP events on the session's stream.
-   profile_read sums the elapsed milliseconds, the algorithmic bytes (weights at their
-   stored precision; f32 K and V of the keys attended) and the launch count. */
+   of every `every`-th loop iteration records its span on the GPU's constant-rate wall clock
+   (earliest block start to latest wave end -- a kernel tracer's duration; for attention, the
+   scores kernel's start to the reduce kernel's end). profile_read sums those milliseconds,
+   the algorithmic bytes (weights at their stored precision; f32 K and V of the keys
+   attended) and the launch count. */
 int mgx_session_profile(mgx_session* session, int32_t every);
 int mgx_session_profile_read(mgx_session* session, int32_t kind, double* ms_total, double* bytes_total,
                              int32_t* launches);
