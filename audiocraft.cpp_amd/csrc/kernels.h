@@ -42,6 +42,7 @@ struct EmbedArgs {
     int n_q;
     const int32_t* ids;   // codebook q's token for position p at ids[q * ids_stride + p - ids_base]
     int ids_stride, ids_base;
+    int ids_req_stride, cols_per_req;   // column n reads request n / cols_per_req's ids (+ that * ids_req_stride)
     const float* table;   // sinusoid [capacity][dim]
     const int* pos;       // device position of this step
     int dim;
@@ -65,6 +66,15 @@ struct GemvArgs {
     int dim, heads, cap;
     const int* pos;       // QKV: device position
     ActBuf dst;           // GELU_ACT destination
+    float* dst_f;         // GELU_ACT: optional f32 copy [col][dst.stride] (an adapted consumer's A x reads it)
+    // optional adapter on this projection (lora.h:50-83): y = Wx + s*B(Ax), DoRA rows scale
+    // y by m / ||W + sBA||, then the strength blend; applied before the epilogue
+    const float* ad_ax;   // [col][ad_rank] A x of the launch's columns; null = no adapter
+    const float* ad_B;    // [out][ad_rank]
+    const float* ad_m;    // [out] magnitude (DoRA) or null (plain LoRA)
+    const float* ad_norm; // [out] ||W + sBA|| per row (DoRA)
+    int ad_rank;
+    float ad_scale, ad_strength;
     unsigned long long* stamp;   // optional [64][2]: per-sub-slot earliest start, latest end (GPU wall clock)
 };
 
@@ -79,46 +89,57 @@ struct AttnArgs {
     float scale;
     const int* pos;       // device position: keys [0, pos]
     ActBuf out;           // the out-projection's activation
+    float* out_f;         // optional f32 copy [col][dim] (an adapted out-projection's A x reads it)
     unsigned long long* stamp;   // optional [64][2]: scores' earliest starts, reduce's latest ends
 };
 
+// One block per (head, request r): q + r*dim, k / v + r*heads*n_ctx*64, output column r.
 struct XAttnArgs {
-    const float* q;   // [dim]
-    const float* k;   // [heads][n_ctx][64]
+    const float* q;   // [n_req][dim]
+    const float* k;   // [n_req][heads][n_ctx][64]
     const float* v;
-    int n_ctx;
+    int n_ctx, dim;
     float scale;
-    ActBuf out;       // column 0 of cross.out's activation
+    ActBuf out;       // cross.out's activation, column r
+    float* out_f;     // optional f32 copy [n_req][dim]
 };
 
+constexpr int MAX_REQ = 16;      // requests of one batched session
+
+// One block per (codebook, request). Request r's arrays sit at r * (their per-request size).
 struct SampleArgs {
-    const float* logits;     // [n_seq][n_q][card]
-    int n_q, card, guided;
-    float cfg_coef;
-    const uint8_t* mask;     // [n_q][steps]
+    const float* logits;     // [n_req][guided ? 2 : 1][n_q][card]
+    int n_q, card, guided, n_req;
+    const uint8_t* mask;     // [n_q][steps] (the same delay pattern for every request)
     int steps, start;
     const int* pos;          // the loop offset is *pos + 1
-    int use_sampling;
-    float temperature;
-    int top_k;
-    const float* uniforms;   // [steps][n_q]
     int special;
-    int32_t* seq;            // [n_q][steps]
-    float* first_logits;     // [n_q][card], written at offset == start
-    float* step_logits;      // [steps - start][n_q][card] or null
+    const float* uniforms;   // [n_req][steps][n_q]
+    int32_t* seq;            // [n_req][n_q][steps]
+    float* first_logits;     // [n_req][n_q][card], written at offset == start
+    float* step_logits;      // [n_req][steps - start][n_q][card] or null
+    float cfg_coef[MAX_REQ], temperature[MAX_REQ];
+    int use_sampling[MAX_REQ], top_k[MAX_REQ];
 };
 
 void launch_embed(const EmbedArgs& a, hipStream_t s);
 void launch_gemv(const GemvArgs& a, hipStream_t s);
 // nch: the 256-key chunks of the position the launch runs at (the grid covers exactly these)
 void launch_attention(const AttnArgs& a, int nch, hipStream_t s);
-void launch_xattn(const XAttnArgs& a, int heads, hipStream_t s);
+void launch_xattn(const XAttnArgs& a, int heads, int n_req, hipStream_t s);
 void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s);
 void launch_xkv_split(const float* kv, int n_ctx, int dim, float* k, float* v, hipStream_t s);
 void launch_sample(const SampleArgs& a, hipStream_t s);
 void launch_advance(int* pos, hipStream_t s);
 // fills n launch-timing slots (64 sub-slots each) with {UINT64_MAX, 0}
+// A x for an adapter (w = A as an f32 matrix [rank][in]; pro LN or F32 with x / x_stride /
+// ln_*; y = [col][y_stride]), the column built as the adapted projection builds it
+void launch_adapter_ax(const GemvArgs& a, hipStream_t s);
 void launch_stamp_init(unsigned long long* p, int n, hipStream_t s);
+// DoRA rows (lora.h:11-32, 142): norm[r] = sqrt(||W_r||^2 + 2s<W_r,(BA)_r> + s^2||(BA)_r||^2)
+// from the dequantized base rows, in double; bad != 0 afterwards if a base weight was not finite
+void launch_dora_norm(const DevMat& w, const float* A, const float* B, int rank, float scale, float* norm, int* bad,
+                      hipStream_t s);
 void launch_repack(int type, const uint8_t* raw, int64_t rows, int in, void* q, uint16_t* d, hipStream_t s);
 
 }  // namespace mgx

@@ -156,14 +156,18 @@ __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= a.dim) return;
     const int p = *a.pos;
-    float e = 0.0f;
-    for (int q = 0; q < a.n_q; ++q) {
-        const int id = a.ids[(size_t)q * a.ids_stride + (p - a.ids_base)];
-        const float v = mat_elem(a.emb[q], id, i);
-        e = q == 0 ? v : e + v;
+    const float tab = a.table[(size_t)p * a.dim + i];
+    for (int r = 0; r * a.cols_per_req < a.ncol; ++r) {
+        const int32_t* ids = a.ids + (size_t)r * a.ids_req_stride;
+        float e = 0.0f;
+        for (int q = 0; q < a.n_q; ++q) {
+            const int id = ids[(size_t)q * a.ids_stride + (p - a.ids_base)];
+            const float v = mat_elem(a.emb[q], id, i);
+            e = q == 0 ? v : e + v;
+        }
+        const float x = tab + e;
+        for (int n = r * a.cols_per_req; n < (r + 1) * a.cols_per_req && n < a.ncol; ++n) a.x[(size_t)n * a.dim + i] = x;
     }
-    const float x = a.table[(size_t)p * a.dim + i] + e;
-    for (int n = 0; n < a.ncol; ++n) a.x[(size_t)n * a.dim + i] = x;
 }
 
 __global__ void k_advance(int* pos) { *pos = *pos + 1; }
@@ -481,6 +485,32 @@ __device__ __forceinline__ void prologue(const GemvArgs& a, const LdsAct& x, dou
     }
 }
 
+// Adapter on one output (row, column) of a projection (lora.h:50-83): lo = B[row] . (Ax)[col]
+// as f32 with rank k -> partial (k>>3) mod 64 (fmaf in order) folded by the 64-wide butterfly
+// (partials >= 8 are zero: the first three levels add +0.0f), times s; v = base + lo; DoRA
+// rows v *= m[row] / norm[row]; strength blend base + (v - base) * strength.
+__device__ __forceinline__ float adapt(const GemvArgs& a, int row, int col, float base) {
+    const float* bp = a.ad_B + (size_t)row * a.ad_rank;
+    const float* xp = a.ad_ax + (size_t)col * a.ad_rank;
+    float part[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) part[l] = 0.0f;
+    for (int k = 0; k < a.ad_rank; ++k) part[k >> 3] = __builtin_fmaf(bp[k], xp[k], part[k >> 3]);
+#pragma unroll
+    for (int l = 0; l < 8; ++l) part[l] = part[l] + 0.0f;
+#pragma unroll
+    for (int off = 4; off >= 1; off >>= 1)
+#pragma unroll
+        for (int l = 0; l < off; ++l) part[l] = part[l] + part[l + off];
+    const float lo = part[0] * a.ad_scale;
+    float v = base + lo;
+    if (a.ad_m) {
+        v = v * (a.ad_m[row] / a.ad_norm[row]);
+        if (a.ad_strength != 1.0f) v = base + (v - base) * a.ad_strength;
+    }
+    return v;
+}
+
 // U > 0: every lane owns exactly U units (units == G * U). U == 0: any unit count, a runtime
 // loop in passes of 8 units per lane (needs G == 8 so a pass covers each partial once).
 template <int WT, int NC, int G, int U, int PRO, int EPI, int WAVES>
@@ -612,6 +642,11 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
             for (int m = 0; m < h; ++m) acc[n][m] = acc[n][m] + acc[n][m + h];
         v[n] = fold_to0<G>(acc[n][0]);
     }
+    if (a.ad_ax && t == 0 && row < out) {
+#pragma unroll
+        for (int n = 0; n < NC; ++n)
+            if (n < ncol) v[n] = adapt(a, row, n, v[n]);
+    }
     // 6. epilogue: lane 0 of each row group holds every column's value
     if constexpr (EPI == EPI_GELU_ACT) {
         // the block's R rows -> LDS tile -> GELU (one value per lane, spread over the waves)
@@ -644,6 +679,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
                 if (d.kind == ACT_F16) d.h[(size_t)n * d.stride + o] = f2h(g);
                 else d.f[(size_t)n * d.stride + o] = g;
             }
+            if (a.dst_f && lane < 32) a.dst_f[(size_t)n * d.stride + o] = g;
         }
         return;
     }
@@ -852,6 +888,7 @@ __global__ __launch_bounds__(64) void k_attn_reduce(AttnArgs a) {
     for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc)
         if (cc < nch) r = r + part[cc];
     put_act(a.out, n, h * 64 + lane, r, lane);
+    if (a.out_f) a.out_f[(size_t)n * a.dim + h * 64 + lane] = r;
     if (a.stamp && lane == 0) atomicMax(stamp_sub(a.stamp) + 1, (unsigned long long)wall_clock64());
 }
 
@@ -863,16 +900,16 @@ __global__ __launch_bounds__(256) void k_xattn(XAttnArgs a) {
     // One block per head, n_ctx <= 256 keys (one chunk). Scores: 16 lanes per key (four dims
     // each), 16 keys per pass; after the halving reduce thread (wave, g, t) holds key
     // 16t + 4*wave + g. V: partial g16 = key mod 16, lane%16 -> dims 4*(lane%16)..+3.
-    const int h = blockIdx.x;
+    const int h = blockIdx.x, r = blockIdx.y, H = gridDim.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, t = lane & 15;
     const int nc = a.n_ctx;
-    const float* K = a.k + (size_t)h * nc * 64;
-    const float* V = a.v + (size_t)h * nc * 64;
+    const float* K = a.k + ((size_t)r * H + h) * nc * 64;
+    const float* V = a.v + ((size_t)r * H + h) * nc * 64;
     __shared__ float el[256];
     __shared__ float red_f[4];
     __shared__ float4 vred[16][16];
     __shared__ float ol[64];
-    const float4 q = ((const float4*)(a.q + h * 64))[t];
+    const float4 q = ((const float4*)(a.q + (size_t)r * a.dim + h * 64))[t];
     float4 kv[16];
 #pragma unroll
     for (int it = 0; it < 16; ++it) {
@@ -906,8 +943,8 @@ __global__ __launch_bounds__(256) void k_xattn(XAttnArgs a) {
     el[jt] = jt < nc ? dexpf(sc - M) : 0.0f;
     lds_barrier();
     // the 256-key sum in double (butterfly), every wave; p = e * (float)(1/sum)
-    const double r = ((double)el[lane] + (double)el[lane + 128]) + ((double)el[lane + 64] + (double)el[lane + 192]);
-    const float inv = (float)(1.0 / (0.0 + fold64d_b(r)));
+    const double es = ((double)el[lane] + (double)el[lane + 128]) + ((double)el[lane + 64] + (double)el[lane + 192]);
+    const float inv = (float)(1.0 / (0.0 + fold64d_b(es)));
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int m = 0; m < 16; ++m) {
@@ -934,7 +971,8 @@ __global__ __launch_bounds__(256) void k_xattn(XAttnArgs a) {
         rr.x = rr.x + take_up<32>(rr.x); rr.y = rr.y + take_up<32>(rr.y); rr.z = rr.z + take_up<32>(rr.z); rr.w = rr.w + take_up<32>(rr.w);
         rr.x = rr.x + take_up<16>(rr.x); rr.y = rr.y + take_up<16>(rr.y); rr.z = rr.z + take_up<16>(rr.z); rr.w = rr.w + take_up<16>(rr.w);
         if (lane < 16) ((float4*)ol)[dq] = make_float4(0.0f + rr.x, 0.0f + rr.y, 0.0f + rr.z, 0.0f + rr.w);
-        put_act(a.out, 0, h * 64 + lane, ol[lane], lane);
+        put_act(a.out, r, h * 64 + lane, ol[lane], lane);
+        if (a.out_f) a.out_f[(size_t)r * a.dim + h * 64 + lane] = ol[lane];
     }
 }
 
@@ -1013,14 +1051,20 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
     __shared__ float inv_sh;
     __shared__ uint32_t prefix_sh;
     __shared__ int k_sh;
-    const float* cond = a.logits + (size_t)q * C;
-    const float* null_l = a.logits + (size_t)(a.n_q + q) * C;
+    const int r = blockIdx.y;
+    const float cfg_coef = a.cfg_coef[r], temperature = a.temperature[r];
+    const int use_sampling = a.use_sampling[r], top_k = a.top_k[r];
+    const float* lr = a.logits + (size_t)r * (a.guided ? 2 : 1) * a.n_q * C;
+    const float* cond = lr + (size_t)q * C;
+    const float* null_l = lr + (size_t)(a.n_q + q) * C;
     const int offset = *a.pos + 1;
-    float* first = offset == a.start ? a.first_logits : nullptr;
-    float* stepl = a.step_logits ? a.step_logits + ((size_t)(offset - a.start) * a.n_q + q) * C : nullptr;
+    float* first = offset == a.start ? a.first_logits + (size_t)r * a.n_q * C : nullptr;
+    float* stepl = a.step_logits ? a.step_logits + (((size_t)r * (a.steps - a.start) + (offset - a.start)) * a.n_q + q) * C : nullptr;
+    const float* uniforms = a.uniforms + (size_t)r * a.steps * a.n_q;
+    int32_t* seq = a.seq + (size_t)r * a.n_q * a.steps;
     for (int i = tid; i < C; i += 256) {
         float v = cond[i];
-        if (a.guided) v = null_l[i] + (cond[i] - null_l[i]) * a.cfg_coef;
+        if (a.guided) v = null_l[i] + (cond[i] - null_l[i]) * cfg_coef;
         lg[i] = v;
         if (first) first[(size_t)q * C + i] = v;
         if (stepl) stepl[i] = v;
@@ -1029,7 +1073,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
     const bool live = a.mask[(size_t)q * a.steps + offset] != 0;
     int token;
     if (!live) token = a.special;
-    else if (!a.use_sampling || !(a.temperature > 0.0f)) {
+    else if (!use_sampling || !(temperature > 0.0f)) {
         // argmax, lowest index on ties
         float best = -__builtin_inff();
         int bi = 0x7fffffff;
@@ -1062,7 +1106,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
         pk = red_f[0];
         for (int w = 1; w < 4; ++w) pk = pk < red_f[w] ? red_f[w] : pk;
         for (int i = tid; i < C; i += 256) {
-            const double e = dexp(((double)lg[i] - (double)pk) / (double)a.temperature);
+            const double e = dexp(((double)lg[i] - (double)pk) / (double)temperature);
             ex[i] = e;
             pr[i] = (float)e;
         }
@@ -1071,7 +1115,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
         __syncthreads();
         for (int i = tid; i < C; i += 256) pr[i] = pr[i] * inv_sh;
         __syncthreads();
-        const int k = a.top_k;
+        const int k = top_k;
         if (k > 0 && k < C) {
             // top_k_filter: the k-th largest value counting repeats, by MSB-first radix select
             // over the bit patterns (non-negative floats order like their bits)
@@ -1146,7 +1190,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
             pick_sh = C - 1;
         }
         __syncthreads();
-        const double target = (double)a.uniforms[(size_t)offset * a.n_q + q] * 1.0;
+        const double target = (double)uniforms[(size_t)offset * a.n_q + q] * 1.0;
         if (exact_sh) {
             // thread t owns elements [SMP_PER*t, SMP_PER*t + SMP_PER); exact prefix sums
             double loc[SMP_PER];
@@ -1187,7 +1231,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
         token = pick_sh;
     }
     if (tid == 0) {
-        int32_t* slot = a.seq + (size_t)q * a.steps + offset;
+        int32_t* slot = seq + (size_t)q * a.steps + offset;
         if (*slot == -1) *slot = token;
     }
 }
@@ -1297,6 +1341,8 @@ void launch_gemv(const GemvArgs& a0, hipStream_t s) {
             };
             adv(a.src);
             adv(a.dst);
+            if (a0.dst_f) a.dst_f = a0.dst_f + (size_t)c0 * a0.dst.stride;
+            if (a0.ad_ax) a.ad_ax = a0.ad_ax + (size_t)c0 * a0.ad_rank;
             if (a0.epi == EPI_QKV) {
                 a.y = a0.y + (size_t)c0 * a0.dim;
                 a.k = a0.k + (size_t)c0 * a0.heads * a0.cap * 64;
@@ -1338,14 +1384,14 @@ void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
     }
     hipLaunchKernelGGL(k_attn_reduce, dim3(a.heads, a.ncol), dim3(64), 0, s, a);
 }
-void launch_xattn(const XAttnArgs& a, int heads, hipStream_t s) {
-    hipLaunchKernelGGL(k_xattn, dim3(heads), dim3(256), 0, s, a);
+void launch_xattn(const XAttnArgs& a, int heads, int n_req, hipStream_t s) {
+    hipLaunchKernelGGL(k_xattn, dim3(heads, n_req), dim3(256), 0, s, a);
 }
 void launch_xkv_split(const float* kv, int n_ctx, int dim, float* k, float* v, hipStream_t s) {
     hipLaunchKernelGGL(k_xkv_split, dim3((n_ctx * 2 * dim + 255) / 256), dim3(256), 0, s, kv, n_ctx, dim, k, v);
 }
 void launch_sample(const SampleArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_sample, dim3(a.n_q), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_sample, dim3(a.n_q, a.n_req), dim3(256), 0, s, a);
 }
 __global__ void k_stamp_init(unsigned long long* p, int n) {
     const int i = blockIdx.x * 256 + threadIdx.x;
@@ -1353,6 +1399,94 @@ __global__ void k_stamp_init(unsigned long long* p, int n) {
 }
 void launch_stamp_init(unsigned long long* p, int n, hipStream_t s) {
     hipLaunchKernelGGL(k_stamp_init, dim3((n * STAMP_SUB + 255) / 256), dim3(256), 0, s, p, n);
+}
+// A x of an adapted projection (the inner mul_mat of lora.h:50-83's s * B(Ax)): one block per
+// (column, four rank rows). The column is built in LDS as the projection's own prologue
+// builds it (LayerNorm, or the f32 column as is); wave w takes rank row 4 * blockIdx.y + w:
+// lane l sums the 8-element units l, l + 64, ... of the row in element order (fmaf), and the
+// 64 partials fold by the butterfly -- the f32-weight convention of every projection.
+template <int KG, bool LN>
+__global__ __launch_bounds__(256) void k_adapter_ax(GemvArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = blockIdx.x;
+    const int in = a.w.in, nf = in / 4;
+    LdsAct x{};
+    x.in = in;
+    x.f = (float*)lds;
+    double* red = (double*)(lds + (size_t)in * 4);
+    float4 xr[KG], wr[KG], br[KG];
+    const float4* xs = (const float4*)(a.x + (size_t)col * a.x_stride);
+#pragma unroll
+    for (int j = 0; j < KG; ++j) {
+        const int f = tid + 256 * j < nf ? tid + 256 * j : nf - 1;
+        xr[j] = xs[f];
+        if (LN) { wr[j] = ((const float4*)a.ln_w)[f]; br[j] = ((const float4*)a.ln_b)[f]; }
+    }
+    prologue<T_F32, KG, LN>(a, x, red, 0, tid, lane, xr, wr, br);
+    lds_barrier();
+    const int k = blockIdx.y * 4 + wave;
+    if (k >= a.w.out) return;
+    const float* A = (const float*)a.w.q + (size_t)k * in;
+    float p = 0.0f;
+    for (int u = lane; u < in / 8; u += 64) {
+        const float4 w0 = *(const float4*)(A + 8 * u), w1 = *(const float4*)(A + 8 * u + 4);
+        const float4 x0 = *(const float4*)(x.f + 8 * u), x1 = *(const float4*)(x.f + 8 * u + 4);
+        p = __builtin_fmaf(w0.x, x0.x, p); p = __builtin_fmaf(w0.y, x0.y, p);
+        p = __builtin_fmaf(w0.z, x0.z, p); p = __builtin_fmaf(w0.w, x0.w, p);
+        p = __builtin_fmaf(w1.x, x1.x, p); p = __builtin_fmaf(w1.y, x1.y, p);
+        p = __builtin_fmaf(w1.z, x1.z, p); p = __builtin_fmaf(w1.w, x1.w, p);
+    }
+    p = fold64(p);
+    if (lane == 0) a.y[(size_t)col * a.y_stride + k] = p;
+}
+template <int KG> static void adapter_ax_go(const GemvArgs& a, hipStream_t s) {
+    const dim3 grid(a.ncol, (a.w.out + 3) / 4);
+    const size_t lds = (size_t)a.w.in * 4 + 512 * 8;
+    if (a.pro == PRO_LN) hipLaunchKernelGGL((k_adapter_ax<KG, true>), grid, dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((k_adapter_ax<KG, false>), grid, dim3(256), lds, s, a);
+}
+void launch_adapter_ax(const GemvArgs& a, hipStream_t s) {
+    switch ((a.w.in + 1023) / 1024) {
+    case 1: adapter_ax_go<1>(a, s); break;
+    case 2: adapter_ax_go<2>(a, s); break;
+    case 3: adapter_ax_go<3>(a, s); break;
+    case 4: adapter_ax_go<4>(a, s); break;
+    case 5: adapter_ax_go<5>(a, s); break;
+    case 6: adapter_ax_go<6>(a, s); break;
+    case 7: adapter_ax_go<7>(a, s); break;
+    default: adapter_ax_go<8>(a, s); break;
+    }
+}
+// DoRA rows (lora.h:11-32): one thread per row, sequential double sums over the row.
+__global__ __launch_bounds__(64) void k_dora_norm(DevMat w, const float* A, const float* B, int rank, float scale,
+                                                  float* norm, int* bad) {
+    const int r = blockIdx.x * 64 + threadIdx.x;
+    if (r >= w.out) return;
+    const int in = w.in;
+    double sum = (double)in * 1e-12;
+    int nonfinite = 0;
+    for (int i = 0; i < in; ++i) {
+        const float x = mat_elem(w, r, i);
+        nonfinite |= !__builtin_isfinite(x);
+        sum += (double)x * x;
+    }
+    const float base = (float)sum;
+    double t2 = 0.0, t3 = 0.0;
+    for (int i = 0; i < in; ++i) {
+        double acc = 0.0;
+        for (int k = 0; k < rank; ++k) acc += (double)B[(size_t)r * rank + k] * A[(size_t)k * in + i];
+        const float ba = (float)acc;
+        const float x = mat_elem(w, r, i);
+        t2 += (double)x * ba;
+        t3 += (double)ba * ba;
+    }
+    const double nsq = (double)base + 2.0 * scale * t2 + (double)scale * scale * t3;
+    norm[r] = (float)__builtin_sqrt(nsq);
+    if (nonfinite) atomicOr(bad, 1);
+}
+void launch_dora_norm(const DevMat& w, const float* A, const float* B, int rank, float scale, float* norm, int* bad,
+                      hipStream_t s) {
+    hipLaunchKernelGGL(k_dora_norm, dim3((w.out + 63) / 64), dim3(64), 0, s, w, A, B, rank, scale, norm, bad);
 }
 void launch_repack(int type, const uint8_t* raw, int64_t rows, int in, void* q, uint16_t* d, hipStream_t s) {
     const int64_t nblocks = rows * (in / 32);

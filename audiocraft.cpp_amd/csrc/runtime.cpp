@@ -16,6 +16,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <algorithm>
+#include <atomic>
 #include <map>
 #include <memory>
 #include <random>
@@ -82,9 +83,23 @@ int act_kind(int wtype) {
 
 }  // namespace
 
+// One adapted projection on the device (ac::LoraProjection, lora.h:39-47): A as an f32
+// matrix of `rank` rows, B [out][rank], DoRA magnitude and the fixed row norms
+// ||W + s*BA|| (lora.h:11-32), s = alpha / rank (times the strength for plain LoRA,
+// lora.h:142); DoRA blends with the strength after the row scaling.
+struct AdapterW {
+    mgx::DevMat A{};
+    const float* B = nullptr;
+    const float* m = nullptr;
+    float* norm = nullptr;
+    int rank = 0;
+    float scale = 0.0f, strength = 1.0f;
+};
+
 struct LayerW {
     mgx::DevMat w[P_COUNT];
     const float *n1w, *n1b, *ncw, *ncb, *n2w, *n2b;
+    const AdapterW* ad[P_COUNT] = {};   // null: no adapter, or one that is the identity
 };
 
 struct mgx_model {
@@ -94,7 +109,11 @@ struct mgx_model {
     mgx::DevMat emb[8]{}, heads{}, cond_proj{};
     const float *cond_proj_b = nullptr, *out_w = nullptr, *out_b = nullptr;
     std::vector<LayerW> L;
-    ~mgx_model() { mem.release(); }
+    DevArena ad_mem;                 // adapter tensors, replaced as a whole by set_adapters
+    std::vector<AdapterW> ads;
+    int ad_rank_max = 0;
+    std::atomic<int> live{0};        // streams (and sessions) using the model
+    ~mgx_model() { ad_mem.release(); mem.release(); }
 };
 
 // Device buffers of activation columns in one of the three forms (Q8_0 blocks, fp16, f32).
@@ -116,16 +135,18 @@ struct ActStore {
 struct mgx_stream {
     mgx_model* m = nullptr;
     int cap = 0, n_seq = 0, cross = 0, n_ctx = 0, used = 0, forwards = 0, max_chunks = 0;
+    int n_req = 1, cpr = 1;                  // requests, and columns (streams) per request
     int kv_rows = 0;                         // cache rows per head: cap rounded up to whole 256-key chunks
     hipStream_t hs = nullptr;
     DevArena mem;
     float *K = nullptr, *V = nullptr;        // per layer [n_seq][H][kv_rows][64]
-    float *xk = nullptr, *xv = nullptr;      // per layer [H][n_ctx][64], stream 0
+    float *xk = nullptr, *xv = nullptr;      // per layer [n_req][H][n_ctx][64], each request's stream 0
+    float* ax = nullptr;                     // adapter A x of the running projection [n_seq][rank]
     float* table = nullptr;                  // sinusoid [cap][dim]
     int* dpos = nullptr;                     // the position the next step processes
     float* cmax = nullptr;                   // [n_seq][H][max_chunks * ATT_SUBS] attention score-block maxima
     float *x = nullptr, *qb = nullptr, *scores = nullptr, *opart = nullptr, *logits = nullptr;
-    float* qc = nullptr;                     // cross q [dim]
+    float* qc = nullptr;                     // cross q [n_req][dim]
     ActStore act_o, act_c, act_f;            // attention out, cross-attention out, GELU out
     int32_t* ids = nullptr;                  // [n_q][cap] staged ids for mgx_forward
     // Launch timing: when `prof_on`, every GEMV and attention launch gets a slot in `stamps`
@@ -141,6 +162,7 @@ struct mgx_stream {
         if (hs) (void)hipStreamSynchronize(hs);
         mem.release();
         if (hs) (void)hipStreamDestroy(hs);
+        if (m) m->live.fetch_sub(1);
     }
     // the next timing slot, or null when profiling is off or the slots are used up
     unsigned long long* stamp_slot(int kind, double bytes) {
@@ -296,20 +318,41 @@ mgx::GemvArgs& epi_store(mgx::GemvArgs& a, float* y, int stride, bool resid = fa
     return a;
 }
 
-// One sequence step at the device position *s->dpos for every stream (codebook q's id at
-// ids[q * ids_stride + pos - ids_base]); with `heads`, the step's logits land in s->logits.
-// `position` is the host's view of *s->dpos: it sizes the attention grids (the kernels read
-// the exact key count on the device). Ends by advancing the device position.
+// A projection with its adapter, if any: A x first, from the column the projection builds
+// (its LayerNorm or f32 source; for an activation-form source, `xf` holds the same column in
+// f32), then the GEMV adds s * B(Ax) in its epilogue (lora.h:50-83).
+void gemv_ad(mgx_stream* s, mgx::GemvArgs a, const AdapterW* ad, const float* xf = nullptr, int xf_stride = 0) {
+    if (ad) {
+        mgx::GemvArgs b = ga(ad->A, a.ncol);
+        if (a.pro == mgx::PRO_ACT) {
+            pro_f32(b, xf, xf_stride);
+        } else {
+            b.pro = a.pro; b.x = a.x; b.x_stride = a.x_stride; b.ln_w = a.ln_w; b.ln_b = a.ln_b; b.eps = a.eps;
+        }
+        b.y = s->ax; b.y_stride = ad->rank;
+        mgx::launch_adapter_ax(b, s->hs);
+        a.ad_ax = s->ax; a.ad_B = ad->B; a.ad_m = ad->m; a.ad_norm = ad->norm; a.ad_rank = ad->rank;
+        a.ad_scale = ad->scale; a.ad_strength = ad->strength;
+    }
+    gemv(s, a);
+}
+
+// One sequence step at the device position *s->dpos for every stream: column n belongs to
+// request n / cpr, whose codebook q id sits at ids[r * ids_req_stride + q * ids_stride + pos -
+// ids_base]. With `heads`, the step's logits land in s->logits. `position` is the host's view
+// of *s->dpos: it sizes the attention grids (the kernels read the exact key count on the
+// device). Ends by advancing the device position.
 int att_chunks(int position) { return position / mgx::ATT_CHUNK + 1; }
 
-void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, bool heads, const mgx::SampleArgs* sample,
-          int position) {
+void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int ids_req_stride, bool heads,
+          const mgx::SampleArgs* sample, int position) {
     const mgx_model* m = s->m;
     const mgx_lm_config& c = m->c;
-    const int N = s->n_seq, D = c.dim;
+    const int N = s->n_seq, D = c.dim, R = s->n_req;
     mgx::EmbedArgs e{};
     for (int q = 0; q < c.n_q; ++q) e.emb[q] = m->emb[q];
     e.n_q = c.n_q; e.ids = ids; e.ids_stride = ids_stride; e.ids_base = ids_base; e.table = s->table;
+    e.ids_req_stride = ids_req_stride; e.cols_per_req = s->cpr;
     e.pos = s->dpos; e.dim = D; e.x = s->x; e.ncol = N;
     mgx::launch_embed(e, s->hs);
     const float scale = 1.0f / std::sqrt((float)c.head_dim);
@@ -323,13 +366,14 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, bool 
             pro_ln(a, s->x, D, L.n1w, L.n1b, c.norm_eps);
             a.epi = mgx::EPI_QKV; a.y = s->qb; a.k = Kl; a.v = Vl; a.dim = D; a.heads = c.heads; a.cap = s->kv_rows;
             a.pos = s->dpos;
-            gemv(s, a);
+            gemv_ad(s, a, L.ad[P_QKV]);
         }
         {
             mgx::AttnArgs at{};
             at.q = s->qb; at.k = Kl; at.v = Vl; at.scores = s->scores; at.opart = s->opart; at.cmax = s->cmax;
             at.dim = D; at.heads = c.heads; at.cap = s->kv_rows; at.max_chunks = s->max_chunks; at.ncol = N;
             at.scale = scale; at.pos = s->dpos; at.out = s->act_o.view(L.w[P_OUT].type);
+            at.out_f = L.ad[P_OUT] ? s->act_o.f : nullptr;
             // f32 K and V of every key attended, every stream
             at.stamp = s->stamp_slot(PROF_ATTN, 2.0 * N * c.heads * (position + 1) * 64 * 4);
             mgx::launch_attention(at, att_chunks(position), s->hs);
@@ -338,34 +382,37 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, bool 
             mgx::GemvArgs a = ga(L.w[P_OUT], N);
             pro_act(a, s->act_o.view(L.w[P_OUT].type));
             epi_store(a, s->x, D, true);
-            gemv(s, a);
+            gemv_ad(s, a, L.ad[P_OUT], s->act_o.f, D);
         }
-        // cross-attention, conditional stream only (the null stream's contribution is 0)
+        // cross-attention, each request's conditional stream only (the null stream's
+        // contribution is exactly 0): column r * cpr of x
         if (s->cross) {
-            mgx::GemvArgs a = ga(L.w[P_CQ], 1);
-            pro_ln(a, s->x, D, L.ncw, L.ncb, c.norm_eps);
+            mgx::GemvArgs a = ga(L.w[P_CQ], R);
+            pro_ln(a, s->x, s->cpr * D, L.ncw, L.ncb, c.norm_eps);
             epi_store(a, s->qc, D);
-            gemv(s, a);
+            gemv_ad(s, a, L.ad[P_CQ]);
             mgx::XAttnArgs xa{};
-            xa.q = s->qc; xa.k = s->xk + (size_t)l * c.heads * s->n_ctx * 64;
-            xa.v = s->xv + (size_t)l * c.heads * s->n_ctx * 64; xa.n_ctx = s->n_ctx; xa.scale = scale;
+            const size_t xl = (size_t)l * R * c.heads * s->n_ctx * 64;
+            xa.q = s->qc; xa.k = s->xk + xl; xa.v = s->xv + xl; xa.n_ctx = s->n_ctx; xa.dim = D; xa.scale = scale;
             xa.out = s->act_c.view(L.w[P_COUT].type);
-            mgx::launch_xattn(xa, c.heads, s->hs);
-            mgx::GemvArgs b = ga(L.w[P_COUT], 1);
+            xa.out_f = L.ad[P_COUT] ? s->act_c.f : nullptr;
+            mgx::launch_xattn(xa, c.heads, R, s->hs);
+            mgx::GemvArgs b = ga(L.w[P_COUT], R);
             pro_act(b, s->act_c.view(L.w[P_COUT].type));
-            epi_store(b, s->x, D, true);
-            gemv(s, b);
+            epi_store(b, s->x, s->cpr * D, true);
+            gemv_ad(s, b, L.ad[P_COUT], s->act_c.f, D);
         }
         // feed-forward: LN2 + ff.0 + GELU (quantized in the epilogue), ff.2 + residual
         {
             mgx::GemvArgs a = ga(L.w[P_FF0], N);
             pro_ln(a, s->x, D, L.n2w, L.n2b, c.norm_eps);
             a.epi = mgx::EPI_GELU_ACT; a.dst = s->act_f.view(L.w[P_FF2].type);
-            gemv(s, a);
+            a.dst_f = L.ad[P_FF2] ? s->act_f.f : nullptr;
+            gemv_ad(s, a, L.ad[P_FF0]);
             mgx::GemvArgs b = ga(L.w[P_FF2], N);
             pro_act(b, s->act_f.view(L.w[P_FF2].type));
             epi_store(b, s->x, D, true);
-            gemv(s, b);
+            gemv_ad(s, b, L.ad[P_FF2], s->act_f.f, c.ff_dim);
         }
     }
     if (heads) {
@@ -420,17 +467,29 @@ void validate_tensors(const mgx_lm_config& c, const mgx_tensor* t, int n) {
     }
 }
 
-void make_stream(mgx_model* m, int capacity, int n_seq, const float* t5, int n_ctx, int cross, mgx_stream** out) {
+// A stream of n_seq columns for n_req requests (n_seq / n_req columns each; column r * cpr is
+// request r's conditional stream). With `cross`, t5[r] [n_ctx][cond_dim] is request r's
+// conditioning: projected through lm.cond_proj once and through every layer's cross.kv once.
+void make_stream(mgx_model* m, int capacity, int n_seq, int n_req, const float* const* t5, int n_ctx, int cross,
+                 mgx_stream** out) {
     const mgx_lm_config& c = m->c;
     if (capacity <= 0 || n_seq <= 0) throw Error(MGX_ERR_INVALID, "the kv cache needs positive dimensions");
     if (n_seq > 16) throw Error(MGX_ERR_INVALID, "at most 16 streams per forward");
-    if (cross && (n_ctx <= 0 || !t5)) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
+    if (n_req <= 0 || n_req > mgx::MAX_REQ || n_seq % n_req) throw Error(MGX_ERR_INVALID, "bad request count");
+    if (cross && n_ctx <= 0) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
+    if (cross)
+        for (int r = 0; r < n_req; ++r)
+            if (!t5 || !t5[r]) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
     if (cross && n_ctx > 256) throw Error(MGX_ERR_INVALID, "at most 256 conditioning tokens");
     HIP_OK(hipSetDevice(m->device));
     auto s = std::make_unique<mgx_stream>();
-    s->m = m; s->cap = capacity; s->n_seq = n_seq; s->cross = cross ? 1 : 0; s->n_ctx = cross ? n_ctx : 0;
+    s->m = m;
+    m->live.fetch_add(1);
+    s->cap = capacity; s->n_seq = n_seq; s->cross = cross ? 1 : 0; s->n_ctx = cross ? n_ctx : 0;
+    s->n_req = n_req; s->cpr = n_seq / n_req;
     s->max_chunks = (capacity + mgx::ATT_CHUNK - 1) / mgx::ATT_CHUNK;
     s->kv_rows = s->max_chunks * mgx::ATT_CHUNK;
+    if (s->max_chunks > mgx::ATT_MAX_CHUNKS) throw Error(MGX_ERR_INVALID, "capacity above 4096 positions");
     HIP_OK(hipStreamCreateWithFlags(&s->hs, hipStreamNonBlocking));
     const size_t kv = s->layer_kv() * c.layers;
     s->K = s->mem.alloc<float>(kv);
@@ -442,44 +501,46 @@ void make_stream(mgx_model* m, int capacity, int n_seq, const float* t5, int n_c
     HIP_OK(hipMemcpyAsync(s->table, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice, s->hs));
     s->dpos = s->mem.alloc<int>(1);
     HIP_OK(hipMemsetAsync(s->dpos, 0, sizeof(int), s->hs));
-    if (s->max_chunks > mgx::ATT_MAX_CHUNKS) throw Error(MGX_ERR_INVALID, "capacity above 4096 positions");
     s->cmax = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * mgx::ATT_SUBS);
     s->x = s->mem.alloc<float>((size_t)n_seq * c.dim);
     s->qb = s->mem.alloc<float>((size_t)n_seq * c.dim);
     s->scores = s->mem.alloc<float>((size_t)n_seq * c.heads * s->kv_rows);
     s->opart = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * 64);
     s->logits = s->mem.alloc<float>((size_t)n_seq * c.n_q * c.card);
-    s->qc = s->mem.alloc<float>((size_t)c.dim);
+    s->qc = s->mem.alloc<float>((size_t)n_req * c.dim);
     s->alloc_act(s->act_o, n_seq, c.dim);
-    s->alloc_act(s->act_c, 1, c.dim);
+    s->alloc_act(s->act_c, n_req, c.dim);
     s->alloc_act(s->act_f, n_seq, c.ff_dim);
     s->ids = s->mem.alloc<int32_t>((size_t)c.n_q * capacity);
+    if (m->ad_rank_max > 0) s->ax = s->mem.alloc<float>((size_t)std::max(n_seq, 2) * m->ad_rank_max);
     if (s->cross) {
         // lm.cond_proj . t5 + bias, stream 0 only (pipeline.cpp:144-180), then every layer's
-        // cross.kv of it, once.
+        // cross.kv of it, once per request.
         const int nc = s->n_ctx;
         float* t5d = s->mem.alloc<float>((size_t)nc * c.cond_dim);
-        HIP_OK(hipMemcpyAsync(t5d, t5, sizeof(float) * (size_t)nc * c.cond_dim, hipMemcpyHostToDevice, s->hs));
         float* ctx = s->mem.alloc<float>((size_t)nc * c.dim);
         float* kvp = s->mem.alloc<float>((size_t)nc * 2 * c.dim);
-        s->xk = s->mem.alloc<float>((size_t)c.layers * c.heads * nc * 64);
-        s->xv = s->mem.alloc<float>((size_t)c.layers * c.heads * nc * 64);
-        for (int col = 0; col < nc; ++col) {
-            mgx::GemvArgs a = ga(m->cond_proj, 1);
-            pro_f32(a, t5d + (size_t)col * c.cond_dim, c.cond_dim);
-            epi_store(a, ctx + (size_t)col * c.dim, c.dim);
-            gemv(s.get(), a);
-        }
-        mgx::launch_add_bias(ctx, m->cond_proj_b, c.dim, nc, s->hs);
-        for (int l = 0; l < c.layers; ++l) {
+        s->xk = s->mem.alloc<float>((size_t)c.layers * n_req * c.heads * nc * 64);
+        s->xv = s->mem.alloc<float>((size_t)c.layers * n_req * c.heads * nc * 64);
+        for (int r = 0; r < n_req; ++r) {
+            HIP_OK(hipMemcpyAsync(t5d, t5[r], sizeof(float) * (size_t)nc * c.cond_dim, hipMemcpyHostToDevice, s->hs));
             for (int col = 0; col < nc; ++col) {
-                mgx::GemvArgs a = ga(m->L[(size_t)l].w[P_CKV], 1);
-                pro_f32(a, ctx + (size_t)col * c.dim, c.dim);
-                epi_store(a, kvp + (size_t)col * 2 * c.dim, 2 * c.dim);
+                mgx::GemvArgs a = ga(m->cond_proj, 1);
+                pro_f32(a, t5d + (size_t)col * c.cond_dim, c.cond_dim);
+                epi_store(a, ctx + (size_t)col * c.dim, c.dim);
                 gemv(s.get(), a);
             }
-            mgx::launch_xkv_split(kvp, nc, c.dim, s->xk + (size_t)l * c.heads * nc * 64,
-                                  s->xv + (size_t)l * c.heads * nc * 64, s->hs);
+            mgx::launch_add_bias(ctx, m->cond_proj_b, c.dim, nc, s->hs);
+            for (int l = 0; l < c.layers; ++l) {
+                for (int col = 0; col < nc; ++col) {
+                    mgx::GemvArgs a = ga(m->L[(size_t)l].w[P_CKV], 1);
+                    pro_f32(a, ctx + (size_t)col * c.dim, c.dim);
+                    epi_store(a, kvp + (size_t)col * 2 * c.dim, 2 * c.dim);
+                    gemv_ad(s.get(), a, m->L[(size_t)l].ad[P_CKV]);
+                }
+                const size_t off = ((size_t)l * n_req + r) * c.heads * nc * 64;
+                mgx::launch_xkv_split(kvp, nc, c.dim, s->xk + off, s->xv + off, s->hs);
+            }
         }
     }
     HIP_OK(hipGetLastError());
@@ -546,7 +607,87 @@ int mgx_model_create(const mgx_lm_config* cfg, const mgx_tensor* t, int32_t n, m
 int mgx_model_set_adapters(mgx_model* model, const mgx_adapter* adapters, int32_t n) {
     return guarded([&] {
         if (!model) throw Error(MGX_ERR_INVALID, "null model");
-        if (n != 0 || adapters) throw Error(MGX_ERR_INVALID, "adapters are not supported by this build yet");
+        if (n < 0 || (n > 0 && !adapters)) throw Error(MGX_ERR_INVALID, "bad adapter list");
+        if (model->live.load() != 0)
+            throw Error(MGX_ERR_STATE, "adapters can change only while no stream or session uses the model");
+        const mgx_lm_config& c = model->c;
+        // load_lora / load_mg_lora's checks (lora.h:113-176, 195-210), all before any change
+        struct Slot { int layer, proj; };
+        std::vector<Slot> slots((size_t)n);
+        for (int i = 0; i < n; ++i) {
+            const mgx_adapter& a = adapters[i];
+            const std::string target = a.target ? a.target : "";
+            int li = -1, pi = -1;
+            for (int l = 0; l < c.layers && li < 0; ++l)
+                for (int k = 0; k < P_COUNT; ++k)
+                    if (target == "lm." + std::to_string(l) + "." + PROJ[k] + ".weight") { li = l; pi = k; break; }
+            if (li < 0) throw Error(MGX_ERR_INVALID, "unsupported MusicGen adapter target: " + target);
+            for (int j = 0; j < i; ++j)
+                if (slots[(size_t)j].layer == li && slots[(size_t)j].proj == pi)
+                    throw Error(MGX_ERR_INVALID, "two adapters for " + target);
+            slots[(size_t)i] = {li, pi};
+            if (a.rank <= 0 || !std::isfinite(a.alpha) || a.alpha <= 0 || !std::isfinite(a.strength))
+                throw Error(MGX_ERR_INVALID, "invalid adapter rank, alpha or strength");
+            if (a.rank > 64) throw Error(MGX_ERR_INVALID, "adapter ranks above 64 are not supported");
+            if (!a.A || !a.B) throw Error(MGX_ERR_INVALID, "adapter shape mismatch: " + target);
+            const mgx::DevMat& W = model->L[(size_t)li].w[pi];
+            for (size_t k = 0; k < (size_t)a.rank * W.in; ++k)
+                if (!std::isfinite(a.A[k])) throw Error(MGX_ERR_INVALID, "nonfinite adapter tensor");
+            for (size_t k = 0; k < (size_t)W.out * a.rank; ++k)
+                if (!std::isfinite(a.B[k])) throw Error(MGX_ERR_INVALID, "nonfinite adapter tensor");
+            if (a.magnitude)
+                for (int k = 0; k < W.out; ++k)
+                    if (!std::isfinite(a.magnitude[k])) throw Error(MGX_ERR_INVALID, "nonfinite adapter tensor");
+        }
+        HIP_OK(hipSetDevice(model->device));
+        for (LayerW& L : model->L)
+            for (int k = 0; k < P_COUNT; ++k) L.ad[k] = nullptr;
+        model->ad_mem.release();
+        model->ads.assign((size_t)n, AdapterW{});
+        model->ad_rank_max = 0;
+        if (n == 0) return;
+        hipStream_t hs;
+        HIP_OK(hipStreamCreateWithFlags(&hs, hipStreamNonBlocking));
+        struct StreamGuard { hipStream_t s; ~StreamGuard() { (void)hipStreamSynchronize(s); (void)hipStreamDestroy(s); } } sg{hs};
+        int* bad = model->ad_mem.alloc<int>(1);
+        HIP_OK(hipMemsetAsync(bad, 0, sizeof(int), hs));
+        for (int i = 0; i < n; ++i) {
+            const mgx_adapter& a = adapters[i];
+            AdapterW& w = model->ads[(size_t)i];
+            const mgx::DevMat& W = model->L[(size_t)slots[(size_t)i].layer].w[slots[(size_t)i].proj];
+            w.rank = a.rank;
+            w.scale = (a.magnitude ? 1.0f : a.strength) * a.alpha / (float)a.rank;   // lora.h:142
+            w.strength = a.magnitude ? a.strength : 1.0f;
+            // a zero-strength adapter leaves the projection as it is (lora.h:62)
+            if ((a.magnitude && w.strength == 0.0f) || (!a.magnitude && w.scale == 0.0f)) continue;
+            float* A = model->ad_mem.alloc<float>((size_t)a.rank * W.in);
+            float* B = model->ad_mem.alloc<float>((size_t)W.out * a.rank);
+            HIP_OK(hipMemcpyAsync(A, a.A, sizeof(float) * (size_t)a.rank * W.in, hipMemcpyHostToDevice, hs));
+            HIP_OK(hipMemcpyAsync(B, a.B, sizeof(float) * (size_t)W.out * a.rank, hipMemcpyHostToDevice, hs));
+            w.A.type = mgx::T_F32; w.A.in = W.in; w.A.out = a.rank; w.A.q = A; w.A.d = nullptr;
+            w.B = B;
+            if (a.magnitude) {
+                float* mg = model->ad_mem.alloc<float>((size_t)W.out);
+                HIP_OK(hipMemcpyAsync(mg, a.magnitude, sizeof(float) * (size_t)W.out, hipMemcpyHostToDevice, hs));
+                w.m = mg;
+                w.norm = model->ad_mem.alloc<float>((size_t)W.out);
+                mgx::launch_dora_norm(W, A, B, a.rank, w.scale, w.norm, bad, hs);
+                HIP_OK(hipGetLastError());
+            }
+            model->L[(size_t)slots[(size_t)i].layer].ad[slots[(size_t)i].proj] = &w;
+            model->ad_rank_max = std::max(model->ad_rank_max, a.rank);
+        }
+        int nonfinite = 0;
+        HIP_OK(hipMemcpyAsync(&nonfinite, bad, sizeof(int), hipMemcpyDeviceToHost, hs));
+        HIP_OK(hipStreamSynchronize(hs));
+        if (nonfinite) {
+            for (LayerW& L : model->L)
+                for (int k = 0; k < P_COUNT; ++k) L.ad[k] = nullptr;
+            model->ads.clear();
+            model->ad_rank_max = 0;
+            model->ad_mem.release();
+            throw Error(MGX_ERR_INVALID, "nonfinite DoRA base weight");
+        }
     });
 }
 
@@ -557,7 +698,7 @@ int mgx_stream_create(mgx_model* model, int32_t capacity, int32_t n_seq, const f
     return guarded([&] {
         if (!model || !out) throw Error(MGX_ERR_INVALID, "null argument");
         *out = nullptr;
-        make_stream(model, capacity, n_seq, t5_hidden, n_ctx, cross_attention, out);
+        make_stream(model, capacity, n_seq, 1, &t5_hidden, n_ctx, cross_attention, out);
     });
 }
 
@@ -577,7 +718,7 @@ int mgx_forward(mgx_stream* s, const int32_t* ids, int32_t n_tokens, float* logi
         HIP_OK(hipMemcpyAsync(s->dpos, &used, sizeof(int), hipMemcpyHostToDevice, s->hs));
         // A prefill is the same per-position arithmetic as single steps (its causal mask only
         // adds exact zeros), so the tokens run one position at a time.
-        for (int t = 0; t < n_tokens; ++t) step(s, s->ids, n_tokens, used, t == n_tokens - 1, nullptr, used + t);
+        for (int t = 0; t < n_tokens; ++t) step(s, s->ids, n_tokens, used, 0, t == n_tokens - 1, nullptr, used + t);
         HIP_OK(hipGetLastError());
         if (logits_out)
             HIP_OK(hipMemcpyAsync(logits_out, s->logits, sizeof(float) * (size_t)s->n_seq * c.n_q * c.card,
@@ -606,15 +747,18 @@ void mgx_stream_destroy(mgx_stream* s) { delete s; }
 // ------------------------------------------------------------------------------------
 // generation sessions: mg_generate (pipeline.cpp:199-314) cut into resumable pieces
 // ------------------------------------------------------------------------------------
+// R requests in lockstep (one for mgx_session_create): the same prompt length, generation
+// length, conditioning length and guidance; each its own conditioning, prompt, seed and
+// sampling parameters, KV cache columns and sampler rows.
 struct mgx_session {
     mgx_model* m = nullptr;
     std::unique_ptr<mgx_stream> s;
     DevArena mem;
-    int K = 0, T = 0, S = 0, start = 0, next = 0;   // next: the next loop offset to run
+    int R = 1, K = 0, T = 0, S = 0, start = 0, next = 0;   // next: the next loop offset to run
     bool guided = false;
-    std::vector<int32_t> seq;
+    std::vector<int32_t> seq;                     // [R][K][S]
     int32_t* dseq = nullptr;
-    float *dfirst = nullptr, *dsteps = nullptr;
+    float *dfirst = nullptr, *dsteps = nullptr;   // [R][K][card], [R][S - start][K][card]
     mgx::SampleArgs sa{};
     double prefill_seconds = 0.0, decode_seconds = 0.0;
     int prof_every = 0;
@@ -638,65 +782,82 @@ struct mgx_session {
 
 namespace {
 
-void session_create(mgx_model* m, const float* t5_hidden, int32_t n_ctx, int32_t description_empty,
-                    const int32_t* prompt, int32_t prompt_len, const mgx_generate_params* p, int keep_steps,
-                    mgx_session** out) {
-    if (!m || !p || !out) throw Error(MGX_ERR_INVALID, "null argument");
+void session_create(mgx_model* m, const mgx_batch_request* reqs, int R, int32_t n_ctx, int32_t prompt_len,
+                    int keep_steps, mgx_session** out) {
+    if (!m || !reqs || !out) throw Error(MGX_ERR_INVALID, "null argument");
     *out = nullptr;
     const mgx_lm_config& c = m->c;
-    const int K = c.n_q, T = p->max_gen_len;
-    if (T <= 0) throw Error(MGX_ERR_INVALID, "max_gen_len must be positive");
-    if (prompt_len < 0 || prompt_len >= T) throw Error(MGX_ERR_INVALID, "the prompt must be shorter than the generation");
-    if (prompt_len > 0 && !prompt) throw Error(MGX_ERR_INVALID, "prompt codes do not hold n_q * prompt_len values");
-    if (n_ctx <= 0) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
-    for (int64_t i = 0; i < (int64_t)K * prompt_len; ++i)
-        if (prompt[i] < 0 || prompt[i] >= c.card) throw Error(MGX_ERR_INVALID, "prompt code out of range");
+    if (R <= 0 || R > mgx::MAX_REQ) throw Error(MGX_ERR_INVALID, "a batch holds 1 to 16 requests");
+    const int K = c.n_q, T = reqs[0].params.max_gen_len;
+    // mg_generate's argument checks (pipeline.cpp:204-212), per request
+    for (int r = 0; r < R; ++r) {
+        const mgx_batch_request& q = reqs[r];
+        if (q.params.max_gen_len <= 0) throw Error(MGX_ERR_INVALID, "max_gen_len must be positive");
+        if (q.params.max_gen_len != T) throw Error(MGX_ERR_INVALID, "the requests of a batch share max_gen_len");
+        if (prompt_len < 0 || prompt_len >= T) throw Error(MGX_ERR_INVALID, "the prompt must be shorter than the generation");
+        if (prompt_len > 0 && !q.prompt_codes) throw Error(MGX_ERR_INVALID, "prompt codes do not hold n_q * prompt_len values");
+        if (n_ctx <= 0) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
+        for (int64_t i = 0; i < (int64_t)K * prompt_len; ++i)
+            if (q.prompt_codes[i] < 0 || q.prompt_codes[i] >= c.card) throw Error(MGX_ERR_INVALID, "prompt code out of range");
+        if ((mgx_use_guidance(q.params.cfg_coef, q.description_empty) != 0) !=
+            (mgx_use_guidance(reqs[0].params.cfg_coef, reqs[0].description_empty) != 0))
+            throw Error(MGX_ERR_INVALID, "the requests of a batch are all guided or all unguided");
+    }
     auto ss = std::make_unique<mgx_session>();
-    ss->m = m; ss->K = K; ss->T = T;
+    ss->m = m; ss->R = R; ss->K = K; ss->T = T;
     if (const char* g = std::getenv("MGX_GRAPHS")) ss->use_graphs = std::strcmp(g, "0") != 0;
     // DelayPattern with delays 0..n_q-1 (pattern.h:31-115): S = T + n_q, start = P + 1.
     ss->S = 1 + T + (K - 1);
     ss->start = prompt_len + 1;
     ss->next = ss->start;
     const int S = ss->S, start = ss->start;
-    ss->seq.assign((size_t)K * S, c.special_token_id);
+    ss->guided = mgx_use_guidance(reqs[0].params.cfg_coef, reqs[0].description_empty) != 0;
+    if (R * (ss->guided ? 2 : 1) > 16) throw Error(MGX_ERR_INVALID, "at most 16 streams per batch (8 guided requests)");
     std::vector<uint8_t> mask((size_t)K * S, 0);
     for (int q = 0; q < K; ++q)
-        for (int st = 0; st < S; ++st) {
-            const int t = ss->pattern_t(q, st);
-            if (t < 0) continue;
-            mask[(size_t)q * S + st] = 1;
-            ss->seq[(size_t)q * S + st] = t < prompt_len ? prompt[(size_t)q * prompt_len + t] : -1;
-        }
-    ss->guided = mgx_use_guidance(p->cfg_coef, description_empty) != 0;
-    const bool sampling = p->use_sampling && p->temperature > 0.0f;
+        for (int st = 0; st < S; ++st) mask[(size_t)q * S + st] = ss->pattern_t(q, st) >= 0;
+    ss->seq.assign((size_t)R * K * S, c.special_token_id);
     // The reference draws one uniform per sampled slot, step by step and codebook by
     // codebook (pipeline.cpp:278-288, rng.h:20-22); which slots draw depends only on the
-    // mask, so the whole stream is drawn here.
-    std::vector<float> uni((size_t)S * K, 0.0f);
-    if (sampling) {
-        std::mt19937 g((uint32_t)p->seed);
-        for (int st = start; st < S; ++st)
-            for (int q = 0; q < K; ++q)
-                if (mask[(size_t)q * S + st]) uni[(size_t)st * K + q] = ((g() >> 8) + 0.5f) * (1.0f / 16777216.0f);
+    // mask, so each request's whole stream is drawn here.
+    std::vector<float> uni((size_t)R * S * K, 0.0f);
+    mgx::SampleArgs& sa = ss->sa;
+    for (int r = 0; r < R; ++r) {
+        const mgx_batch_request& rq = reqs[r];
+        int32_t* seq = ss->seq.data() + (size_t)r * K * S;
+        for (int q = 0; q < K; ++q)
+            for (int st = 0; st < S; ++st) {
+                const int t = ss->pattern_t(q, st);
+                if (t >= 0) seq[(size_t)q * S + st] = t < prompt_len ? rq.prompt_codes[(size_t)q * prompt_len + t] : -1;
+            }
+        const mgx_generate_params& p = rq.params;
+        if (p.use_sampling && p.temperature > 0.0f) {
+            std::mt19937 g((uint32_t)p.seed);
+            float* u = uni.data() + (size_t)r * S * K;
+            for (int st = start; st < S; ++st)
+                for (int q = 0; q < K; ++q)
+                    if (mask[(size_t)q * S + st]) u[(size_t)st * K + q] = ((g() >> 8) + 0.5f) * (1.0f / 16777216.0f);
+        }
+        sa.cfg_coef[r] = p.cfg_coef; sa.temperature[r] = p.temperature;
+        sa.use_sampling[r] = p.use_sampling; sa.top_k[r] = p.top_k;
     }
+    std::vector<const float*> t5s((size_t)R);
+    for (int r = 0; r < R; ++r) t5s[(size_t)r] = reqs[r].t5_hidden;
     mgx_stream* raw = nullptr;
-    make_stream(m, S, ss->guided ? 2 : 1, t5_hidden, n_ctx, ss->guided ? 1 : 0, &raw);
+    make_stream(m, S, R * (ss->guided ? 2 : 1), R, t5s.data(), n_ctx, ss->guided ? 1 : 0, &raw);
     ss->s.reset(raw);
     mgx_stream* st = ss->s.get();
     ss->dseq = ss->mem.alloc<int32_t>(ss->seq.size());
     uint8_t* dmask = ss->mem.alloc<uint8_t>(mask.size());
     float* duni = ss->mem.alloc<float>(uni.size());
-    ss->dfirst = ss->mem.alloc<float>((size_t)K * c.card);
-    if (keep_steps) ss->dsteps = ss->mem.alloc<float>((size_t)(S - start) * K * c.card);
+    ss->dfirst = ss->mem.alloc<float>((size_t)R * K * c.card);
+    if (keep_steps) ss->dsteps = ss->mem.alloc<float>((size_t)R * (S - start) * K * c.card);
     HIP_OK(hipMemcpyAsync(ss->dseq, ss->seq.data(), ss->seq.size() * 4, hipMemcpyHostToDevice, st->hs));
     HIP_OK(hipMemcpyAsync(dmask, mask.data(), mask.size(), hipMemcpyHostToDevice, st->hs));
     HIP_OK(hipMemcpyAsync(duni, uni.data(), uni.size() * 4, hipMemcpyHostToDevice, st->hs));
     HIP_OK(hipStreamSynchronize(st->hs));
-    mgx::SampleArgs& sa = ss->sa;
-    sa.logits = st->logits; sa.n_q = K; sa.card = c.card; sa.guided = ss->guided; sa.cfg_coef = p->cfg_coef;
-    sa.mask = dmask; sa.steps = S; sa.use_sampling = p->use_sampling; sa.temperature = p->temperature;
-    sa.top_k = p->top_k; sa.uniforms = duni; sa.special = c.special_token_id; sa.seq = ss->dseq;
+    sa.logits = st->logits; sa.n_q = K; sa.card = c.card; sa.guided = ss->guided; sa.n_req = R;
+    sa.mask = dmask; sa.steps = S; sa.uniforms = duni; sa.special = c.special_token_id; sa.seq = ss->dseq;
     sa.start = start; sa.pos = st->dpos; sa.first_logits = ss->dfirst; sa.step_logits = ss->dsteps;
     *out = ss.release();
 }
@@ -706,7 +867,7 @@ hipGraphExec_t capture(mgx_session* ss, bool full, int position) {
     hipGraph_t g = nullptr;
     hipGraphExec_t e = nullptr;
     HIP_OK(hipStreamBeginCapture(s->hs, hipStreamCaptureModeThreadLocal));
-    step(s, ss->dseq, ss->S, 0, full, full ? &ss->sa : nullptr, position);
+    step(s, ss->dseq, ss->S, 0, ss->K * ss->S, full, full ? &ss->sa : nullptr, position);
     HIP_OK(hipStreamEndCapture(s->hs, &g));
     const hipError_t rc = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
@@ -720,12 +881,12 @@ void run_position(mgx_session* ss, bool full, bool profiled, int position) {
     if (profiled) {
         s->prof_on = true;
         s->prof_pos = position;
-        step(s, ss->dseq, ss->S, 0, full, full ? &ss->sa : nullptr, position);
+        step(s, ss->dseq, ss->S, 0, ss->K * ss->S, full, full ? &ss->sa : nullptr, position);
         s->prof_on = false;
         return;
     }
     if (!ss->use_graphs) {
-        step(s, ss->dseq, ss->S, 0, full, full ? &ss->sa : nullptr, position);
+        step(s, ss->dseq, ss->S, 0, ss->K * ss->S, full, full ? &ss->sa : nullptr, position);
         return;
     }
     hipGraphExec_t& g = (full ? ss->g_step : ss->g_body)[att_chunks(position) - 1];
@@ -766,37 +927,50 @@ int session_step(mgx_session* ss, int n) {
     return done;
 }
 
-void session_finish(mgx_session* ss, int32_t* codes_out, float* first_logits_out, float* step_logits_out,
+void session_finish(mgx_session* ss, int req, int32_t* codes_out, float* first_logits_out, float* step_logits_out,
                     mgx_generate_report* rep) {
     const mgx_lm_config& c = ss->m->c;
     mgx_stream* s = ss->s.get();
     const int K = ss->K, T = ss->T, S = ss->S;
+    if (req < 0 || req >= ss->R) throw Error(MGX_ERR_INVALID, "request index out of range");
     if (rep) {
         rep->prefill_tokens = ss->start;
         rep->decode_steps = S - ss->start - 1;
         rep->forwards = ss->next - ss->start;
         rep->prefill_seconds = ss->prefill_seconds;
         rep->decode_seconds = ss->decode_seconds;
-        rep->cache_bytes = mgx_stream_cache_bytes(s);
+        rep->cache_bytes = mgx_stream_cache_bytes(s) / (uint64_t)ss->R;
     }
-    HIP_OK(hipMemcpy(ss->seq.data(), ss->dseq, ss->seq.size() * 4, hipMemcpyDeviceToHost));
+    const size_t per = (size_t)K * S;
+    HIP_OK(hipMemcpy(ss->seq.data() + req * per, ss->dseq + req * per, per * 4, hipMemcpyDeviceToHost));
     if (first_logits_out && ss->next > ss->start)
-        HIP_OK(hipMemcpy(first_logits_out, ss->dfirst, sizeof(float) * (size_t)K * c.card, hipMemcpyDeviceToHost));
-    if (step_logits_out && ss->dsteps)
-        HIP_OK(hipMemcpy(step_logits_out, ss->dsteps, sizeof(float) * (size_t)(S - ss->start) * K * c.card,
+        HIP_OK(hipMemcpy(first_logits_out, ss->dfirst + (size_t)req * K * c.card, sizeof(float) * (size_t)K * c.card,
                          hipMemcpyDeviceToHost));
+    if (step_logits_out && ss->dsteps) {
+        const size_t n = (size_t)(S - ss->start) * K * c.card;
+        HIP_OK(hipMemcpy(step_logits_out, ss->dsteps + req * n, sizeof(float) * n, hipMemcpyDeviceToHost));
+    }
     if (!codes_out) return;
     // revert_pattern_sequence + the final check (pipeline.cpp:307-313)
+    const int32_t* seq = ss->seq.data() + req * per;
     for (size_t i = 0; i < (size_t)K * T; ++i) codes_out[i] = c.special_token_id;
     for (int q = 0; q < K; ++q)
         for (int st = 0; st < S; ++st) {
             const int t = ss->pattern_t(q, st);
-            if (t >= 0) codes_out[(size_t)q * T + t] = ss->seq[(size_t)q * S + st];
+            if (t >= 0) codes_out[(size_t)q * T + t] = seq[(size_t)q * S + st];
         }
     if (ss->next == S)
         for (size_t i = 0; i < (size_t)K * T; ++i)
             if (codes_out[i] < 0 || codes_out[i] >= c.card)
                 throw Error(MGX_ERR_INVALID, "the generated sequence has a position the pattern never filled");
+}
+
+mgx_batch_request one_request(const float* t5_hidden, int32_t description_empty, const int32_t* prompt,
+                              const mgx_generate_params* p) {
+    if (!p) throw Error(MGX_ERR_INVALID, "null argument");
+    mgx_batch_request r{};
+    r.t5_hidden = t5_hidden; r.description_empty = description_empty; r.prompt_codes = prompt; r.params = *p;
+    return r;
 }
 
 }  // namespace
@@ -807,7 +981,8 @@ int mgx_session_create(mgx_model* m, const float* t5_hidden, int32_t n_ctx, int3
                        const int32_t* prompt_codes, int32_t prompt_len, const mgx_generate_params* params,
                        int32_t keep_step_logits, mgx_session** out) {
     return guarded([&] {
-        session_create(m, t5_hidden, n_ctx, description_empty, prompt_codes, prompt_len, params, keep_step_logits, out);
+        const mgx_batch_request r = one_request(t5_hidden, description_empty, prompt_codes, params);
+        session_create(m, &r, 1, n_ctx, prompt_len, keep_step_logits, out);
     });
 }
 
@@ -825,9 +1000,24 @@ int mgx_session_finish(mgx_session* ss, int32_t* codes_out, float* first_logits_
                        mgx_generate_report* report) {
     return guarded([&] {
         if (!ss) throw Error(MGX_ERR_INVALID, "null session");
-        session_finish(ss, codes_out, first_logits_out, step_logits_out, report);
+        session_finish(ss, 0, codes_out, first_logits_out, step_logits_out, report);
     });
 }
+
+int mgx_batch_create(mgx_model* m, const mgx_batch_request* requests, int32_t n_requests, int32_t n_ctx,
+                     int32_t prompt_len, int32_t keep_step_logits, mgx_session** out) {
+    return guarded([&] { session_create(m, requests, n_requests, n_ctx, prompt_len, keep_step_logits, out); });
+}
+
+int mgx_batch_finish(mgx_session* ss, int32_t request, int32_t* codes_out, float* first_logits_out,
+                     float* step_logits_out, mgx_generate_report* report) {
+    return guarded([&] {
+        if (!ss) throw Error(MGX_ERR_INVALID, "null session");
+        session_finish(ss, request, codes_out, first_logits_out, step_logits_out, report);
+    });
+}
+
+int32_t mgx_session_requests(const mgx_session* ss) { return ss ? ss->R : -1; }
 
 int mgx_session_profile(mgx_session* ss, int32_t every) {
     return guarded([&] {
@@ -884,10 +1074,11 @@ int mgx_generate(mgx_model* m, const float* t5_hidden, int32_t n_ctx, int32_t de
     return guarded([&] {
         if (!codes_out || !rep) throw Error(MGX_ERR_INVALID, "null argument");
         mgx_session* raw = nullptr;
-        session_create(m, t5_hidden, n_ctx, description_empty, prompt, prompt_len, p, step_logits_out != nullptr, &raw);
+        const mgx_batch_request r = one_request(t5_hidden, description_empty, prompt, p);
+        session_create(m, &r, 1, n_ctx, prompt_len, step_logits_out != nullptr, &raw);
         std::unique_ptr<mgx_session> ss(raw);
         session_step(ss.get(), ss->S);
-        session_finish(ss.get(), codes_out, first_logits_out, step_logits_out, rep);
+        session_finish(ss.get(), 0, codes_out, first_logits_out, step_logits_out, rep);
     });
 }
 

@@ -40,6 +40,12 @@ class GenerateParams(C.Structure):
                 ("top_k", C.c_int32), ("cfg_coef", C.c_float), ("seed", C.c_uint64)]
 
 
+class BatchRequest(C.Structure):
+    """mgx_batch_request: one request of a lockstep batch."""
+    _fields_ = [("t5_hidden", C.c_void_p), ("description_empty", C.c_int32), ("prompt_codes", C.c_void_p),
+                ("params", GenerateParams)]
+
+
 class GenerateReport(C.Structure):
     _fields_ = [("cache_bytes", C.c_uint64), ("prefill_tokens", C.c_int32), ("decode_steps", C.c_int32),
                 ("forwards", C.c_int32), ("prefill_seconds", C.c_double), ("decode_seconds", C.c_double)]
@@ -49,7 +55,8 @@ EXPORTS = ["mgx_model_create", "mgx_model_set_adapters", "mgx_model_destroy", "m
            "mgx_stream_reset", "mgx_stream_used", "mgx_stream_forwards", "mgx_stream_cache_bytes",
            "mgx_stream_destroy", "mgx_use_guidance", "mgx_generate", "mgx_session_create", "mgx_session_step",
            "mgx_session_remaining", "mgx_session_finish", "mgx_session_destroy", "mgx_session_profile",
-           "mgx_session_profile_read", "mgx_session_hip_stream", "mgx_last_error"]
+           "mgx_session_profile_read", "mgx_session_hip_stream", "mgx_batch_create", "mgx_batch_finish",
+           "mgx_session_requests", "mgx_last_error"]
 
 _lib = None
 
@@ -93,6 +100,10 @@ def load(path=None):
                                              C.POINTER(C.c_int32)]
     lib.mgx_session_hip_stream.restype = P
     lib.mgx_session_hip_stream.argtypes = [P]
+    lib.mgx_batch_create.argtypes = [P, C.POINTER(BatchRequest), C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                     C.POINTER(P)]
+    lib.mgx_batch_finish.argtypes = [P, C.c_int32, P, P, P, C.POINTER(GenerateReport)]
+    lib.mgx_session_requests.argtypes = [P]
     if path is None:
         _lib = lib
     return lib
@@ -130,6 +141,27 @@ class Model:
         h = C.c_void_p()
         _check(self.lib, self.lib.mgx_model_create(C.byref(config), arr, len(tensors), C.byref(h)))
         self.handle = h
+
+    def set_adapters(self, adapters):
+        """mgx_model_set_adapters. adapters: dicts with target, A [rank][in], B [out][rank],
+        magnitude [out] or None, alpha, strength (rank is A's row count). [] detaches."""
+        arr = (Adapter * max(1, len(adapters)))()
+        keep = []
+        for i, a in enumerate(adapters):
+            A = np.ascontiguousarray(a["A"], np.float32)
+            B = np.ascontiguousarray(a["B"], np.float32)
+            m = a.get("magnitude")
+            m = None if m is None else np.ascontiguousarray(m, np.float32)
+            t = a["target"].encode()
+            keep += [A, B, m, t]
+            arr[i].target = t
+            arr[i].A = A.ctypes.data
+            arr[i].B = B.ctypes.data
+            arr[i].magnitude = None if m is None else m.ctypes.data
+            arr[i].rank = int(a.get("rank", A.shape[0]))
+            arr[i].alpha = float(a["alpha"])
+            arr[i].strength = float(a.get("strength", 1.0))
+        _check(self.lib, self.lib.mgx_model_set_adapters(self.handle, arr if adapters else None, len(adapters)))
 
     def close(self):
         if self.handle:
@@ -266,3 +298,50 @@ class Session:
             self.close()
         except Exception:
             pass
+
+
+class Batch(Session):
+    """mgx_batch_*: several requests decoded in lockstep, one KV cache column set each.
+
+    requests: dicts with t5 [n_ctx][cond_dim], prompt [n_q][prompt_len], params
+    (GenerateParams) and optionally description_empty."""
+
+    def __init__(self, model, requests, prompt_len, keep_step_logits=False):
+        self.lib = model.lib
+        self.model = model
+        self.params = requests[0]["params"]
+        self.prompt_len = prompt_len
+        self.keep = keep_step_logits
+        self.n = len(requests)
+        arr = (BatchRequest * self.n)()
+        self._keep = []
+        n_ctx = None
+        for i, r in enumerate(requests):
+            t5 = np.ascontiguousarray(r["t5"], np.float32)
+            n_ctx = t5.shape[0] if n_ctx is None else n_ctx
+            prompt = np.ascontiguousarray(r["prompt"], np.int32) if prompt_len else None
+            self._keep += [t5, prompt]
+            arr[i].t5_hidden = t5.ctypes.data
+            arr[i].description_empty = 1 if r.get("description_empty") else 0
+            arr[i].prompt_codes = None if prompt is None else prompt.ctypes.data
+            arr[i].params = r["params"]
+        h = C.c_void_p()
+        _check(self.lib, self.lib.mgx_batch_create(model.handle, arr, self.n, n_ctx, prompt_len,
+                                                   1 if keep_step_logits else 0, C.byref(h)))
+        self.handle = h
+
+    def requests(self):
+        return self.lib.mgx_session_requests(self.handle)
+
+    def finish(self, request=0):
+        c = self.model.config
+        T = self.params.max_gen_len
+        S = T + c.n_q
+        start = self.prompt_len + 1
+        codes = np.zeros((c.n_q, T), np.int32)
+        first = np.zeros((c.n_q, c.card), np.float32)
+        steps = np.zeros((S - start, c.n_q, c.card), np.float32) if self.keep else None
+        rep = GenerateReport()
+        _check(self.lib, self.lib.mgx_batch_finish(self.handle, request, _ptr(codes), _ptr(first), _ptr(steps),
+                                                   C.byref(rep)))
+        return codes, first, rep, steps

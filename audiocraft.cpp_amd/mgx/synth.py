@@ -78,6 +78,40 @@ def synth_codes(seed, n_q, length, card=2048):
     return out
 
 
+# The projections an adapter may target (lora.h:201-202) and their (in, out) widths.
+def adapter_shapes(config):
+    d, f = config.dim, config.ff_dim
+    return {"self.qkv": (d, 3 * d), "self.out": (d, d), "cross.q": (d, d), "cross.kv": (d, 2 * d),
+            "cross.out": (d, d), "ff.0": (d, f), "ff.2": (f, d)}
+
+
+def synth_adapters(config, rank=16, targets=("self.qkv", "ff.0", "ff.2"), dora=True, alpha=None, strength=1.0,
+                   seed=0):
+    """Rank-`rank` adapters on `targets` of every layer, as dicts for Model.set_adapters:
+    A [rank][in] and B [out][rank] N(0, 0.01); for DoRA rows a magnitude [out] U(0.9, 1.1).
+    alpha defaults to rank (scale 1). Streams are seeded per tensor name, as the weights are
+    (stem + ".lora_A" / ".lora_B" / ".magnitude", the adapter GGUF names of lora.h:125-150)."""
+    lib = _lib()
+    widths = adapter_shapes(config)
+    out = []
+    for l in range(config.layers):
+        for t in targets:
+            i, o = widths[t]
+            stem = f"lm.{l}.{t}.weight"
+            A = np.empty((rank, i), np.float32)
+            B = np.empty((o, rank), np.float32)
+            lib.mgx_synth_normal(lib.mgx_synth_seed(seed, (stem + ".lora_A").encode()), 0.01, A.ctypes.data, A.size)
+            lib.mgx_synth_normal(lib.mgx_synth_seed(seed, (stem + ".lora_B").encode()), 0.01, B.ctypes.data, B.size)
+            a = dict(target=stem, rank=rank, alpha=float(rank if alpha is None else alpha), strength=float(strength),
+                     A=A, B=B, magnitude=None)
+            if dora:
+                u = np.empty(o, np.int32)
+                lib.mgx_synth_codes(lib.mgx_synth_seed(seed, (stem + ".magnitude").encode()), 1 << 24, u.ctypes.data, o)
+                a["magnitude"] = (0.9 + 0.2 * ((u.astype(np.float64) + 0.5) / float(1 << 24))).astype(np.float32)
+            out.append(a)
+    return out
+
+
 def pack(ttype, x):
     """Packs a float32 [rows][ne0] array into ggml bytes of `ttype`."""
     x = np.ascontiguousarray(x, np.float32)

@@ -74,9 +74,13 @@ typedef struct mgx_adapter {
    HIP device once. `tensors` may be freed after the call. */
 int mgx_model_create(const mgx_lm_config* cfg, const mgx_tensor* tensors, int32_t n_tensors, mgx_model** out);
 
-/* Attaches adapters (load_mg_lora, lora.h:195-210) for every later forward. DoRA rows on a
-   quantized base use the dequantized base rows for ||W||^2 (the reference throws there,
-   lora.h:11-13). n == 0 detaches. */
+/* Attaches adapters (load_mg_lora, lora.h:195-210) for every stream and session created
+   afterwards; the reference passes its LoraMap to mg_generate (pipeline.h:63-67). Checks as
+   load_lora does (lora.h:113-176): a supported target, rank > 0, finite alpha > 0 and
+   strength, finite A, B and magnitude; in addition rank <= 64 and one adapter per target.
+   DoRA rows on a quantized base use the dequantized base rows for ||W||^2 (the reference
+   throws there, lora.h:11-13). n == 0 detaches. MGX_ERR_STATE while any stream or session of
+   the model exists. The host arrays may be freed after the call. */
 int mgx_model_set_adapters(mgx_model* model, const mgx_adapter* adapters, int32_t n);
 
 void mgx_model_destroy(mgx_model* model);
@@ -153,6 +157,26 @@ int32_t mgx_session_remaining(const mgx_session* session);
 int mgx_session_finish(mgx_session* session, int32_t* codes_out, float* first_logits_out, float* step_logits_out,
                        mgx_generate_report* report);
 void mgx_session_destroy(mgx_session* session);
+
+/* Batched decode of several requests in lockstep (no reference counterpart: the reference
+   runs one job at a time, src/serve/http.h:201-205; each request is mg_generate,
+   pipeline.cpp:199-314). The requests share the prompt length, max_gen_len, the conditioning
+   length n_ctx and whether guidance is on (mg_use_guidance); each has its own conditioning,
+   prompt, seed, sampling parameters and cfg_coef, and its own KV cache. At most 16 streams:
+   16 unguided or 8 guided requests. Every request's codes, first logits and per-step logits
+   equal those of mgx_generate on that request alone. Step, profile and destroy through the
+   mgx_session_* calls; mgx_session_finish reads request 0. */
+typedef struct mgx_batch_request {
+    const float* t5_hidden;          /* [n_ctx][cond_dim] */
+    int32_t description_empty;
+    const int32_t* prompt_codes;     /* [n_q][prompt_len] */
+    mgx_generate_params params;
+} mgx_batch_request;
+int mgx_batch_create(mgx_model* model, const mgx_batch_request* requests, int32_t n_requests, int32_t n_ctx,
+                     int32_t prompt_len, int32_t keep_step_logits, mgx_session** out);
+int mgx_batch_finish(mgx_session* session, int32_t request, int32_t* codes_out, float* first_logits_out,
+                     float* step_logits_out, mgx_generate_report* report);
+int32_t mgx_session_requests(const mgx_session* session);
 
 /* Launch timing (no reference counterpart; the reference has wall clocks only,
    pipeline.cpp:15-18): with every > 0, each GEMV (kind 0) and self-attention (kind 1) launch
