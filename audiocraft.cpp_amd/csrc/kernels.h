@@ -21,20 +21,27 @@ constexpr int MAX_CARD = 2048;   // sampler's LDS rows
 
 // A weight matrix in device layout: `out` rows of `in`. Q8_0: int8 q[out][in] + fp16
 // d[out][in/32]; Q4_0: the 16 nibble bytes of each block q[out][in/2] + d; F16 / F32: q only.
+// For the matrix-core GEMV (Q8_0, or null): dt, the scales tile-transposed [out/16][in/32][16];
+// qm, the quants again in operand order [out/16][in/32][64 lanes][8]: lane 16g + c holds row
+// 16 * tile + c, bytes 8g..8g+7 of the block -- one wave load is 512 contiguous bytes.
 struct DevMat {
     int type, in, out;
     const void* q;
     const uint16_t* d;
+    const uint16_t* dt;
+    const int8_t* qm;
 };
 
 // Activation columns in the form the consuming weights multiply against.
 struct ActBuf {
     int kind;      // ACT_Q8 / ACT_F16 / ACT_F32
     int stride;    // elements per column
-    int8_t* q;     // Q8 quants [col][stride]
-    float* d;      // Q8 scales [col][stride/32] (fp16 values widened)
+    int8_t* q;     // Q8 quants [col][stride]; block-major: [stride/32][4 g][16 col][8], element
+                   // 32b + 8g + j of column c at (b * 64 + 16g + c) * 8 + j (matrix-core operand order)
+    float* d;      // Q8 scales [col][stride/32] (fp16 values widened); block-major: [stride/32][16 col]
     uint16_t* h;   // fp16 [col][stride]
     float* f;      // f32 [col][stride]
+    int bm;        // Q8 block-major (the matrix-core GEMV's source; at most 16 columns)
 };
 
 struct EmbedArgs {
@@ -123,7 +130,20 @@ struct SampleArgs {
 };
 
 void launch_embed(const EmbedArgs& a, hipStream_t s);
+// A GEMV launch (the matrix-core kernel when gemv_mf_ok, otherwise the vector kernels in groups
+// of two columns).
 void launch_gemv(const GemvArgs& a, hipStream_t s);
+// True when launch_gemv runs `a` on the matrix cores: Q8_0 weights with dt and qm, 3 to 16
+// columns, a supported width, rows a multiple of the tile, a PRO_ACT source in block-major Q8.
+bool gemv_mf_ok(const GemvArgs& a);
+// Q8 activation columns from f32 ones for a matrix-core GEMV: a.x / x_stride (+ LayerNorm
+// a.ln_w / ln_b / eps when a.pro == PRO_LN) -> a.dst (block-major Q8, stride a.w.in), exactly as
+// the vector GEMV's prologue builds them; a.ncol columns. With a.w.q set (an adapter's A, f32
+// [rank][in]) it also writes A x of the same columns to a.y [col][a.y_stride].
+void launch_act_prep(const GemvArgs& a, hipStream_t s);
+// dt from d, and qm from q, for a Q8_0 matrix (out a multiple of 16)
+void launch_scales_t(const DevMat& w, uint16_t* dt, hipStream_t s);
+void launch_weights_mf(const DevMat& w, int8_t* qm, hipStream_t s);
 // nch: the 256-key chunks of the position the launch runs at (the grid covers exactly these)
 void launch_attention(const AttnArgs& a, int nch, hipStream_t s);
 void launch_xattn(const XAttnArgs& a, int heads, int n_req, hipStream_t s);

@@ -128,9 +128,17 @@ __device__ __forceinline__ void quant_q8_lane(float v, int lane, int8_t* qdst, f
     if ((lane & 31) == 0) *ddst = h2f(f2h(d));
 }
 
+// Byte offset of element i of column col in a block-major Q8 buffer: block i / 32 holds 512
+// bytes in matrix-core operand order [g = (i % 32) / 8][col][i % 8].
+__device__ __forceinline__ size_t bm_off(int col, int i) {
+    return (size_t)(i >> 5) * 512 + ((i >> 3) & 3) * 128 + col * 8 + (i & 7);
+}
+
 // Writes element i (of a column) in the activation form the consumer's weights want.
 __device__ __forceinline__ void put_act(const ActBuf& a, int col, int i, float v, int lane) {
-    if (a.kind == ACT_Q8) quant_q8_lane(v, lane, a.q + (size_t)col * a.stride + i, a.d + (size_t)col * (a.stride / 32) + i / 32);
+    if (a.kind == ACT_Q8 && a.bm)
+        quant_q8_lane(v, lane, a.q + bm_off(col, i), a.d + (size_t)(i / 32) * 16 + col);
+    else if (a.kind == ACT_Q8) quant_q8_lane(v, lane, a.q + (size_t)col * a.stride + i, a.d + (size_t)col * (a.stride / 32) + i / 32);
     else if (a.kind == ACT_F16) a.h[(size_t)col * a.stride + i] = f2h(v);
     else a.f[(size_t)col * a.stride + i] = v;
 }
@@ -280,11 +288,12 @@ __device__ __forceinline__ void stamp_end(unsigned long long* p, unsigned long l
 }
 
 struct LdsAct {
-    int8_t* q;     // Q8 [col][in]
+    int8_t* q;     // Q8 [col][in]  (bm_col >= 0: global block-major, column bm_col)
     float* d;      // Q8 [col][in/32]
     uint16_t* h;   // F16 [col][in]
     float* f;      // F32 [col][in]
     int in;
+    int bm_col;
 };
 
 template <int WT> struct WUnit;
@@ -469,7 +478,10 @@ __device__ __forceinline__ void prologue(const GemvArgs& a, const LdsAct& x, dou
                                 | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.y * id) << 8
                                 | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.z * id) << 16
                                 | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.w * id) << 24;
-            if (f < nf) {
+            if (f < nf && x.bm_col >= 0) {
+                *(uint32_t*)(x.q + bm_off(x.bm_col, 4 * f)) = word;
+                if ((lane & 7) == 0) x.d[(size_t)(f / 8) * 16 + x.bm_col] = h2f(f2h(d));
+            } else if (f < nf) {
                 *(uint32_t*)(x.q + (size_t)n * in + 4 * f) = word;
                 if ((lane & 7) == 0) x.d[(size_t)n * nb + f / 8] = h2f(f2h(d));
             }
@@ -489,9 +501,8 @@ __device__ __forceinline__ void prologue(const GemvArgs& a, const LdsAct& x, dou
 // as f32 with rank k -> partial (k>>3) mod 64 (fmaf in order) folded by the 64-wide butterfly
 // (partials >= 8 are zero: the first three levels add +0.0f), times s; v = base + lo; DoRA
 // rows v *= m[row] / norm[row]; strength blend base + (v - base) * strength.
-__device__ __forceinline__ float adapt(const GemvArgs& a, int row, int col, float base) {
-    const float* bp = a.ad_B + (size_t)row * a.ad_rank;
-    const float* xp = a.ad_ax + (size_t)col * a.ad_rank;
+__device__ __forceinline__ float adapt_from(const GemvArgs& a, const float* bp, const float* xp, float m, float norm,
+                                            float base) {
     float part[8];
 #pragma unroll
     for (int l = 0; l < 8; ++l) part[l] = 0.0f;
@@ -505,10 +516,14 @@ __device__ __forceinline__ float adapt(const GemvArgs& a, int row, int col, floa
     const float lo = part[0] * a.ad_scale;
     float v = base + lo;
     if (a.ad_m) {
-        v = v * (a.ad_m[row] / a.ad_norm[row]);
+        v = v * (m / norm);
         if (a.ad_strength != 1.0f) v = base + (v - base) * a.ad_strength;
     }
     return v;
+}
+__device__ __forceinline__ float adapt(const GemvArgs& a, int row, int col, float base) {
+    return adapt_from(a, a.ad_B + (size_t)row * a.ad_rank, a.ad_ax + (size_t)col * a.ad_rank,
+                      a.ad_m ? a.ad_m[row] : 1.0f, a.ad_m ? a.ad_norm[row] : 1.0f, base);
 }
 
 // U > 0: every lane owns exactly U units (units == G * U). U == 0: any unit count, a runtime
@@ -529,6 +544,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
     const int row_ld = row < out ? row : out - 1;
     LdsAct x;
     x.in = in;
+    x.bm_col = -1;
     x.q = (int8_t*)lds; x.d = (float*)(lds + (size_t)NC * in); x.h = (uint16_t*)lds; x.f = (float*)lds;
     float* tile = (float*)(lds + lds_act_bytes(WT, NC, in));
     double* red = (double*)(lds + lds_act_bytes(WT, NC, in) + (size_t)NC * R * 4);
@@ -671,7 +687,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
                 int8_t qv;
                 float dv;
                 quant_q8_lane(g, lane, &qv, &dv);
-                if (lane < 32) {
+                if (lane < 32 && d.bm) {
+                    d.q[bm_off(n, o)] = qv;
+                    if (lane == 0) d.d[(size_t)(o / 32) * 16 + n] = dv;
+                } else if (lane < 32) {
                     d.q[(size_t)n * d.stride + o] = qv;
                     if (lane == 0) d.d[(size_t)n * (d.stride / 32) + o / 32] = dv;
                 }
@@ -1272,6 +1291,197 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
     stamp_end(a.stamp, t0);
 }
 
+// ------------------------------------------------------------------------------------
+// multi-column Q8_0 GEMV on the matrix cores (3 to 16 activation columns)
+// ------------------------------------------------------------------------------------
+// The integer dot product of each 32-element block, for 16 rows x 16 columns, is one
+// v_mfma_i32_16x16x32_i8 (exact: integer sums). The float terms (float)isum * (dw * dx) are
+// then summed as every GEMV sums them: partial b mod 64 in increasing b, the 64 partials
+// folded by the butterfly (offsets 32..1). Wave w of KW owns the partials p = w (mod KW), whose
+// butterfly is a subtree of the full one: it visits them in the subtree's in-order (bit-
+// reversed) order and merges finished subtrees as a binary counter does, which performs the
+// same additions on the same operands; the KW subtree sums meet in LDS for the top levels.
+// Lane (g, c) = (lane / 16, lane % 16) feeds row c / column c, bytes 8g..8g+7 of each block,
+// and receives rows 4g..4g+3 of column c. Activations come in Q8 form from global memory;
+// weight scales from the tile-transposed copy dt.
+typedef int mf_v4i __attribute__((ext_vector_type(4)));
+
+template <int BITS>
+__host__ __device__ constexpr int bitrev(int j) {
+    int r = 0;
+    for (int k = 0; k < BITS; ++k) r |= ((j >> k) & 1) << (BITS - 1 - k);
+    return r;
+}
+template <int N>
+__host__ __device__ constexpr int ilog2() { return N <= 1 ? 0 : 1 + ilog2<N / 2>(); }
+
+template <int NB, int KW, int TILES, int EPI>
+__global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
+    constexpr int M = 64 / KW;                        // leaves (partials) per wave
+    constexpr int LB = ilog2<M>();
+    constexpr int S = NB >= 64 ? NB / 64 : 1;         // blocks per partial
+    constexpr int NVL = NB >= 64 ? M : NB / KW;       // leaves with blocks: i < NVL
+    constexpr int ROWS = 16 * TILES, NT = 64 * KW;
+    static_assert(NB % KW == 0 && (NB < 64 || NB % 64 == 0), "unsupported width");
+    static_assert(EPI != EPI_GELU_ACT || ROWS == 32, "GELU blocks quantize whole 32-row blocks");
+    __shared__ float red[KW][ROWS][17];
+    // adapter operands: the tile's B rows, every column's A x (rank <= 64), DoRA m and norm
+    constexpr int AD_MAX = (ROWS + 16) * 64 + 2 * ROWS, AD_PER = (AD_MAX + 64 * KW - 1) / (64 * KW);
+    __shared__ float adsh[AD_MAX];
+    const unsigned long long t0 = stamp_begin(a.stamp);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    const int row0 = blockIdx.x * ROWS, ncol = a.ncol;
+    const ActBuf& x = a.src;
+    const int8_t* Wm = a.w.qm;
+    // 1. every load of the wave, in visiting order (a leaf's weights, activations and scales
+    //    together, so its products can start while later leaves are still loading)
+    uint2 wa[TILES][M][S], xb[M][S], dw[TILES][M][S];
+    float xd[M][S];
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+        const int i = bitrev<LB>(j);
+        if (i >= NVL) continue;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int b = w + KW * i + 64 * s;
+#pragma unroll
+            for (int t = 0; t < TILES; ++t)
+                wa[t][j][s] = *(const uint2*)(Wm + (((size_t)(row0 / 16 + t) * NB + b) * 64 + lane) * 8);
+            xb[j][s] = *(const uint2*)(x.q + ((size_t)b * 64 + lane) * 8);
+            xd[j][s] = x.d[(size_t)b * 16 + c16];
+#pragma unroll
+            for (int t = 0; t < TILES; ++t)
+                dw[t][j][s] = *(const uint2*)(a.w.dt + ((size_t)(row0 / 16 + t) * NB + b) * 16 + 4 * g);
+        }
+    }
+    // adapter operands behind the weights (used only in the epilogue)
+    const int ad_nb = a.ad_ax ? ROWS * a.ad_rank : 0, ad_nx = a.ad_ax ? ad_nb + ncol * a.ad_rank : 0;
+    const int ad_n = ad_nx + (a.ad_ax && a.ad_m ? 2 * ROWS : 0);
+    float adr[AD_PER];
+#pragma unroll
+    for (int k = 0; k < AD_PER; ++k) {
+        const int e = tid + 64 * KW * k;
+        adr[k] = e < ad_nb ? a.ad_B[(size_t)row0 * a.ad_rank + e]
+               : e < ad_nx ? a.ad_ax[e - ad_nb]
+               : e < ad_nx + ROWS ? (e < ad_n ? a.ad_m[row0 + e - ad_nx] : 0.0f)
+               : (e < ad_n ? a.ad_norm[row0 + e - ad_nx - ROWS] : 0.0f);
+    }
+    // keep every load above in flight together: the scheduler would otherwise sink each next
+    // to its first use and pay the memory latency once per leaf
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. every block's integer products first (independent matrix-core issues), then the
+    //    leaves in order, merged as a binary counter
+    mf_v4i pr[TILES][M][S];
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+        if (bitrev<LB>(j) >= NVL) continue;
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int t = 0; t < TILES; ++t) {
+                const mf_v4i z = {0, 0, 0, 0};
+                pr[t][j][s] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                    (long)(((unsigned long long)wa[t][j][s].y << 32) | wa[t][j][s].x),
+                    (long)(((unsigned long long)xb[j][s].y << 32) | xb[j][s].x), z, 0, 0, 0);
+            }
+    }
+    float4 lev[TILES][LB + 1];
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+        const int i = bitrev<LB>(j);
+        float4 leaf[TILES];
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) leaf[t] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < NVL) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+#pragma unroll
+                for (int t = 0; t < TILES; ++t) {
+                    const mf_v4i r = pr[t][j][s];
+                    const float dx = xd[j][s];
+                    const float d0 = h2f((uint16_t)(dw[t][j][s].x & 0xffffu)) * dx;
+                    const float d1 = h2f((uint16_t)(dw[t][j][s].x >> 16)) * dx;
+                    const float d2 = h2f((uint16_t)(dw[t][j][s].y & 0xffffu)) * dx;
+                    const float d3 = h2f((uint16_t)(dw[t][j][s].y >> 16)) * dx;
+                    leaf[t].x = leaf[t].x + (float)r[0] * d0;
+                    leaf[t].y = leaf[t].y + (float)r[1] * d1;
+                    leaf[t].z = leaf[t].z + (float)r[2] * d2;
+                    leaf[t].w = leaf[t].w + (float)r[3] * d3;
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) {
+            float4 carry = leaf[t];
+            int k = 0;
+#pragma unroll
+            for (; k < LB && ((j >> k) & 1); ++k) {
+                carry.x = lev[t][k].x + carry.x; carry.y = lev[t][k].y + carry.y;
+                carry.z = lev[t][k].z + carry.z; carry.w = lev[t][k].w + carry.w;
+            }
+            lev[t][k] = carry;
+        }
+    }
+    // 3. the KW subtree sums -> the top of the tree, one (row, column) per thread
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+        red[w][16 * t + 4 * g + 0][c16] = lev[t][LB].x;
+        red[w][16 * t + 4 * g + 1][c16] = lev[t][LB].y;
+        red[w][16 * t + 4 * g + 2][c16] = lev[t][LB].z;
+        red[w][16 * t + 4 * g + 3][c16] = lev[t][LB].w;
+    }
+#pragma unroll
+    for (int k = 0; k < AD_PER; ++k)
+        if (tid + 64 * KW * k < ad_n) adsh[tid + 64 * KW * k] = adr[k];
+    __syncthreads();
+    for (int idx0 = 0; idx0 < ROWS * 16; idx0 += NT) {
+        const int idx = idx0 + tid;
+        if (idx0 + (tid & ~63) >= ROWS * 16) break;    // whole waves past the tile
+        const int n = idx / ROWS, r = idx % ROWS, row = row0 + r;
+        float v[KW];
+#pragma unroll
+        for (int q = 0; q < KW; ++q) v[q] = red[q][r][n];
+#pragma unroll
+        for (int off = KW / 2; off >= 1; off >>= 1)
+#pragma unroll
+            for (int q = 0; q < off; ++q) v[q] = v[q] + v[q + off];
+        float y = v[0];
+        const bool live = n < ncol;
+        if (a.ad_ax && live)
+            y = adapt_from(a, adsh + r * a.ad_rank, adsh + ad_nb + n * a.ad_rank, a.ad_m ? adsh[ad_nx + r] : 1.0f,
+                           a.ad_m ? adsh[ad_nx + ROWS + r] : 1.0f, y);
+        if constexpr (EPI == EPI_GELU_ACT) {
+            const float ge = gelu_erf(y);
+            const ActBuf& d = a.dst;
+            if (d.kind == ACT_Q8) {
+                int8_t qv;
+                float dv;
+                quant_q8_lane(ge, lane, &qv, &dv);    // lanes 32k..32k+31: one column's 32 rows
+                if (live && d.bm) {
+                    d.q[bm_off(n, row)] = qv;
+                    if ((lane & 31) == 0) d.d[(size_t)(row / 32) * 16 + n] = dv;
+                } else if (live) {
+                    d.q[(size_t)n * d.stride + row] = qv;
+                    if ((lane & 31) == 0) d.d[(size_t)n * (d.stride / 32) + row / 32] = dv;
+                }
+            } else if (live) {
+                if (d.kind == ACT_F16) d.h[(size_t)n * d.stride + row] = f2h(ge);
+                else d.f[(size_t)n * d.stride + row] = ge;
+            }
+            if (live && a.dst_f) a.dst_f[(size_t)n * d.stride + row] = ge;
+        } else if (live) {
+            if (EPI == EPI_STORE) a.y[(size_t)n * a.y_stride + row] = y;
+            else if (EPI == EPI_RESID) a.y[(size_t)n * a.y_stride + row] = a.y[(size_t)n * a.y_stride + row] + y;
+            else {
+                const int sec = row / a.dim, wi = row - sec * a.dim, head = wi >> 6, dm = wi & 63;
+                if (sec == 0) a.y[(size_t)n * a.dim + wi] = y;
+                else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + *a.pos) * 64 + dm] = y;
+            }
+        }
+    }
+    stamp_end(a.stamp, t0);
+}
+
 constexpr int PV_WAVES = 8;   // softmax + V block: 8 waves share the exps, 4 do V
 
 // ---- GEMV launch: kernel choice by weight type, prologue / epilogue kind and unit count
@@ -1327,7 +1537,60 @@ template <int WT> static void gemv_wt(const GemvArgs& a, hipStream_t s) {
 }
 
 // Columns go in groups of two (every per-column pointer advanced by the group's offset).
+// ---- matrix-core GEMV: (blocks per row, waves per 16-row tile) choices
+static int mf_kw(int nb, int tiles_out) {
+    const int base = nb >= 128 ? (nb == 256 ? 16 : 8) : 4;
+    const int kw = tiles_out >= 256 ? base : 16;
+    return nb % kw == 0 ? kw : base;
+}
+static bool mf_width(int nb) {
+    return nb == 4 || nb == 16 || nb == 32 || nb == 48 || nb == 64 || nb == 128 || nb == 192 || nb == 256;
+}
+bool gemv_mf_ok(const GemvArgs& a) {
+    const int rows = a.epi == EPI_GELU_ACT ? 32 : 16;
+    return a.w.type == T_Q8_0 && a.w.dt && a.w.qm && a.pro == PRO_ACT && a.src.kind == ACT_Q8 && a.src.bm &&
+           a.src.stride == a.w.in &&
+           a.ncol >= 3 && a.ncol <= 16 && a.w.in % 32 == 0 && mf_width(a.w.in / 32) && a.w.out % rows == 0 &&
+           (a.epi != EPI_GELU_ACT || a.w.in <= 2048);
+}
+template <int NB, int KW, int TILES, int EPI> static void mf_go(const GemvArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((k_gemv_mf<NB, KW, TILES, EPI>), dim3(a.w.out / (16 * TILES)), dim3(64 * KW), 0, s, a);
+}
+template <int NB, int KW> static void mf_epi(const GemvArgs& a, hipStream_t s) {
+    switch (a.epi) {
+    case EPI_STORE: mf_go<NB, KW, 1, EPI_STORE>(a, s); break;
+    case EPI_RESID: mf_go<NB, KW, 1, EPI_RESID>(a, s); break;
+    case EPI_QKV: mf_go<NB, KW, 1, EPI_QKV>(a, s); break;
+    default: if constexpr (NB <= 64) mf_go<NB, KW, 2, EPI_GELU_ACT>(a, s); break;
+    }
+}
+template <int NB> static void mf_nb(const GemvArgs& a, hipStream_t s) {
+    // mf_kw gives 4 only below 128 blocks, 8 only at 128 / 192, 16 only when it divides NB
+    switch (mf_kw(NB, a.w.out / (a.epi == EPI_GELU_ACT ? 32 : 16))) {
+    case 4: if constexpr (NB < 128) mf_epi<NB, 4>(a, s); break;
+    case 8: if constexpr (NB == 128 || NB == 192) mf_epi<NB, 8>(a, s); break;
+    default: if constexpr (NB % 16 == 0) mf_epi<NB, 16>(a, s); break;
+    }
+}
+static void launch_gemv_mf(const GemvArgs& a, hipStream_t s) {
+    switch (a.w.in / 32) {
+    case 4: mf_nb<4>(a, s); break;
+    case 16: mf_nb<16>(a, s); break;
+    case 32: mf_nb<32>(a, s); break;
+    case 48: mf_nb<48>(a, s); break;
+    case 64: mf_nb<64>(a, s); break;
+    case 128: mf_nb<128>(a, s); break;
+    case 192: mf_nb<192>(a, s); break;
+    default: mf_nb<256>(a, s); break;
+    }
+}
+
 void launch_gemv(const GemvArgs& a0, hipStream_t s) {
+    if (gemv_mf_ok(a0)) {
+        launch_gemv_mf(a0, s);
+        return;
+    }
+    if (a0.pro == PRO_ACT && a0.src.bm) return;   // the caller checks gemv_mf_ok before making one
     for (int c0 = 0; c0 < a0.ncol; c0 += 2) {
         GemvArgs a = a0;
         a.ncol = a0.ncol - c0 < 2 ? a0.ncol - c0 : 2;
@@ -1400,19 +1663,20 @@ __global__ void k_stamp_init(unsigned long long* p, int n) {
 void launch_stamp_init(unsigned long long* p, int n, hipStream_t s) {
     hipLaunchKernelGGL(k_stamp_init, dim3((n * STAMP_SUB + 255) / 256), dim3(256), 0, s, p, n);
 }
-// A x of an adapted projection (the inner mul_mat of lora.h:50-83's s * B(Ax)): one block per
-// (column, four rank rows). The column is built in LDS as the projection's own prologue
-// builds it (LayerNorm, or the f32 column as is); wave w takes rank row 4 * blockIdx.y + w:
-// lane l sums the 8-element units l, l + 64, ... of the row in element order (fmaf), and the
-// 64 partials fold by the butterfly -- the f32-weight convention of every projection.
+// Column preparation for a projection, one block per (column, role), the column built as the
+// vector GEMV's prologue builds it (LayerNorm or the f32 column as is):
+//  - role "quantize" (blockIdx.y == 0 when a.dst.q is set): the Q8 activation column, written
+//    straight to a.dst (the matrix-core GEMV's source);
+//  - role "A x" (the other blocks, when a.w.q is set; a.w = the adapter's A as an f32 matrix
+//    [rank][in]): the inner mul_mat of lora.h:50-83's s * B(Ax). Wave w takes rank row
+//    4 * (blockIdx.y - first) + w: lane l sums the 8-element units l, l + 64, ... of the row in
+//    element order (fmaf), and the 64 partials fold by the butterfly -- the f32-weight
+//    convention of every projection. Output a.y [col][a.y_stride].
 template <int KG, bool LN>
-__global__ __launch_bounds__(256) void k_adapter_ax(GemvArgs a) {
+__global__ __launch_bounds__(256) void k_prep(GemvArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = blockIdx.x;
     const int in = a.w.in, nf = in / 4;
-    LdsAct x{};
-    x.in = in;
-    x.f = (float*)lds;
     double* red = (double*)(lds + (size_t)in * 4);
     float4 xr[KG], wr[KG], br[KG];
     const float4* xs = (const float4*)(a.x + (size_t)col * a.x_stride);
@@ -1422,9 +1686,23 @@ __global__ __launch_bounds__(256) void k_adapter_ax(GemvArgs a) {
         xr[j] = xs[f];
         if (LN) { wr[j] = ((const float4*)a.ln_w)[f]; br[j] = ((const float4*)a.ln_b)[f]; }
     }
+    const int first = a.dst.q ? 1 : 0;
+    if ((int)blockIdx.y < first) {
+        LdsAct g{};
+        g.in = in;
+        g.bm_col = a.dst.bm ? col : -1;
+        g.q = a.dst.bm ? a.dst.q : a.dst.q + (size_t)col * a.dst.stride;
+        g.d = a.dst.bm ? a.dst.d : a.dst.d + (size_t)col * (a.dst.stride / 32);
+        prologue<T_Q8_0, KG, LN>(a, g, red, 0, tid, lane, xr, wr, br);
+        return;
+    }
+    LdsAct x{};
+    x.in = in;
+    x.bm_col = -1;
+    x.f = (float*)lds;
     prologue<T_F32, KG, LN>(a, x, red, 0, tid, lane, xr, wr, br);
     lds_barrier();
-    const int k = blockIdx.y * 4 + wave;
+    const int k = ((int)blockIdx.y - first) * 4 + wave;
     if (k >= a.w.out) return;
     const float* A = (const float*)a.w.q + (size_t)k * in;
     float p = 0.0f;
@@ -1439,24 +1717,59 @@ __global__ __launch_bounds__(256) void k_adapter_ax(GemvArgs a) {
     p = fold64(p);
     if (lane == 0) a.y[(size_t)col * a.y_stride + k] = p;
 }
-template <int KG> static void adapter_ax_go(const GemvArgs& a, hipStream_t s) {
-    const dim3 grid(a.ncol, (a.w.out + 3) / 4);
+template <int KG> static void prep_go(const GemvArgs& a, hipStream_t s) {
+    const int ny = (a.dst.q ? 1 : 0) + (a.w.q ? (a.w.out + 3) / 4 : 0);
+    const dim3 grid(a.ncol, ny);
     const size_t lds = (size_t)a.w.in * 4 + 512 * 8;
-    if (a.pro == PRO_LN) hipLaunchKernelGGL((k_adapter_ax<KG, true>), grid, dim3(256), lds, s, a);
-    else hipLaunchKernelGGL((k_adapter_ax<KG, false>), grid, dim3(256), lds, s, a);
+    if (a.pro == PRO_LN) hipLaunchKernelGGL((k_prep<KG, true>), grid, dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((k_prep<KG, false>), grid, dim3(256), lds, s, a);
 }
-void launch_adapter_ax(const GemvArgs& a, hipStream_t s) {
+static void prep_launch(const GemvArgs& a, hipStream_t s) {
     switch ((a.w.in + 1023) / 1024) {
-    case 1: adapter_ax_go<1>(a, s); break;
-    case 2: adapter_ax_go<2>(a, s); break;
-    case 3: adapter_ax_go<3>(a, s); break;
-    case 4: adapter_ax_go<4>(a, s); break;
-    case 5: adapter_ax_go<5>(a, s); break;
-    case 6: adapter_ax_go<6>(a, s); break;
-    case 7: adapter_ax_go<7>(a, s); break;
-    default: adapter_ax_go<8>(a, s); break;
+    case 1: prep_go<1>(a, s); break;
+    case 2: prep_go<2>(a, s); break;
+    case 3: prep_go<3>(a, s); break;
+    case 4: prep_go<4>(a, s); break;
+    case 5: prep_go<5>(a, s); break;
+    case 6: prep_go<6>(a, s); break;
+    case 7: prep_go<7>(a, s); break;
+    default: prep_go<8>(a, s); break;
     }
 }
+void launch_adapter_ax(const GemvArgs& a0, hipStream_t s) {
+    GemvArgs a = a0;
+    a.dst = ActBuf{};
+    prep_launch(a, s);
+}
+void launch_act_prep(const GemvArgs& a, hipStream_t s) { prep_launch(a, s); }
+
+// Q8_0 scales tile-transposed: dt[(r/16 * nb + b) * 16 + r%16] = d[r * nb + b].
+__global__ void k_scales_t(const uint16_t* d, int nb, int out, uint16_t* dt) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= out * nb) return;
+    const int r = i / nb, b = i - r * nb;
+    dt[((size_t)(r >> 4) * nb + b) * 16 + (r & 15)] = d[i];
+}
+// Q8_0 quants in operand order: qm[((r/16 * nb + b) * 64 + 16g + r%16) * 8 + j] = q[r][32b + 8g + j]
+__global__ void k_weights_mf(const int8_t* q, int in, int out, int8_t* qm) {
+    const size_t u = (size_t)blockIdx.x * 256 + threadIdx.x;   // one 8-byte piece
+    const int nb = in / 32;
+    if (u >= (size_t)out * nb * 4) return;
+    const int lanei = (int)(u & 63);
+    const size_t tb = u >> 6;
+    const int b = (int)(tb % nb), tile = (int)(tb / nb);
+    const int g = lanei >> 4, c = lanei & 15;
+    *(uint2*)(qm + u * 8) = *(const uint2*)(q + (size_t)(tile * 16 + c) * in + b * 32 + 8 * g);
+}
+void launch_weights_mf(const DevMat& w, int8_t* qm, hipStream_t s) {
+    const size_t n = (size_t)w.out * (w.in / 32) * 4;
+    hipLaunchKernelGGL(k_weights_mf, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const int8_t*)w.q, w.in, w.out, qm);
+}
+void launch_scales_t(const DevMat& w, uint16_t* dt, hipStream_t s) {
+    const int nb = w.in / 32;
+    hipLaunchKernelGGL(k_scales_t, dim3((w.out * nb + 255) / 256), dim3(256), 0, s, w.d, nb, w.out, dt);
+}
+
 // DoRA rows (lora.h:11-32): one thread per row, sequential double sums over the row.
 __global__ __launch_bounds__(64) void k_dora_norm(DevMat w, const float* A, const float* B, int rank, float scale,
                                                   float* norm, int* bad) {

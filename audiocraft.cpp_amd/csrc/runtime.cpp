@@ -123,11 +123,13 @@ struct ActStore {
     uint16_t* h = nullptr;
     float* f = nullptr;
     int stride = 0;
-    mgx::ActBuf view(int wtype) const {
+    // bm: Q8 block-major, the layout a matrix-core GEMV reads (16 column slots are allocated)
+    mgx::ActBuf view(int wtype, bool bm = false) const {
         mgx::ActBuf a{};
         a.kind = act_kind(wtype);
         a.stride = stride;
         a.q = q; a.d = d; a.h = h; a.f = f;
+        a.bm = bm && a.kind == mgx::ACT_Q8 ? 1 : 0;
         return a;
     }
 };
@@ -148,6 +150,7 @@ struct mgx_stream {
     float *x = nullptr, *qb = nullptr, *scores = nullptr, *opart = nullptr, *logits = nullptr;
     float* qc = nullptr;                     // cross q [n_req][dim]
     ActStore act_o, act_c, act_f;            // attention out, cross-attention out, GELU out
+    ActStore act_ln;                         // LayerNorm'd columns in Q8 form (matrix-core GEMVs)
     int32_t* ids = nullptr;                  // [n_q][cap] staged ids for mgx_forward
     // Launch timing: when `prof_on`, every GEMV and attention launch gets a slot in `stamps`
     // (device [slot][2]: earliest block start, latest wave end on the GPU wall clock).
@@ -172,11 +175,14 @@ struct mgx_stream {
     }
     size_t layer_kv() const { return (size_t)n_seq * m->c.heads * kv_rows * 64; }
     void alloc_act(ActStore& a, int cols, int stride) {
+        if (n_seq >= 3) cols = std::max(cols, 16);   // block-major Q8 has 16 column slots
         a.stride = stride;
         a.q = mem.alloc<int8_t>((size_t)cols * stride);
         a.d = mem.alloc<float>((size_t)cols * stride / 32);
         a.h = mem.alloc<uint16_t>((size_t)cols * stride);
         a.f = mem.alloc<float>((size_t)cols * stride);
+        HIP_OK(hipMemsetAsync(a.q, 0, (size_t)cols * stride, hs));
+        HIP_OK(hipMemsetAsync(a.d, 0, (size_t)cols * stride / 32 * sizeof(float), hs));
     }
 };
 
@@ -292,6 +298,8 @@ enum { PROF_GEMV = 0, PROF_ATTN = 1 };
 
 // One projection. Algorithmic bytes of a launch = the weights at their stored precision.
 void gemv(mgx_stream* s, mgx::GemvArgs a) {
+    if (a.pro == mgx::PRO_ACT && a.src.bm && !mgx::gemv_mf_ok(a))
+        throw Error(MGX_ERR_INVALID, "internal: a block-major source for a projection the matrix cores cannot run");
     a.stamp = s->stamp_slot(PROF_GEMV, (double)a.w.in * a.w.out * bytes_per_weight(a.w.type));
     mgx::launch_gemv(a, s->hs);
 }
@@ -322,6 +330,28 @@ mgx::GemvArgs& epi_store(mgx::GemvArgs& a, float* y, int stride, bool resid = fa
 // (its LayerNorm or f32 source; for an activation-form source, `xf` holds the same column in
 // f32), then the GEMV adds s * B(Ax) in its epilogue (lora.h:50-83).
 void gemv_ad(mgx_stream* s, mgx::GemvArgs a, const AdapterW* ad, const float* xf = nullptr, int xf_stride = 0) {
+    if (a.pro != mgx::PRO_ACT) {
+        // the matrix-core GEMV reads its columns in Q8 form: LayerNorm / quantize them (and
+        // take the adapter's A x from the same f32 column) in one preparation launch
+        mgx::GemvArgs m = a;
+        m.pro = mgx::PRO_ACT;
+        m.src = s->act_ln.view(mgx::T_Q8_0, true);
+        m.src.stride = a.w.in;
+        if (s->act_ln.q && a.w.in <= s->act_ln.stride && mgx::gemv_mf_ok(m)) {
+            mgx::GemvArgs p = ga(ad ? ad->A : mgx::DevMat{}, a.ncol);
+            p.w.in = a.w.in;
+            p.pro = a.pro; p.x = a.x; p.x_stride = a.x_stride; p.ln_w = a.ln_w; p.ln_b = a.ln_b; p.eps = a.eps;
+            p.dst = m.src;
+            if (ad) { p.y = s->ax; p.y_stride = ad->rank; }
+            mgx::launch_act_prep(p, s->hs);
+            if (ad) {
+                m.ad_ax = s->ax; m.ad_B = ad->B; m.ad_m = ad->m; m.ad_norm = ad->norm; m.ad_rank = ad->rank;
+                m.ad_scale = ad->scale; m.ad_strength = ad->strength;
+            }
+            gemv(s, m);
+            return;
+        }
+    }
     if (ad) {
         mgx::GemvArgs b = ga(ad->A, a.ncol);
         if (a.pro == mgx::PRO_ACT) {
@@ -335,6 +365,15 @@ void gemv_ad(mgx_stream* s, mgx::GemvArgs a, const AdapterW* ad, const float* xf
         a.ad_scale = ad->scale; a.ad_strength = ad->strength;
     }
     gemv(s, a);
+}
+
+// Whether the projection w over ncol activation-form columns runs on the matrix cores (its
+// producer then writes block-major Q8).
+bool mf_src(const mgx::DevMat& w, int ncol, int epi) {
+    mgx::GemvArgs a = ga(w, ncol);
+    a.pro = mgx::PRO_ACT; a.epi = epi;
+    a.src.kind = act_kind(w.type); a.src.bm = 1; a.src.stride = w.in;
+    return mgx::gemv_mf_ok(a);
 }
 
 // One sequence step at the device position *s->dpos for every stream: column n belongs to
@@ -358,6 +397,8 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
     const float scale = 1.0f / std::sqrt((float)c.head_dim);
     for (int l = 0; l < c.layers; ++l) {
         const LayerW& L = m->L[(size_t)l];
+        const bool bo = mf_src(L.w[P_OUT], N, mgx::EPI_RESID), bc = mf_src(L.w[P_COUT], R, mgx::EPI_RESID);
+        const bool bf = mf_src(L.w[P_FF2], N, mgx::EPI_RESID);
         float* Kl = s->K + (size_t)l * s->layer_kv();
         float* Vl = s->V + (size_t)l * s->layer_kv();
         // self-attention: LN1 + qkv with the K/V append, scores, softmax + V (+ chunk reduce)
@@ -372,7 +413,7 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
             mgx::AttnArgs at{};
             at.q = s->qb; at.k = Kl; at.v = Vl; at.scores = s->scores; at.opart = s->opart; at.cmax = s->cmax;
             at.dim = D; at.heads = c.heads; at.cap = s->kv_rows; at.max_chunks = s->max_chunks; at.ncol = N;
-            at.scale = scale; at.pos = s->dpos; at.out = s->act_o.view(L.w[P_OUT].type);
+            at.scale = scale; at.pos = s->dpos; at.out = s->act_o.view(L.w[P_OUT].type, bo);
             at.out_f = L.ad[P_OUT] ? s->act_o.f : nullptr;
             // f32 K and V of every key attended, every stream
             at.stamp = s->stamp_slot(PROF_ATTN, 2.0 * N * c.heads * (position + 1) * 64 * 4);
@@ -380,7 +421,7 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
         }
         {
             mgx::GemvArgs a = ga(L.w[P_OUT], N);
-            pro_act(a, s->act_o.view(L.w[P_OUT].type));
+            pro_act(a, s->act_o.view(L.w[P_OUT].type, bo));
             epi_store(a, s->x, D, true);
             gemv_ad(s, a, L.ad[P_OUT], s->act_o.f, D);
         }
@@ -394,11 +435,11 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
             mgx::XAttnArgs xa{};
             const size_t xl = (size_t)l * R * c.heads * s->n_ctx * 64;
             xa.q = s->qc; xa.k = s->xk + xl; xa.v = s->xv + xl; xa.n_ctx = s->n_ctx; xa.dim = D; xa.scale = scale;
-            xa.out = s->act_c.view(L.w[P_COUT].type);
+            xa.out = s->act_c.view(L.w[P_COUT].type, bc);
             xa.out_f = L.ad[P_COUT] ? s->act_c.f : nullptr;
             mgx::launch_xattn(xa, c.heads, R, s->hs);
             mgx::GemvArgs b = ga(L.w[P_COUT], R);
-            pro_act(b, s->act_c.view(L.w[P_COUT].type));
+            pro_act(b, s->act_c.view(L.w[P_COUT].type, bc));
             epi_store(b, s->x, s->cpr * D, true);
             gemv_ad(s, b, L.ad[P_COUT], s->act_c.f, D);
         }
@@ -406,11 +447,11 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
         {
             mgx::GemvArgs a = ga(L.w[P_FF0], N);
             pro_ln(a, s->x, D, L.n2w, L.n2b, c.norm_eps);
-            a.epi = mgx::EPI_GELU_ACT; a.dst = s->act_f.view(L.w[P_FF2].type);
+            a.epi = mgx::EPI_GELU_ACT; a.dst = s->act_f.view(L.w[P_FF2].type, bf);
             a.dst_f = L.ad[P_FF2] ? s->act_f.f : nullptr;
             gemv_ad(s, a, L.ad[P_FF0]);
             mgx::GemvArgs b = ga(L.w[P_FF2], N);
-            pro_act(b, s->act_f.view(L.w[P_FF2].type));
+            pro_act(b, s->act_f.view(L.w[P_FF2].type, bf));
             epi_store(b, s->x, D, true);
             gemv_ad(s, b, L.ad[P_FF2], s->act_f.f, c.ff_dim);
         }
@@ -419,7 +460,7 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
         mgx::GemvArgs a = ga(m->heads, N);
         pro_ln(a, s->x, D, m->out_w, m->out_b, c.norm_eps);
         epi_store(a, s->logits, c.n_q * c.card);
-        gemv(s, a);
+        gemv_ad(s, a, nullptr);
     }
     if (sample) mgx::launch_sample(*sample, s->hs);
     mgx::launch_advance(s->dpos, s->hs);
@@ -511,6 +552,7 @@ void make_stream(mgx_model* m, int capacity, int n_seq, int n_req, const float* 
     s->alloc_act(s->act_o, n_seq, c.dim);
     s->alloc_act(s->act_c, n_req, c.dim);
     s->alloc_act(s->act_f, n_seq, c.ff_dim);
+    if (n_seq >= 3) s->alloc_act(s->act_ln, n_seq, c.dim);
     s->ids = s->mem.alloc<int32_t>((size_t)c.n_q * capacity);
     if (m->ad_rank_max > 0) s->ax = s->mem.alloc<float>((size_t)std::max(n_seq, 2) * m->ad_rank_max);
     if (s->cross) {
@@ -599,6 +641,20 @@ int mgx_model_create(const mgx_lm_config* cfg, const mgx_tensor* t, int32_t n, m
             L.n2w = load_vec(m.get(), t, n, p + "norm2.weight", c.dim, s);
             L.n2b = load_vec(m.get(), t, n, p + "norm2.bias", c.dim, s);
         }
+        // every Q8_0 projection's matrix-core copies: tile-transposed scales, operand-order quants
+        auto with_dt = [&](mgx::DevMat& w) {
+            if (w.type != mgx::T_Q8_0 || w.out % 16 || w.in % 32) return;
+            uint16_t* dt = m->mem.alloc<uint16_t>((size_t)w.out * (w.in / 32));
+            int8_t* qm = m->mem.alloc<int8_t>((size_t)w.out * w.in);
+            mgx::launch_scales_t(w, dt, s);
+            mgx::launch_weights_mf(w, qm, s);
+            HIP_OK(hipGetLastError());
+            w.dt = dt;
+            w.qm = qm;
+        };
+        with_dt(m->heads);
+        for (LayerW& L : m->L)
+            for (int k = 0; k < P_COUNT; ++k) with_dt(L.w[k]);
         HIP_OK(hipStreamSynchronize(s));
         *out = m.release();
     });

@@ -40,21 +40,29 @@ WORKLOADS = {
                       desc="musicgen-small-shaped LM, F16, CFG 2 streams, 500-frame prompt + 1500-frame continuation"),
     "large-q4": dict(shape="large", wtype=2, prompt=1500, gen=1500, seed=1, n_ctx=32,
                      desc="musicgen-large-shaped LM, Q4_0, CFG 2 streams, 1500-frame prompt + 1500-frame continuation"),
+    # 8 independent requests in lockstep (16 streams), request r seeded 1 + r (memory, prompt,
+    # sampling), rank-16 DoRA rows (alpha 16, strength 1) on every layer's qkv, ff.0 and ff.2
+    "medium-q8-batch8-dora": dict(shape="medium", wtype=8, prompt=500, gen=1500, seed=1, n_ctx=24, requests=8,
+                                  adapters=dict(rank=16, targets=("self.qkv", "ff.0", "ff.2"), dora=True),
+                                  desc="musicgen-medium-shaped LM, Q8_0, 8 requests x CFG 2 streams (16 rows), "
+                                       "rank-16 DoRA rows on qkv/ff.0/ff.2, 500-frame prompts + 1500-frame "
+                                       "continuations"),
 }
 BPW = {8: 34 / 32, 2: 18 / 32, 1: 2.0, 0: 4.0}
 HBM_PEAK_GBS = 8000.0
 
 
-def step_bytes(c, wbpw, n_seq, n_ctx, u):
+def step_bytes(c, wbpw, n_seq, n_ctx, u, requests=1, adapter_bytes=0.0):
     """Algorithmic HBM bytes of one decode step attending u keys: weights at stored precision
-    (cross.kv excluded: projected once per request) + f32 LN params + f32 K/V read and write +
-    the conditional stream's cross K/V + logits."""
+    (cross.kv excluded: projected once per request) + adapter tensors (f32 A, B, magnitude and
+    row norms, read once per step) + f32 LN params + f32 K/V read and write + each request's
+    conditional-stream cross K/V + logits."""
     L, d, F, Q, C = c.layers, c.dim, c.ff_dim, c.n_q, c.card
     w = (L * (3 * d * d + d * d + d * d + d * d + 2 * d * F) + Q * C * d + Q * d) * wbpw + (6 * L + 2) * d * 4
     kv_read = 2 * L * d * u * n_seq * 4
     kv_write = 2 * L * d * n_seq * 4
-    xkv = 2 * L * d * n_ctx * 4
-    return w + kv_read + kv_write + xkv + Q * C * n_seq * 4
+    xkv = 2 * L * d * n_ctx * 4 * requests
+    return w + adapter_bytes + kv_read + kv_write + xkv + Q * C * n_seq * 4
 
 
 def gemv_traffic(workload):
@@ -91,14 +99,15 @@ def device_copy(mib):
     hip_sync()
 
 
-def cpu_baseline(w, model, t5, prompt, seconds):
+def cpu_baseline(w, model, t5, prompt, seconds, adapters=None):
     """The oracle (a CPU restatement of the reference's ggml-CPU decode step, including its
     per-step cross.kv projection) on the host: prefill untimed, then decode steps for about
-    `seconds` of wall time."""
+    `seconds` of wall time. For a batch workload it times request 0: the reference serves
+    requests one after another, so its aggregate rate is the one-request rate."""
     from oracle import cpu_ref as R
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
     R.set_threads(threads)
-    rm = R.RefModel(model.config, model.tensors)
+    rm = R.RefModel(model.config, model.tensors, adapters)
     # calibrate on a few steps, then run the bounded sample
     T = w["prompt"] + w["gen"]
     _, _, rep, _ = rm.generate(t5, prompt, w["prompt"], T, top_k=250, temperature=1.0, cfg_coef=3.0,
@@ -108,9 +117,10 @@ def cpu_baseline(w, model, t5, prompt, seconds):
     _, _, rep, _ = rm.generate(t5, prompt, w["prompt"], T, top_k=250, temperature=1.0, cfg_coef=3.0,
                                seed=w["seed"], recompute_cross_kv=True, max_forwards=n + 1)
     steps = rep.forwards - 1
+    which = "request 0 of the batch (requests run one after another)" if w.get("requests", 1) > 1 else "same workload"
     return dict(value=round(steps / rep.decode_seconds, 3), unit="frames/s", cores=R.lib().ref_get_threads(),
                 kind="port",
-                sample=f"oracle CPU restatement of the reference ggml path, same workload: {w['prompt'] + 1}-token "
+                sample=f"oracle CPU restatement of the reference ggml path, {which}: {w['prompt'] + 1}-token "
                        f"prefill untimed, then the first {steps} decode steps timed "
                        f"({rep.decode_seconds:.1f} s, prefill {rep.prefill_seconds:.1f} s)")
 
@@ -143,13 +153,21 @@ def main():
     t_build = time.time()
     model = mgx.SyntheticModel(w["shape"], w["wtype"], seed=w["seed"])
     c = model.config
-    t5 = mgx.synth_memory(w["seed"], w["n_ctx"])
-    prompt = mgx.synth_codes(w["seed"], c.n_q, w["prompt"], c.card)
+    R = w.get("requests", 1)
+    T = w["prompt"] + w["gen"]
+    reqs = [dict(t5=mgx.synth_memory(w["seed"] + r, w["n_ctx"]),
+                 prompt=mgx.synth_codes(w["seed"] + r, c.n_q, w["prompt"], c.card),
+                 params=mgx.GenerateParams(T, 1, 1.0, 250, 3.0, w["seed"] + r)) for r in range(R)]
+    t5, prompt = reqs[0]["t5"], reqs[0]["prompt"]
     gm = mgx.Model(c, model.tensors)
+    adapters, adapter_bytes = None, 0.0
+    if w.get("adapters"):
+        adapters = mgx.synth_adapters(c, **w["adapters"])
+        gm.set_adapters(adapters)
+        # A, B, magnitude and the row norms, f32
+        adapter_bytes = sum(4.0 * (a["A"].size + a["B"].size + 2 * a["B"].shape[0]) for a in adapters)
     print(f"[bench] {args.workload}: {model.nbytes() / 1e9:.2f} GB of weights built and uploaded in "
           f"{time.time() - t_build:.1f} s", file=sys.stderr, flush=True)
-    T = w["prompt"] + w["gen"]
-    params = mgx.GenerateParams(T, 1, 1.0, 250, 3.0, w["seed"])
     S = T + c.n_q
     start = w["prompt"] + 1
 
@@ -167,9 +185,10 @@ def main():
                     ms, by, n = sess.profile_read(k)
                     acc[0] += ms; acc[1] += by; acc[2] += n
                 sess.close()
-            sess = mgx.Session(gm, t5, prompt, w["prompt"], params)
+            sess = mgx.Batch(gm, reqs, w["prompt"]) if R > 1 else mgx.Session(gm, t5, prompt, w["prompt"],
+                                                                               reqs[0]["params"])
             sess.step(1)                                   # prefill, untimed
-            print(f"[bench] session prefilled ({start} tokens)", file=sys.stderr, flush=True)
+            print(f"[bench] session prefilled ({start} tokens x {R} requests)", file=sys.stderr, flush=True)
         if warm_left > 0:
             warm_left -= sess.step(min(warm_left, sess.remaining()))
             continue
@@ -183,7 +202,7 @@ def main():
         timed += time.perf_counter() - t0
         sess.profile(0)
         for i in range(done):
-            bytes_total += step_bytes(c, BPW[w["wtype"]], 2, w["n_ctx"], pos0 + i + 1)
+            bytes_total += step_bytes(c, BPW[w["wtype"]], 2 * R, w["n_ctx"], pos0 + i + 1, R, adapter_bytes)
         timed_steps += done
         print(f"[bench] timed {timed_steps}/{args.steps} steps, {timed:.2f} s", file=sys.stderr, flush=True)
     for k, acc in ((0, gemv), (1, attn)):
@@ -191,7 +210,7 @@ def main():
         acc[0] += ms; acc[1] += by; acc[2] += nn
     sess.close()
 
-    fps = timed_steps / timed
+    fps = R * timed_steps / timed                          # frames of every request
     gemv_gbs = gemv[1] / (gemv[0] * 1e-3) / 1e9 if gemv[0] > 0 else 0.0
     attn_gbs = attn[1] / (attn[0] * 1e-3) / 1e9 if attn[0] > 0 else 0.0
     out = {
@@ -208,7 +227,8 @@ def main():
         "vs_baseline": None,
         "dtype": {8: "int8xq8_0+f32", 2: "int8xq4_0+f32", 1: "f16+f32", 0: "f32"}[w["wtype"]],
         "data": "synthetic (seeded random N(0,0.02) weights, N(0,1) memory, uniform prompt codes)",
-        "config": {"workload": w["desc"], "layers": c.layers, "dim": c.dim, "heads": c.heads, "ff_dim": c.ff_dim,
+        "config": {"workload": w["desc"], "requests": R, "layers": c.layers, "dim": c.dim, "heads": c.heads,
+                   "ff_dim": c.ff_dim,
                    "weights": {8: "Q8_0", 2: "Q4_0", 1: "F16", 0: "F32"}[w["wtype"]], "n_ctx": w["n_ctx"],
                    "prompt_frames": w["prompt"], "continuation_frames": w["gen"], "cfg_coef": 3.0, "top_k": 250,
                    "temperature": 1.0, "seed": w["seed"], "parallelism": "single GPU"},
@@ -223,7 +243,7 @@ def main():
     }
     if not args.no_cpu:
         try:
-            out["cpu_baseline"] = cpu_baseline(w, model, t5, prompt, args.cpu_seconds)
+            out["cpu_baseline"] = cpu_baseline(w, model, t5, prompt, args.cpu_seconds, adapters)
         except Exception as e:  # the GPU figure stands without it
             out["cpu_baseline"] = {"error": str(e)}
     print(json.dumps(out), flush=True)

@@ -37,7 +37,7 @@ def test_tiny_forward_matches_oracle(mgx, wtype):
 
 @pytest.mark.parametrize("shape,wtype", [("mini1024", 8), ("mini1024", 2), ("mini1024", 1), ("mini1536", 8),
                                          ("mini2048", 2), ("mini2048", 8)])
-@pytest.mark.parametrize("n_seq", [1, 2, 3])
+@pytest.mark.parametrize("n_seq", [1, 2, 3, 16])
 def test_width_forward_matches_oracle(mgx, shape, wtype, n_seq):
     """The specialised GEMV shapes (dims 1024 / 1536 / 2048, ff 4x) and the column groups."""
     from oracle import cpu_ref as R
