@@ -778,8 +778,9 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
     float4 kv[4];
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-        const int j = b * ATT_SUB + it * 16 + wave * 4 + g;
-        kv[it] = ((const float4*)(K + (size_t)j * 64))[t];   // rows up to the chunk end exist
+        // keys past the position re-read the last key (a cache hit, not HBM traffic)
+        const int j = b * ATT_SUB + it * 16 + wave * 4 + g, jl = j < u ? j : u - 1;
+        kv[it] = ((const float4*)(K + (size_t)jl * 64))[t];
     }
     float p[4];
 #pragma unroll
@@ -836,11 +837,15 @@ __global__ __launch_bounds__(64 * WAVES) void k_attn_pv(AttnArgs a) {
     const int g = (wave & 3) * 4 + (lane >> 4), dq = lane & 15;
     const float* V = a.v + head * a.cap * 64;
     float4 vv[16];
-    if (wave < 4) {
-#pragma unroll
-        for (int m = 0; m < 16; ++m) vv[m] = ((const float4*)(V + (size_t)(c * ATT_CHUNK + g + 16 * m) * 64))[dq];
-    }
     const int u = *a.pos + 1;
+    if (wave < 4) {
+        // keys past the position re-read the last key (a cache hit, not HBM traffic)
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            const int j = c * ATT_CHUNK + g + 16 * m, jl = j < u ? j : u - 1;
+            vv[m] = ((const float4*)(V + (size_t)jl * 64))[dq];
+        }
+    }
     float M = cm[0];
 #pragma unroll
     for (int i = 1; i < NCH * ATT_SUBS; ++i) M = M > cm[i] ? M : cm[i];
