@@ -526,6 +526,10 @@ __device__ __forceinline__ float adapt(const GemvArgs& a, int row, int col, floa
                       a.ad_m ? a.ad_m[row] : 1.0f, a.ad_m ? a.ad_norm[row] : 1.0f, base);
 }
 
+template <int KEYQ>
+__device__ __forceinline__ void xattn_head(const float* qh, const float* K, const float* V, int nc, float scale,
+                                           const ActBuf& out, float* out_f, int dim, int h, int r);
+
 // U > 0: every lane owns exactly U units (units == G * U). U == 0: any unit count, a runtime
 // loop in passes of 8 units per lane (needs G == 8 so a pass covers each partial once).
 template <int WT, int NC, int G, int U, int PRO, int EPI, int WAVES>
@@ -664,6 +668,16 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
             if (n < ncol) v[n] = adapt(a, row, n, v[n]);
     }
     // 6. epilogue: lane 0 of each row group holds every column's value
+    if constexpr (EPI == EPI_XATTN) {
+        // the block's 64 rows are head blockIdx.x's q: LDS, then that head's cross-attention
+        static_assert(R == 64 && NC == 1 && NT == 256, "one head of q per 256-thread block");
+        if (t == 0) tile[wave * M + rl] = v[0];
+        lds_barrier();
+        const int h = blockIdx.x;
+        xattn_head<4>(tile, a.k + (size_t)h * a.xn_ctx * 64, a.v + (size_t)h * a.xn_ctx * 64, a.xn_ctx, a.xscale,
+                      a.dst, a.dst_f, a.dim, h, 0);
+        return;
+    }
     if constexpr (EPI == EPI_GELU_ACT) {
         // the block's R rows -> LDS tile -> GELU (one value per lane, spread over the waves)
         // -> activation form, one 32-row block per wave pass
@@ -920,58 +934,63 @@ __global__ __launch_bounds__(64) void k_attn_reduce(AttnArgs a) {
 // cross-attention of the conditional stream over the projected memory (lm.h:181-199).
 // The null stream's memory is zero, so its block output is exactly zero and is skipped.
 // ------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_xattn(XAttnArgs a) {
-    // One block per head, n_ctx <= 256 keys (one chunk). Scores: 16 lanes per key (four dims
-    // each), 16 keys per pass; after the halving reduce thread (wave, g, t) holds key
-    // 16t + 4*wave + g. V: partial g16 = key mod 16, lane%16 -> dims 4*(lane%16)..+3.
-    const int h = blockIdx.x, r = blockIdx.y, H = gridDim.x;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, t = lane & 15;
-    const int nc = a.n_ctx;
-    const float* K = a.k + ((size_t)r * H + h) * nc * 64;
-    const float* V = a.v + ((size_t)r * H + h) * nc * 64;
+// One head's cross-attention by a 256-thread group (threads 0..255 of the block): n_ctx <= 16
+// * KEYQ keys of one 256-key chunk. Scores: 16 lanes per key (four dims each), 16 keys per pass;
+// after the halving reduce thread (wave, g, t) holds key 16t + 4*wave + g. V: partial g16 = key
+// mod 16, lane%16 -> dims 4*(lane%16)..+3. q: the head's 64 values (global memory or LDS).
+// Output column r, elements h*64..h*64+63 of `out` (and of out_f when set). Every thread of
+// the block must call it (it holds block barriers); threads >= 256 only take part in those.
+template <int KEYQ>
+__device__ __forceinline__ void xattn_head(const float* qh, const float* K, const float* V, int nc, float scale,
+                                           const ActBuf& out, float* out_f, int dim, int h, int r) {
     __shared__ float el[256];
     __shared__ float red_f[4];
     __shared__ float4 vred[16][16];
     __shared__ float ol[64];
-    const float4 q = ((const float4*)(a.q + (size_t)r * a.dim + h * 64))[t];
-    float4 kv[16];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, t = lane & 15;
+    const bool act = tid < 256;
+    const int g16 = (wave & 3) * 4 + g, dq = lane & 15;
+    float4 kv[KEYQ], vv[KEYQ];
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
-        const int j = it * 16 + wave * 4 + g;
-        kv[it] = j < nc ? ((const float4*)(K + (size_t)j * 64))[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int it = 0; it < KEYQ; ++it) {
+        const int j = it * 16 + (wave & 3) * 4 + g;
+        kv[it] = act && j < nc ? ((const float4*)(K + (size_t)j * 64))[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    const int g16 = wave * 4 + g, dq = lane & 15;
-    float4 vv[16];
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
+    for (int m = 0; m < KEYQ; ++m) {
         const int j = g16 + 16 * m;
-        vv[m] = j < nc ? ((const float4*)(V + (size_t)j * 64))[dq] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        vv[m] = act && j < nc ? ((const float4*)(V + (size_t)j * 64))[dq] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
+    const float4 q = ((const float4*)qh)[t];
     float p[16];
 #pragma unroll
     for (int it = 0; it < 16; ++it) {
-        float v = __builtin_fmaf(q.x, kv[it].x, 0.0f);
-        v = __builtin_fmaf(q.y, kv[it].y, v);
-        v = __builtin_fmaf(q.z, kv[it].z, v);
-        p[it] = __builtin_fmaf(q.w, kv[it].w, v);
+        if (it < KEYQ) {
+            float v = __builtin_fmaf(q.x, kv[it].x, 0.0f);
+            v = __builtin_fmaf(q.y, kv[it].y, v);
+            v = __builtin_fmaf(q.z, kv[it].z, v);
+            p[it] = __builtin_fmaf(q.w, kv[it].w, v);
+        } else {
+            p[it] = 0.0f;
+        }
     }
-    const int jt = t * 16 + wave * 4 + g;
-    const float sc = halving16(p, t) * a.scale;
+    const int jt = t * 16 + (wave & 3) * 4 + g;
+    const float sc = halving16(p, t) * scale;
     float mx = jt < nc ? sc : -__builtin_inff();
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(mx, off); mx = mx > o ? mx : o; }
-    if (lane == 0) red_f[wave] = mx;
+    if (act && lane == 0) red_f[wave] = mx;
     lds_barrier();
     float M = red_f[0];
     for (int w = 1; w < 4; ++w) M = M > red_f[w] ? M : red_f[w];
-    el[jt] = jt < nc ? dexpf(sc - M) : 0.0f;
+    if (act) el[jt] = jt < nc ? dexpf(sc - M) : 0.0f;
     lds_barrier();
     // the 256-key sum in double (butterfly), every wave; p = e * (float)(1/sum)
     const double es = ((double)el[lane] + (double)el[lane + 128]) + ((double)el[lane + 64] + (double)el[lane + 192]);
     const float inv = (float)(1.0 / (0.0 + fold64d_b(es)));
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
+    for (int m = 0; m < KEYQ; ++m) {
         const int j = g16 + 16 * m;
         if (j < nc) {
             const float pm = el[j] * inv;
@@ -981,9 +1000,9 @@ __global__ __launch_bounds__(256) void k_xattn(XAttnArgs a) {
             acc.w = __builtin_fmaf(pm, vv[m].w, acc.w);
         }
     }
-    vred[g16][dq] = acc;
+    if (act) vred[g16][dq] = acc;
     lds_barrier();
-    if (g16 < 8) {
+    if (act && g16 < 8) {
         const float4 o = vred[g16 + 8][dq];
         vred[g16][dq] = make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
     }
@@ -995,9 +1014,17 @@ __global__ __launch_bounds__(256) void k_xattn(XAttnArgs a) {
         rr.x = rr.x + take_up<32>(rr.x); rr.y = rr.y + take_up<32>(rr.y); rr.z = rr.z + take_up<32>(rr.z); rr.w = rr.w + take_up<32>(rr.w);
         rr.x = rr.x + take_up<16>(rr.x); rr.y = rr.y + take_up<16>(rr.y); rr.z = rr.z + take_up<16>(rr.z); rr.w = rr.w + take_up<16>(rr.w);
         if (lane < 16) ((float4*)ol)[dq] = make_float4(0.0f + rr.x, 0.0f + rr.y, 0.0f + rr.z, 0.0f + rr.w);
-        put_act(a.out, r, h * 64 + lane, ol[lane], lane);
-        if (a.out_f) a.out_f[(size_t)r * a.dim + h * 64 + lane] = ol[lane];
+        put_act(out, r, h * 64 + lane, ol[lane], lane);
+        if (out_f) out_f[(size_t)r * dim + h * 64 + lane] = ol[lane];
     }
+}
+
+// cross-attention of each request's conditional stream: one block per (head, request)
+__global__ __launch_bounds__(256) void k_xattn(XAttnArgs a) {
+    const int h = blockIdx.x, r = blockIdx.y, H = gridDim.x;
+    const int nc = a.n_ctx;
+    xattn_head<16>(a.q + (size_t)r * a.dim + h * 64, a.k + ((size_t)r * H + h) * nc * 64,
+                   a.v + ((size_t)r * H + h) * nc * 64, nc, a.scale, a.out, a.out_f, a.dim, h, r);
 }
 
 // The hoisted cross K/V: projected [n_ctx][2*dim] -> K [H][n_ctx][64], V [H][n_ctx][64].
@@ -1374,22 +1401,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     // keep every load above in flight together: the scheduler would otherwise sink each next
     // to its first use and pay the memory latency once per leaf
     __builtin_amdgcn_sched_barrier(0);
-    // 2. every block's integer products first (independent matrix-core issues), then the
-    //    leaves in order, merged as a binary counter
-    mf_v4i pr[TILES][M][S];
-#pragma unroll
-    for (int j = 0; j < M; ++j) {
-        if (bitrev<LB>(j) >= NVL) continue;
-#pragma unroll
-        for (int s = 0; s < S; ++s)
-#pragma unroll
-            for (int t = 0; t < TILES; ++t) {
-                const mf_v4i z = {0, 0, 0, 0};
-                pr[t][j][s] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                    (long)(((unsigned long long)wa[t][j][s].y << 32) | wa[t][j][s].x),
-                    (long)(((unsigned long long)xb[j][s].y << 32) | xb[j][s].x), z, 0, 0, 0);
-            }
-    }
+    // 2. leaves in order, merged as a binary counter
     float4 lev[TILES][LB + 1];
 #pragma unroll
     for (int j = 0; j < M; ++j) {
@@ -1402,7 +1414,10 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
             for (int s = 0; s < S; ++s) {
 #pragma unroll
                 for (int t = 0; t < TILES; ++t) {
-                    const mf_v4i r = pr[t][j][s];
+                    const mf_v4i z = {0, 0, 0, 0};
+                    const mf_v4i r = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                        (long)(((unsigned long long)wa[t][j][s].y << 32) | wa[t][j][s].x),
+                        (long)(((unsigned long long)xb[j][s].y << 32) | xb[j][s].x), z, 0, 0, 0);
                     const float dx = xd[j][s];
                     const float d0 = h2f((uint16_t)(dw[t][j][s].x & 0xffffu)) * dx;
                     const float d1 = h2f((uint16_t)(dw[t][j][s].x >> 16)) * dx;
@@ -1590,7 +1605,25 @@ static void launch_gemv_mf(const GemvArgs& a, hipStream_t s) {
     }
 }
 
+bool gemv_xattn_ok(const GemvArgs& a) {
+    return a.epi == EPI_XATTN && a.ncol == 1 && a.pro == PRO_LN && (a.w.type == T_Q8_0 || a.w.type == T_Q4_0) &&
+           (a.w.in == 1024 || a.w.in == 1536 || a.w.in == 2048) && a.w.out == a.w.in && a.xn_ctx >= 1 && a.xn_ctx <= 64;
+}
+template <int WT> static void xattn_go(const GemvArgs& a, hipStream_t s) {
+    switch (a.w.in) {
+    case 1024: gemv_go<WT, 1, 4, 8, PRO_LN, EPI_XATTN, 4>(a, s); break;
+    case 1536: gemv_go<WT, 1, 4, 12, PRO_LN, EPI_XATTN, 4>(a, s); break;
+    default: gemv_go<WT, 1, 4, 16, PRO_LN, EPI_XATTN, 4>(a, s); break;
+    }
+}
+
 void launch_gemv(const GemvArgs& a0, hipStream_t s) {
+    if (a0.epi == EPI_XATTN) {   // the caller checks gemv_xattn_ok
+        if (!gemv_xattn_ok(a0)) return;
+        if (a0.w.type == T_Q8_0) xattn_go<T_Q8_0>(a0, s);
+        else xattn_go<T_Q4_0>(a0, s);
+        return;
+    }
     if (gemv_mf_ok(a0)) {
         launch_gemv_mf(a0, s);
         return;
