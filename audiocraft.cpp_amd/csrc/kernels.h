@@ -10,9 +10,8 @@ enum { ACT_Q8 = 0, ACT_F16 = 1, ACT_F32 = 2 };
 // GEMV prologues: LayerNorm of f32 columns, plain conversion of f32 columns, or a copy of
 // columns already in activation form -- all into LDS, while the weight loads are in flight.
 enum { PRO_LN = 0, PRO_F32 = 1, PRO_ACT = 2 };
-// GEMV epilogues: store, residual add, q + KV-cache append, GELU then activation form,
-// cross-attention of the block's head (cross.q: the block's 64 rows are one head's q).
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GELU_ACT = 3, EPI_XATTN = 4 };
+// GEMV epilogues: store, residual add, q + KV-cache append, GELU then activation form.
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GELU_ACT = 3 };
 
 constexpr int ATT_CHUNK = 256;   // keys per attention chunk (fixes the reduction order)
 constexpr int ATT_MAX_CHUNKS = 16;  // capacity up to 4096 positions
@@ -73,10 +72,8 @@ struct GemvArgs {
     float *k, *v;         // QKV: caches [col][heads][cap][64]
     int dim, heads, cap;
     const int* pos;       // QKV: device position
-    ActBuf dst;           // GELU_ACT / XATTN destination (XATTN: cross.out's activation)
-    float* dst_f;         // GELU_ACT / XATTN: optional f32 copy [col][dst.stride] (an adapted consumer's A x reads it)
-    int xn_ctx;           // XATTN: memory length; a.k / a.v = the layer's cross K / V [H][n_ctx][64]
-    float xscale;
+    ActBuf dst;           // GELU_ACT destination
+    float* dst_f;         // GELU_ACT: optional f32 copy [col][dst.stride] (an adapted consumer's A x reads it)
     // optional adapter on this projection (lora.h:50-83): y = Wx + s*B(Ax), DoRA rows scale
     // y by m / ||W + sBA||, then the strength blend; applied before the epilogue
     const float* ad_ax;   // [col][ad_rank] A x of the launch's columns; null = no adapter
@@ -150,9 +147,6 @@ void launch_weights_mf(const DevMat& w, int8_t* qm, hipStream_t s);
 // nch: the 256-key chunks of the position the launch runs at (the grid covers exactly these)
 void launch_attention(const AttnArgs& a, int nch, hipStream_t s);
 void launch_xattn(const XAttnArgs& a, int heads, int n_req, hipStream_t s);
-// cross.q with the cross-attention fused (EPI_XATTN, one column, LayerNorm prologue): true when
-// the weight type and width have a fused kernel (Q8_0 / Q4_0, dim 1024 / 1536 / 2048, n_ctx <= 64)
-bool gemv_xattn_ok(const GemvArgs& a);
 void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s);
 void launch_xkv_split(const float* kv, int n_ctx, int dim, float* k, float* v, hipStream_t s);
 void launch_sample(const SampleArgs& a, hipStream_t s);

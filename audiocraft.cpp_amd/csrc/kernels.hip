@@ -526,10 +526,6 @@ __device__ __forceinline__ float adapt(const GemvArgs& a, int row, int col, floa
                       a.ad_m ? a.ad_m[row] : 1.0f, a.ad_m ? a.ad_norm[row] : 1.0f, base);
 }
 
-template <int KEYQ>
-__device__ __forceinline__ void xattn_head(const float* qh, const float* K, const float* V, int nc, float scale,
-                                           const ActBuf& out, float* out_f, int dim, int h, int r);
-
 // U > 0: every lane owns exactly U units (units == G * U). U == 0: any unit count, a runtime
 // loop in passes of 8 units per lane (needs G == 8 so a pass covers each partial once).
 template <int WT, int NC, int G, int U, int PRO, int EPI, int WAVES>
@@ -668,16 +664,6 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
             if (n < ncol) v[n] = adapt(a, row, n, v[n]);
     }
     // 6. epilogue: lane 0 of each row group holds every column's value
-    if constexpr (EPI == EPI_XATTN) {
-        // the block's 64 rows are head blockIdx.x's q: LDS, then that head's cross-attention
-        static_assert(R == 64 && NC == 1 && NT == 256, "one head of q per 256-thread block");
-        if (t == 0) tile[wave * M + rl] = v[0];
-        lds_barrier();
-        const int h = blockIdx.x;
-        xattn_head<4>(tile, a.k + (size_t)h * a.xn_ctx * 64, a.v + (size_t)h * a.xn_ctx * 64, a.xn_ctx, a.xscale,
-                      a.dst, a.dst_f, a.dim, h, 0);
-        return;
-    }
     if constexpr (EPI == EPI_GELU_ACT) {
         // the block's R rows -> LDS tile -> GELU (one value per lane, spread over the waves)
         // -> activation form, one 32-row block per wave pass
@@ -1605,25 +1591,7 @@ static void launch_gemv_mf(const GemvArgs& a, hipStream_t s) {
     }
 }
 
-bool gemv_xattn_ok(const GemvArgs& a) {
-    return a.epi == EPI_XATTN && a.ncol == 1 && a.pro == PRO_LN && (a.w.type == T_Q8_0 || a.w.type == T_Q4_0) &&
-           (a.w.in == 1024 || a.w.in == 1536 || a.w.in == 2048) && a.w.out == a.w.in && a.xn_ctx >= 1 && a.xn_ctx <= 64;
-}
-template <int WT> static void xattn_go(const GemvArgs& a, hipStream_t s) {
-    switch (a.w.in) {
-    case 1024: gemv_go<WT, 1, 4, 8, PRO_LN, EPI_XATTN, 4>(a, s); break;
-    case 1536: gemv_go<WT, 1, 4, 12, PRO_LN, EPI_XATTN, 4>(a, s); break;
-    default: gemv_go<WT, 1, 4, 16, PRO_LN, EPI_XATTN, 4>(a, s); break;
-    }
-}
-
 void launch_gemv(const GemvArgs& a0, hipStream_t s) {
-    if (a0.epi == EPI_XATTN) {   // the caller checks gemv_xattn_ok
-        if (!gemv_xattn_ok(a0)) return;
-        if (a0.w.type == T_Q8_0) xattn_go<T_Q8_0>(a0, s);
-        else xattn_go<T_Q4_0>(a0, s);
-        return;
-    }
     if (gemv_mf_ok(a0)) {
         launch_gemv_mf(a0, s);
         return;

@@ -431,21 +431,13 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
             const size_t xl = (size_t)l * R * c.heads * s->n_ctx * 64;
             mgx::GemvArgs a = ga(L.w[P_CQ], R);
             pro_ln(a, s->x, s->cpr * D, L.ncw, L.ncb, c.norm_eps);
-            // one request: cross.q and the cross-attention in one launch (a block per head)
-            mgx::GemvArgs f = a;
-            f.epi = mgx::EPI_XATTN; f.k = s->xk + xl; f.v = s->xv + xl; f.xn_ctx = s->n_ctx; f.xscale = scale;
-            f.dim = D; f.dst = s->act_c.view(L.w[P_COUT].type, bc); f.dst_f = L.ad[P_COUT] ? s->act_c.f : nullptr;
-            if (mgx::gemv_xattn_ok(f)) {
-                gemv_ad(s, f, L.ad[P_CQ]);
-            } else {
-                epi_store(a, s->qc, D);
-                gemv_ad(s, a, L.ad[P_CQ]);
-                mgx::XAttnArgs xa{};
-                xa.q = s->qc; xa.k = s->xk + xl; xa.v = s->xv + xl; xa.n_ctx = s->n_ctx; xa.dim = D; xa.scale = scale;
-                xa.out = f.dst;
-                xa.out_f = f.dst_f;
-                mgx::launch_xattn(xa, c.heads, R, s->hs);
-            }
+            epi_store(a, s->qc, D);
+            gemv_ad(s, a, L.ad[P_CQ]);
+            mgx::XAttnArgs xa{};
+            xa.q = s->qc; xa.k = s->xk + xl; xa.v = s->xv + xl; xa.n_ctx = s->n_ctx; xa.dim = D; xa.scale = scale;
+            xa.out = s->act_c.view(L.w[P_COUT].type, bc);
+            xa.out_f = L.ad[P_COUT] ? s->act_c.f : nullptr;
+            mgx::launch_xattn(xa, c.heads, R, s->hs);
             mgx::GemvArgs b = ga(L.w[P_COUT], R);
             pro_act(b, s->act_c.view(L.w[P_COUT].type, bc));
             epi_store(b, s->x, s->cpr * D, true);

@@ -182,9 +182,8 @@ int32_t mgx_session_requests(const mgx_session* session);
    pipeline.cpp:15-18): with every > 0, each GEMV (kind 0) and self-attention (kind 1) launch
    of every `every`-th loop iteration records its span on the GPU's constant-rate wall clock
    (earliest block start to latest wave end -- a kernel tracer's duration; for attention, the
-   scores kernel's start to the reduce kernel's end). profile_read sums those milliseconds,
-   the algorithmic bytes (weights at their stored precision; f32 K and V of the keys
-   attended) and the launch count. */
+   scores kernel's start to the reduce kernel's end). profile_read sums those milliseconds, the algorithmic bytes (weights at their stored
+   precision; f32 K and V of the keys attended) and the launch count. */
 int mgx_session_profile(mgx_session* session, int32_t every);
 int mgx_session_profile_read(mgx_session* session, int32_t kind, double* ms_total, double* bytes_total,
                              int32_t* launches);
