@@ -160,22 +160,21 @@ __device__ __forceinline__ float mat_elem(const DevMat& m, int r, int i) {
     }
 }
 
+// one block per (256 elements, request): request r's columns r*cols_per_req.. all get its sum
 __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int i = blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
     if (i >= a.dim) return;
     const int p = *a.pos;
     const float tab = a.table[(size_t)p * a.dim + i];
-    for (int r = 0; r * a.cols_per_req < a.ncol; ++r) {
-        const int32_t* ids = a.ids + (size_t)r * a.ids_req_stride;
-        float e = 0.0f;
-        for (int q = 0; q < a.n_q; ++q) {
-            const int id = ids[(size_t)q * a.ids_stride + (p - a.ids_base)];
-            const float v = mat_elem(a.emb[q], id, i);
-            e = q == 0 ? v : e + v;
-        }
-        const float x = tab + e;
-        for (int n = r * a.cols_per_req; n < (r + 1) * a.cols_per_req && n < a.ncol; ++n) a.x[(size_t)n * a.dim + i] = x;
+    const int32_t* ids = a.ids + (size_t)r * a.ids_req_stride;
+    float e = 0.0f;
+    for (int q = 0; q < a.n_q; ++q) {
+        const int id = ids[(size_t)q * a.ids_stride + (p - a.ids_base)];
+        const float v = mat_elem(a.emb[q], id, i);
+        e = q == 0 ? v : e + v;
     }
+    const float x = tab + e;
+    for (int n = r * a.cols_per_req; n < (r + 1) * a.cols_per_req && n < a.ncol; ++n) a.x[(size_t)n * a.dim + i] = x;
 }
 
 __global__ void k_advance(int* pos) { *pos = *pos + 1; }
@@ -1295,7 +1294,8 @@ __global__ __launch_bounds__(256) void k_repack(int type, const uint8_t* raw, in
 // launchers
 // ------------------------------------------------------------------------------------
 void launch_embed(const EmbedArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed, dim3((a.dim + 255) / 256), dim3(256), 0, s, a);
+    const int nreq = (a.ncol + a.cols_per_req - 1) / a.cols_per_req;
+    hipLaunchKernelGGL(k_embed, dim3((a.dim + 255) / 256, nreq), dim3(256), 0, s, a);
 }
 void launch_advance(int* pos, hipStream_t s) { hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, s, pos); }
 void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s) {
@@ -1376,13 +1376,18 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     const int ad_nb = a.ad_ax ? ROWS * a.ad_rank : 0, ad_nx = a.ad_ax ? ad_nb + ncol * a.ad_rank : 0;
     const int ad_n = ad_nx + (a.ad_ax && a.ad_m ? 2 * ROWS : 0);
     float adr[AD_PER];
+    if (a.ad_ax) {
+        // one unconditional load per slot: the address is selected, slots past the end re-read B[0]
 #pragma unroll
-    for (int k = 0; k < AD_PER; ++k) {
-        const int e = tid + 64 * KW * k;
-        adr[k] = e < ad_nb ? a.ad_B[(size_t)row0 * a.ad_rank + e]
-               : e < ad_nx ? a.ad_ax[e - ad_nb]
-               : e < ad_nx + ROWS ? (e < ad_n ? a.ad_m[row0 + e - ad_nx] : 0.0f)
-               : (e < ad_n ? a.ad_norm[row0 + e - ad_nx - ROWS] : 0.0f);
+        for (int k = 0; k < AD_PER; ++k) {
+            const int e = tid + 64 * KW * k;
+            const float* src = e < ad_nb ? a.ad_B + (size_t)row0 * a.ad_rank + e
+                             : e < ad_nx ? a.ad_ax + (e - ad_nb)
+                             : e >= ad_n ? a.ad_B
+                             : e < ad_nx + ROWS ? a.ad_m + row0 + (e - ad_nx)
+                             : a.ad_norm + row0 + (e - ad_nx - ROWS);
+            adr[k] = *src;
+        }
     }
     // keep every load above in flight together: the scheduler would otherwise sink each next
     // to its first use and pay the memory latency once per leaf
@@ -1545,12 +1550,13 @@ template <int WT> static void gemv_wt(const GemvArgs& a, hipStream_t s) {
 // Columns go in groups of two (every per-column pointer advanced by the group's offset).
 // ---- matrix-core GEMV: (blocks per row, waves per 16-row tile) choices
 static int mf_kw(int nb, int tiles_out) {
-    const int base = nb >= 128 ? (nb == 256 ? 16 : 8) : 4;
+    const int base = nb >= 128 ? 8 : 4;
     const int kw = tiles_out >= 256 ? base : 16;
     return nb % kw == 0 ? kw : base;
 }
+// widths 128 .. 6144 (8192 would need more than the 128 registers of a 1024-thread block)
 static bool mf_width(int nb) {
-    return nb == 4 || nb == 16 || nb == 32 || nb == 48 || nb == 64 || nb == 128 || nb == 192 || nb == 256;
+    return nb == 4 || nb == 16 || nb == 32 || nb == 48 || nb == 64 || nb == 128 || nb == 192;
 }
 bool gemv_mf_ok(const GemvArgs& a) {
     const int rows = a.epi == EPI_GELU_ACT ? 32 : 16;
@@ -1586,8 +1592,7 @@ static void launch_gemv_mf(const GemvArgs& a, hipStream_t s) {
     case 48: mf_nb<48>(a, s); break;
     case 64: mf_nb<64>(a, s); break;
     case 128: mf_nb<128>(a, s); break;
-    case 192: mf_nb<192>(a, s); break;
-    default: mf_nb<256>(a, s); break;
+    default: mf_nb<192>(a, s); break;
     }
 }
 
@@ -1742,10 +1747,47 @@ static void prep_launch(const GemvArgs& a, hipStream_t s) {
     default: prep_go<8>(a, s); break;
     }
 }
+// A x of an f32 column (the f32 copy of an activation-form input), straight from global memory:
+// one wave per (column, rank row); lane l sums the 8-element units l, l + 64, ... in element
+// order (fmaf) -- NU of them, all loaded before the first product -- and the 64 partials fold
+// by the butterfly: the same values k_prep's "A x" role computes from its LDS copy.
+template <int NU>
+__global__ __launch_bounds__(64) void k_ax_f32(GemvArgs a) {
+    const int col = blockIdx.x, k = blockIdx.y, lane = threadIdx.x, units = a.w.in / 8;
+    const float* A = (const float*)a.w.q + (size_t)k * a.w.in;
+    const float* x = a.x + (size_t)col * a.x_stride;
+    float4 w0[NU], w1[NU], x0[NU], x1[NU];
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+        const int u0 = lane + 64 * i, u = u0 < units ? u0 : units - 1;
+        w0[i] = *(const float4*)(A + 8 * u); w1[i] = *(const float4*)(A + 8 * u + 4);
+        x0[i] = *(const float4*)(x + 8 * u); x1[i] = *(const float4*)(x + 8 * u + 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // every load in flight before the first product
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+        if (lane + 64 * i >= units) break;
+        p = __builtin_fmaf(w0[i].x, x0[i].x, p); p = __builtin_fmaf(w0[i].y, x0[i].y, p);
+        p = __builtin_fmaf(w0[i].z, x0[i].z, p); p = __builtin_fmaf(w0[i].w, x0[i].w, p);
+        p = __builtin_fmaf(w1[i].x, x1[i].x, p); p = __builtin_fmaf(w1[i].y, x1[i].y, p);
+        p = __builtin_fmaf(w1[i].z, x1[i].z, p); p = __builtin_fmaf(w1[i].w, x1[i].w, p);
+    }
+    p = fold64(p);
+    if (lane == 0) a.y[(size_t)col * a.y_stride + k] = p;
+}
 void launch_adapter_ax(const GemvArgs& a0, hipStream_t s) {
     GemvArgs a = a0;
     a.dst = ActBuf{};
-    prep_launch(a, s);
+    if (a.pro != PRO_F32) { prep_launch(a, s); return; }
+    const dim3 grid(a.ncol, a.w.out);
+    const int nu = (a.w.in / 8 + 63) / 64;
+    if (nu <= 1) hipLaunchKernelGGL(k_ax_f32<1>, grid, dim3(64), 0, s, a);
+    else if (nu <= 2) hipLaunchKernelGGL(k_ax_f32<2>, grid, dim3(64), 0, s, a);
+    else if (nu <= 4) hipLaunchKernelGGL(k_ax_f32<4>, grid, dim3(64), 0, s, a);
+    else if (nu <= 8) hipLaunchKernelGGL(k_ax_f32<8>, grid, dim3(64), 0, s, a);
+    else if (nu <= 12) hipLaunchKernelGGL(k_ax_f32<12>, grid, dim3(64), 0, s, a);
+    else hipLaunchKernelGGL(k_ax_f32<16>, grid, dim3(64), 0, s, a);
 }
 void launch_act_prep(const GemvArgs& a, hipStream_t s) { prep_launch(a, s); }
 
@@ -1776,36 +1818,47 @@ void launch_scales_t(const DevMat& w, uint16_t* dt, hipStream_t s) {
     hipLaunchKernelGGL(k_scales_t, dim3((w.out * nb + 255) / 256), dim3(256), 0, s, w.d, nb, w.out, dt);
 }
 
-// DoRA rows (lora.h:11-32): one thread per row, sequential double sums over the row.
+// DoRA rows (lora.h:11-32): one block per row. The block computes the row's dequantized weights
+// and (BA)_i = (float) sum_k B[r][k] A[k][i] (double, k in order) for a segment of the row into
+// LDS; thread 0 then adds the segment to the three double sums, each in increasing i.
+constexpr int DORA_SEG = 2048;
 __global__ __launch_bounds__(64) void k_dora_norm(DevMat w, const float* A, const float* B, int rank, float scale,
                                                   float* norm, int* bad) {
-    const int r = blockIdx.x * 64 + threadIdx.x;
-    if (r >= w.out) return;
-    const int in = w.in;
-    double sum = (double)in * 1e-12;
+    __shared__ float wv[DORA_SEG], bav[DORA_SEG];
+    const int r = blockIdx.x, tid = threadIdx.x, in = w.in;
+    double sum = (double)in * 1e-12, t2 = 0.0, t3 = 0.0;
     int nonfinite = 0;
-    for (int i = 0; i < in; ++i) {
-        const float x = mat_elem(w, r, i);
-        nonfinite |= !__builtin_isfinite(x);
-        sum += (double)x * x;
+    for (int i0 = 0; i0 < in; i0 += DORA_SEG) {
+        const int n = in - i0 < DORA_SEG ? in - i0 : DORA_SEG;
+        for (int j = tid; j < n; j += 64) {
+            double acc = 0.0;
+            for (int k = 0; k < rank; ++k) acc += (double)B[(size_t)r * rank + k] * A[(size_t)k * in + i0 + j];
+            bav[j] = (float)acc;
+            const float x = mat_elem(w, r, i0 + j);
+            nonfinite |= !__builtin_isfinite(x);
+            wv[j] = x;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int j = 0; j < n; ++j) {
+                const float x = wv[j], ba = bav[j];
+                sum += (double)x * x;
+                t2 += (double)x * ba;
+                t3 += (double)ba * ba;
+            }
+        }
+        __syncthreads();
     }
-    const float base = (float)sum;
-    double t2 = 0.0, t3 = 0.0;
-    for (int i = 0; i < in; ++i) {
-        double acc = 0.0;
-        for (int k = 0; k < rank; ++k) acc += (double)B[(size_t)r * rank + k] * A[(size_t)k * in + i];
-        const float ba = (float)acc;
-        const float x = mat_elem(w, r, i);
-        t2 += (double)x * ba;
-        t3 += (double)ba * ba;
+    if (tid == 0) {
+        const float base = (float)sum;
+        const double nsq = (double)base + 2.0 * scale * t2 + (double)scale * scale * t3;
+        norm[r] = (float)__builtin_sqrt(nsq);
     }
-    const double nsq = (double)base + 2.0 * scale * t2 + (double)scale * scale * t3;
-    norm[r] = (float)__builtin_sqrt(nsq);
     if (nonfinite) atomicOr(bad, 1);
 }
 void launch_dora_norm(const DevMat& w, const float* A, const float* B, int rank, float scale, float* norm, int* bad,
                       hipStream_t s) {
-    hipLaunchKernelGGL(k_dora_norm, dim3((w.out + 63) / 64), dim3(64), 0, s, w, A, B, rank, scale, norm, bad);
+    hipLaunchKernelGGL(k_dora_norm, dim3(w.out), dim3(64), 0, s, w, A, B, rank, scale, norm, bad);
 }
 void launch_repack(int type, const uint8_t* raw, int64_t rows, int in, void* q, uint16_t* d, hipStream_t s) {
     const int64_t nblocks = rows * (in / 32);
