@@ -592,6 +592,24 @@ void make_stream(mgx_model* m, int capacity, int n_seq, int n_req, const float* 
 
 }  // namespace
 
+// library-internal (gguf.cpp): the status/message convention, and a projection's (in, out)
+__attribute__((visibility("hidden"))) int mgx_internal_set_error(int code, const char* msg) {
+    g_error = msg ? msg : "";
+    return code;
+}
+__attribute__((visibility("hidden"))) bool mgx_internal_proj_shape(const mgx_model* m, const char* name, int64_t* in,
+                                                                    int64_t* out) {
+    if (!m || !name) return false;
+    for (int l = 0; l < m->c.layers; ++l)
+        for (int k = 0; k < P_COUNT; ++k)
+            if (std::string(name) == "lm." + std::to_string(l) + "." + PROJ[k] + ".weight") {
+                *in = m->L[(size_t)l].w[k].in;
+                *out = m->L[(size_t)l].w[k].out;
+                return true;
+            }
+    return false;
+}
+
 extern "C" {
 
 const char* mgx_last_error(void) { return g_error.c_str(); }

@@ -56,7 +56,9 @@ EXPORTS = ["mgx_model_create", "mgx_model_set_adapters", "mgx_model_destroy", "m
            "mgx_stream_destroy", "mgx_use_guidance", "mgx_generate", "mgx_session_create", "mgx_session_step",
            "mgx_session_remaining", "mgx_session_finish", "mgx_session_destroy", "mgx_session_profile",
            "mgx_session_profile_read", "mgx_session_hip_stream", "mgx_batch_create", "mgx_batch_finish",
-           "mgx_session_requests", "mgx_last_error"]
+           "mgx_session_requests", "mgx_gguf_open", "mgx_gguf_close", "mgx_gguf_tensor_count", "mgx_gguf_tensor",
+           "mgx_gguf_find_tensor", "mgx_gguf_u32", "mgx_gguf_f32", "mgx_gguf_string", "mgx_gguf_lm_config",
+           "mgx_model_create_from_gguf", "mgx_model_set_adapters_from_gguf", "mgx_last_error"]
 
 _lib = None
 
@@ -104,6 +106,18 @@ def load(path=None):
                                      C.POINTER(P)]
     lib.mgx_batch_finish.argtypes = [P, C.c_int32, P, P, P, C.POINTER(GenerateReport)]
     lib.mgx_session_requests.argtypes = [P]
+    lib.mgx_gguf_open.argtypes = [C.c_char_p, C.POINTER(P)]
+    lib.mgx_gguf_close.argtypes = [P]
+    lib.mgx_gguf_close.restype = None
+    lib.mgx_gguf_tensor_count.argtypes = [P]
+    lib.mgx_gguf_tensor.argtypes = [P, C.c_int32, C.POINTER(Tensor)]
+    lib.mgx_gguf_find_tensor.argtypes = [P, C.c_char_p, C.POINTER(Tensor)]
+    lib.mgx_gguf_u32.argtypes = [P, C.c_char_p, C.POINTER(C.c_uint32)]
+    lib.mgx_gguf_f32.argtypes = [P, C.c_char_p, C.POINTER(C.c_float)]
+    lib.mgx_gguf_string.argtypes = [P, C.c_char_p, C.c_char_p, C.c_uint64, C.POINTER(C.c_uint64)]
+    lib.mgx_gguf_lm_config.argtypes = [P, C.POINTER(LmConfig)]
+    lib.mgx_model_create_from_gguf.argtypes = [P, C.POINTER(P)]
+    lib.mgx_model_set_adapters_from_gguf.argtypes = [P, P, P, C.c_float]
     if path is None:
         _lib = lib
     return lib
@@ -141,6 +155,22 @@ class Model:
         h = C.c_void_p()
         _check(self.lib, self.lib.mgx_model_create(C.byref(config), arr, len(tensors), C.byref(h)))
         self.handle = h
+
+    @classmethod
+    def from_gguf(cls, gguf):
+        """mgx_model_create_from_gguf: LmConfig::from + every tensor of an open Gguf."""
+        m = cls.__new__(cls)
+        m.lib = load()
+        m.config = gguf.lm_config()
+        h = C.c_void_p()
+        _check(m.lib, m.lib.mgx_model_create_from_gguf(gguf.handle, C.byref(h)))
+        m.handle = h
+        return m
+
+    def set_adapters_from_gguf(self, adapter, base=None, strength=1.0):
+        """mgx_model_set_adapters_from_gguf: load_mg_lora on an open adapter Gguf."""
+        _check(self.lib, self.lib.mgx_model_set_adapters_from_gguf(self.handle, adapter.handle,
+                                                                   base.handle if base else None, strength))
 
     def set_adapters(self, adapters):
         """mgx_model_set_adapters. adapters: dicts with target, A [rank][in], B [out][rank],
@@ -190,6 +220,58 @@ class Model:
                                                _ptr(prompt), prompt_len, C.byref(params), _ptr(codes), _ptr(first),
                                                _ptr(steps), C.byref(rep)))
         return codes, first, rep, steps
+
+
+class Gguf:
+    """mgx_gguf: a GGUF file mapped read-only (GgufModel without ggml)."""
+
+    def __init__(self, path):
+        self.lib = load()
+        h = C.c_void_p()
+        _check(self.lib, self.lib.mgx_gguf_open(str(path).encode(), C.byref(h)))
+        self.handle = h
+
+    def tensors(self):
+        """[(name, ggml type, ne (4), nbytes, bytes)] in file order."""
+        out = []
+        for i in range(self.lib.mgx_gguf_tensor_count(self.handle)):
+            t = Tensor()
+            _check(self.lib, self.lib.mgx_gguf_tensor(self.handle, i, C.byref(t)))
+            out.append((t.name.decode(), t.type, tuple(t.ne), t.nbytes, C.string_at(t.data, t.nbytes)))
+        return out
+
+    def u32(self, key):
+        v = C.c_uint32()
+        _check(self.lib, self.lib.mgx_gguf_u32(self.handle, key.encode(), C.byref(v)))
+        return v.value
+
+    def f32(self, key):
+        v = C.c_float()
+        _check(self.lib, self.lib.mgx_gguf_f32(self.handle, key.encode(), C.byref(v)))
+        return v.value
+
+    def string(self, key):
+        n = C.c_uint64()
+        _check(self.lib, self.lib.mgx_gguf_string(self.handle, key.encode(), None, 0, C.byref(n)))
+        buf = C.create_string_buffer(n.value + 1)
+        _check(self.lib, self.lib.mgx_gguf_string(self.handle, key.encode(), buf, n.value + 1, None))
+        return buf.value.decode()
+
+    def lm_config(self):
+        c = LmConfig()
+        _check(self.lib, self.lib.mgx_gguf_lm_config(self.handle, C.byref(c)))
+        return c
+
+    def close(self):
+        if self.handle:
+            self.lib.mgx_gguf_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Stream:

@@ -190,6 +190,31 @@ int mgx_session_profile_read(mgx_session* session, int32_t kind, double* ms_tota
 /* The hipStream_t the session's kernels run on. */
 void* mgx_session_hip_stream(mgx_session* session);
 
+/* GGUF files without ggml: GgufModel / load_gguf (src/gguf_model.h:241-414) for what the LM
+   needs. mgx_gguf_open maps the file read-only and checks the header, every key/value and every
+   tensor's extent against the file size (load_gguf's short-read check, gguf_model.h:384-389);
+   GGUF v2 and v3, tensor types F32 / F16 / BF16 / Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q8_0. Tensor data
+   pointers point into the mapping and stay valid until mgx_gguf_close. */
+typedef struct mgx_gguf mgx_gguf;
+int mgx_gguf_open(const char* path, mgx_gguf** out);
+void mgx_gguf_close(mgx_gguf* gguf);
+int32_t mgx_gguf_tensor_count(const mgx_gguf* gguf);
+int mgx_gguf_tensor(const mgx_gguf* gguf, int32_t index, mgx_tensor* out);
+int mgx_gguf_find_tensor(const mgx_gguf* gguf, const char* name, mgx_tensor* out);   /* GgufModel::get */
+/* GgufModel::u32 / f32 / string (gguf_model.h:273-305): "missing key: ..." or a type error. */
+int mgx_gguf_u32(const mgx_gguf* gguf, const char* key, uint32_t* out);
+int mgx_gguf_f32(const mgx_gguf* gguf, const char* key, float* out);
+int mgx_gguf_string(const mgx_gguf* gguf, const char* key, char* buf, uint64_t capacity, uint64_t* length);
+/* LmConfig::from (src/mg/lm.h:60-90): the ac.* keys and their checks. */
+int mgx_gguf_lm_config(const mgx_gguf* gguf, mgx_lm_config* out);
+/* load_gguf + LmConfig::from + mgx_model_create in one call; the file may be closed afterwards. */
+int mgx_model_create_from_gguf(const mgx_gguf* gguf, mgx_model** out);
+/* load_mg_lora (lora.h:113-176, 195-210) on an adapter file (general.architecture
+   "ac-musicgen-lora"): version, rank, alpha, type, the .lora_A / .lora_B (/ .magnitude) tensors
+   and their shapes against the model, the base-name check when `base` is given; then
+   mgx_model_set_adapters. The adapter file must stay open while the call runs only. */
+int mgx_model_set_adapters_from_gguf(mgx_model* model, const mgx_gguf* adapter, const mgx_gguf* base, float strength);
+
 /* The message of the last failed call on this thread. */
 const char* mgx_last_error(void);
 
