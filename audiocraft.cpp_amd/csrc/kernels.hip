@@ -1658,8 +1658,71 @@ void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
     }
     hipLaunchKernelGGL(k_attn_reduce, dim3(a.heads, a.ncol), dim3(64), 0, s, a);
 }
+// The same cross-attention for n_ctx <= 64 with one wave per (head, request) and no block
+// barrier on the critical path. Equal orders: a key's 16 four-dim partials (lanes t of a
+// 16-lane group) fold by the butterfly (lane t adds lane t+off, off 8..1: lane 0 ends with the
+// butterfly's value); the 256-key double sum is the 64-wide butterfly of the first 64 keys (the
+// others are exact zeros: (e + 0) + (0 + 0) = e); lane d sums dimension d's 16 key-strided
+// partials (key mod 16, fmaf in key order) and folds them by the butterfly in registers.
+__global__ __launch_bounds__(64) void k_xattn_w(XAttnArgs a) {
+    const int h = blockIdx.x, r = blockIdx.y, H = gridDim.x, lane = threadIdx.x, g = lane >> 4, t = lane & 15;
+    const int nc = a.n_ctx;
+    const float* K = a.k + ((size_t)r * H + h) * nc * 64;
+    const float* V = a.v + ((size_t)r * H + h) * nc * 64;
+    __shared__ float pj[64];
+    // every load first: q, the keys' float4s (key 4*it + g), then V column `lane` of each key
+    const float4 q = ((const float4*)(a.q + (size_t)r * a.dim + h * 64))[t];
+    float4 kv[16];
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+        const int j = 4 * it + g, jl = j < nc ? j : nc - 1;
+        kv[it] = ((const float4*)(K + (size_t)jl * 64))[t];
+    }
+    float vv[64];
+#pragma unroll
+    for (int j = 0; j < 64; ++j) vv[j] = V[(size_t)(j < nc ? j : nc - 1) * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
+    // scores: lane (g, 0) holds key 4*it + g after the fold
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+        if (4 * it >= nc) break;
+        float v = __builtin_fmaf(q.x, kv[it].x, 0.0f);
+        v = __builtin_fmaf(q.y, kv[it].y, v);
+        v = __builtin_fmaf(q.z, kv[it].z, v);
+        v = __builtin_fmaf(q.w, kv[it].w, v);
+        v = v + take_up<8>(v);
+        v = v + take_up<4>(v);
+        v = v + take_up<2>(v);
+        v = v + take_up<1>(v);
+        if (t == 0) pj[4 * it + g] = v * a.scale;
+    }
+    __syncthreads();
+    const float sc = lane < nc ? pj[lane] : -__builtin_inff();
+    float M = sc;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(M, off); M = M > o ? M : o; }
+    const float e = lane < nc ? dexpf(sc - M) : 0.0f;
+    const float inv = (float)(1.0 / (0.0 + fold64d_b((double)e)));
+    __syncthreads();
+    pj[lane] = e * inv;
+    __syncthreads();
+    float acc[16];
+#pragma unroll
+    for (int gg = 0; gg < 16; ++gg) acc[gg] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 64; ++j)
+        if (j < nc) acc[j & 15] = __builtin_fmaf(pj[j], vv[j], acc[j & 15]);
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1)
+#pragma unroll
+        for (int gg = 0; gg < off; ++gg) acc[gg] = acc[gg] + acc[gg + off];
+    const float o = 0.0f + acc[0];
+    put_act(a.out, r, h * 64 + lane, o, lane);
+    if (a.out_f) a.out_f[(size_t)r * a.dim + h * 64 + lane] = o;
+}
 void launch_xattn(const XAttnArgs& a, int heads, int n_req, hipStream_t s) {
-    hipLaunchKernelGGL(k_xattn, dim3(heads, n_req), dim3(256), 0, s, a);
+    if (a.n_ctx <= 64) hipLaunchKernelGGL(k_xattn_w, dim3(heads, n_req), dim3(64), 0, s, a);
+    else hipLaunchKernelGGL(k_xattn, dim3(heads, n_req), dim3(256), 0, s, a);
 }
 void launch_xkv_split(const float* kv, int n_ctx, int dim, float* k, float* v, hipStream_t s) {
     hipLaunchKernelGGL(k_xkv_split, dim3((n_ctx * 2 * dim + 255) / 256), dim3(256), 0, s, kv, n_ctx, dim, k, v);
