@@ -51,7 +51,7 @@ struct EmbedArgs {
     int ids_stride, ids_base;
     int ids_req_stride, cols_per_req;   // column n reads request n / cols_per_req's ids (+ that * ids_req_stride)
     const float* table;   // sinusoid [capacity][dim]
-    const int* pos;       // device position of this step
+    const int* pos;       // [request] device position of this step
     int dim;
     float* x;             // [ncol][dim]
     int ncol;
@@ -71,7 +71,8 @@ struct GemvArgs {
     int y_stride;
     float *k, *v;         // QKV: caches [col][heads][cap][64]
     int dim, heads, cap;
-    const int* pos;       // QKV: device position
+    const int* pos;       // QKV: [request] device positions; column n belongs to request n / cpr
+    int cpr;
     ActBuf dst;           // GELU_ACT destination
     float* dst_f;         // GELU_ACT: optional f32 copy [col][dst.stride] (an adapted consumer's A x reads it)
     // optional adapter on this projection (lora.h:50-83): y = Wx + s*B(Ax), DoRA rows scale
@@ -82,6 +83,9 @@ struct GemvArgs {
     const float* ad_norm; // [out] ||W + sBA|| per row (DoRA)
     int ad_rank;
     float ad_scale, ad_strength;
+    // optional per-column gate (STORE / RESID): columns whose gate is 0 keep their destination
+    const int* gate;
+    int col0;             // the launch's first column in the caller's numbering (pos, gate)
     unsigned long long* stamp;   // optional [64][2]: per-sub-slot earliest start, latest end (GPU wall clock)
 };
 
@@ -94,7 +98,8 @@ struct AttnArgs {
     float* cmax;          // [col][heads][max_chunks * ATT_SUBS] score-block maxima
     int dim, heads, cap, max_chunks, ncol;
     float scale;
-    const int* pos;       // device position: keys [0, pos]
+    const int* pos;       // [request] device positions: column n attends keys [0, pos[n / cpr]]
+    int cpr;
     ActBuf out;           // the out-projection's activation
     float* out_f;         // optional f32 copy [col][dim] (an adapted out-projection's A x reads it)
     unsigned long long* stamp;   // optional [64][2]: scores' earliest starts, reduce's latest ends
@@ -105,7 +110,8 @@ struct XAttnArgs {
     const float* q;   // [n_req][dim]
     const float* k;   // [n_req][heads][n_ctx][64]
     const float* v;
-    int n_ctx, dim;
+    int n_ctx, dim;   // n_ctx: the rows per head (every request's count when nc is null)
+    const int* nc;    // optional [n_req] conditioning tokens per request (0: writes zeros)
     float scale;
     ActBuf out;       // cross.out's activation, column r
     float* out_f;     // optional f32 copy [n_req][dim]
@@ -113,20 +119,32 @@ struct XAttnArgs {
 
 constexpr int MAX_REQ = 16;      // requests of one batched session
 
-// One block per (codebook, request). Request r's arrays sit at r * (their per-request size).
+// A request's sampling parameters and loop bounds, in device memory (one per request) so that
+// a captured step serves whichever requests a batch holds.
+struct ReqParams {
+    float cfg_coef, temperature;
+    int use_sampling, top_k, guided;
+    int start, steps;   // the loop runs offsets start .. steps - 1 (pipeline.cpp:255-302)
+    int pad;
+};
+
+// One block per (codebook, request). Request r samples at offset pos[r] + 1 when that offset
+// is in [start, steps) and, with `live` set, live[r] != 0.
 struct SampleArgs {
-    const float* logits;     // [n_req][guided ? 2 : 1][n_q][card]
-    int n_q, card, guided, n_req;
-    const uint8_t* mask;     // [n_q][steps] (the same delay pattern for every request)
-    int steps, start;
-    const int* pos;          // the loop offset is *pos + 1
+    const float* logits;     // [n_req][cpr][n_q][card]: column 0 conditional, column 1 null
+    int n_q, card, n_req, cpr;
+    const ReqParams* par;    // [n_req]
+    const int* pos;          // [n_req]
+    const int* live;         // [n_req] or null (every request)
+    int seq_len;             // row length of mask, uniforms and seq
+    const uint8_t* mask;     // request r's at mask + r * mask_stride: [n_q][seq_len]
+    long long mask_stride;   // 0: one delay pattern for every request
     int special;
-    const float* uniforms;   // [n_req][steps][n_q]
-    int32_t* seq;            // [n_req][n_q][steps]
+    const float* uniforms;   // [n_req][seq_len][n_q]
+    int32_t* seq;            // [n_req][n_q][seq_len]
     float* first_logits;     // [n_req][n_q][card], written at offset == start
-    float* step_logits;      // [n_req][steps - start][n_q][card] or null
-    float cfg_coef[MAX_REQ], temperature[MAX_REQ];
-    int use_sampling[MAX_REQ], top_k[MAX_REQ];
+    float* step_logits;      // [n_req][step_rows][n_q][card] (row offset - start) or null
+    int step_rows;
 };
 
 void launch_embed(const EmbedArgs& a, hipStream_t s);
@@ -148,9 +166,16 @@ void launch_weights_mf(const DevMat& w, int8_t* qm, hipStream_t s);
 void launch_attention(const AttnArgs& a, int nch, hipStream_t s);
 void launch_xattn(const XAttnArgs& a, int heads, int n_req, hipStream_t s);
 void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s);
-void launch_xkv_split(const float* kv, int n_ctx, int dim, float* k, float* v, hipStream_t s);
+// rows: the row count per head of k and v (>= n_ctx)
+void launch_xkv_split(const float* kv, int n_ctx, int rows, int dim, float* k, float* v, hipStream_t s);
 void launch_sample(const SampleArgs& a, hipStream_t s);
-void launch_advance(int* pos, hipStream_t s);
+// The position step after a forward: with live null every request's position advances; with
+// live set only live requests advance, and one whose next offset would reach par.steps
+// retires (live 0, position 0).
+void launch_advance(int* pos, int* live, const ReqParams* par, int n_req, hipStream_t s);
+// Opens request r of a slotted batch: position 0, live, its parameters and conditioning length.
+void launch_slot_open(int* pos, int* live, ReqParams* par, int* nc, int r, const ReqParams& p, int n_ctx,
+                      hipStream_t s);
 // fills n launch-timing slots (64 sub-slots each) with {UINT64_MAX, 0}
 // A x for an adapter (w = A as an f32 matrix [rank][in]; pro LN or F32 with x / x_stride /
 // ln_*; y = [col][y_stride]), the column built as the adapted projection builds it

@@ -164,7 +164,7 @@ __device__ __forceinline__ float mat_elem(const DevMat& m, int r, int i) {
 __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
     const int i = blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
     if (i >= a.dim) return;
-    const int p = *a.pos;
+    const int p = a.pos[r];
     const float tab = a.table[(size_t)p * a.dim + i];
     const int32_t* ids = a.ids + (size_t)r * a.ids_req_stride;
     float e = 0.0f;
@@ -177,7 +177,21 @@ __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
     for (int n = r * a.cols_per_req; n < (r + 1) * a.cols_per_req && n < a.ncol; ++n) a.x[(size_t)n * a.dim + i] = x;
 }
 
-__global__ void k_advance(int* pos) { *pos = *pos + 1; }
+__global__ __launch_bounds__(64) void k_advance(int* pos, int* live, const ReqParams* par, int n) {
+    const int r = threadIdx.x;
+    if (r >= n) return;
+    if (!live) { pos[r] = pos[r] + 1; return; }
+    if (!live[r]) return;
+    const int np = pos[r] + 1;
+    if (np + 1 >= par[r].steps) { live[r] = 0; pos[r] = 0; }
+    else pos[r] = np;
+}
+
+__global__ __launch_bounds__(64) void k_slot_open(int* pos, int* live, ReqParams* par, int* nc, int r, ReqParams p,
+                                                  int n_ctx) {
+    if (threadIdx.x != 0) return;
+    pos[r] = 0; live[r] = 1; par[r] = p; nc[r] = n_ctx;
+}
 
 __global__ __launch_bounds__(256) void k_add_bias(float* y, const float* b, int n, int ncol) {
     const int i = blockIdx.x * 256 + threadIdx.x;
@@ -706,12 +720,12 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
     for (int n = 0; n < NC; ++n) {
         if (n >= ncol) break;
         const float r = v[n];
-        if (EPI == EPI_STORE) a.y[(size_t)n * a.y_stride + row] = r;
-        else if (EPI == EPI_RESID) a.y[(size_t)n * a.y_stride + row] = yo[n] + r;
+        if (EPI == EPI_STORE) { if (!a.gate || a.gate[a.col0 + n]) a.y[(size_t)n * a.y_stride + row] = r; }
+        else if (EPI == EPI_RESID) { if (!a.gate || a.gate[a.col0 + n]) a.y[(size_t)n * a.y_stride + row] = yo[n] + r; }
         else {
             const int sec = row / a.dim, wi = row - sec * a.dim, head = wi >> 6, dm = wi & 63;
             if (sec == 0) a.y[(size_t)n * a.dim + wi] = r;
-            else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + *a.pos) * 64 + dm] = r;
+            else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + a.pos[(a.col0 + n) / a.cpr]) * 64 + dm] = r;
         }
     }
 }
@@ -767,7 +781,7 @@ __device__ __forceinline__ float halving4(const float (&p)[4], int t) {
 __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
     const unsigned long long t0 = stamp_begin(a.stamp);
     const int b = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
-    const int u = *a.pos + 1;
+    const int u = a.pos[n / a.cpr] + 1;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, t = lane & 15;
     const size_t head = (size_t)n * a.heads + h;
     const float* K = a.k + head * a.cap * 64;
@@ -836,7 +850,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_attn_pv(AttnArgs a) {
     const int g = (wave & 3) * 4 + (lane >> 4), dq = lane & 15;
     const float* V = a.v + head * a.cap * 64;
     float4 vv[16];
-    const int u = *a.pos + 1;
+    const int u = a.pos[n / a.cpr] + 1;
     if (wave < 4) {
         // keys past the position re-read the last key (a cache hit, not HBM traffic)
 #pragma unroll
@@ -900,7 +914,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_attn_pv(AttnArgs a) {
 // Chunk results added in order; the head's 64 outputs go to the out-projection activation.
 __global__ __launch_bounds__(64) void k_attn_reduce(AttnArgs a) {
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
-    const int u = *a.pos + 1, nch = (u + ATT_CHUNK - 1) / ATT_CHUNK;
+    const int u = a.pos[n / a.cpr] + 1, nch = (u + ATT_CHUNK - 1) / ATT_CHUNK;
     const size_t head = (size_t)n * a.heads + h;
     float part[ATT_MAX_CHUNKS];
 #pragma unroll
@@ -1007,18 +1021,18 @@ __device__ __forceinline__ void xattn_head(const float* qh, const float* K, cons
 // cross-attention of each request's conditional stream: one block per (head, request)
 __global__ __launch_bounds__(256) void k_xattn(XAttnArgs a) {
     const int h = blockIdx.x, r = blockIdx.y, H = gridDim.x;
-    const int nc = a.n_ctx;
-    xattn_head<16>(a.q + (size_t)r * a.dim + h * 64, a.k + ((size_t)r * H + h) * nc * 64,
-                   a.v + ((size_t)r * H + h) * nc * 64, nc, a.scale, a.out, a.out_f, a.dim, h, r);
+    const int nc = a.nc ? a.nc[r] : a.n_ctx;
+    xattn_head<16>(a.q + (size_t)r * a.dim + h * 64, a.k + ((size_t)r * H + h) * a.n_ctx * 64,
+                   a.v + ((size_t)r * H + h) * a.n_ctx * 64, nc, a.scale, a.out, a.out_f, a.dim, h, r);
 }
 
-// The hoisted cross K/V: projected [n_ctx][2*dim] -> K [H][n_ctx][64], V [H][n_ctx][64].
-__global__ __launch_bounds__(256) void k_xkv_split(const float* kv, int n_ctx, int dim, float* k, float* v) {
+// The hoisted cross K/V: projected [n_ctx][2*dim] -> K [H][rows][64], V [H][rows][64] (first n_ctx rows).
+__global__ __launch_bounds__(256) void k_xkv_split(const float* kv, int n_ctx, int rows, int dim, float* k, float* v) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n_ctx * 2 * dim) return;
     const int t = i / (2 * dim), r = i - t * 2 * dim;
     const int sec = r / dim, w = r - sec * dim, head = w >> 6, d = w & 63;
-    (sec == 0 ? k : v)[((size_t)head * n_ctx + t) * 64 + d] = kv[i];
+    (sec == 0 ? k : v)[((size_t)head * rows + t) * 64 + d] = kv[i];
 }
 
 // ------------------------------------------------------------------------------------
@@ -1088,27 +1102,31 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
     __shared__ uint32_t prefix_sh;
     __shared__ int k_sh;
     const int r = blockIdx.y;
-    const float cfg_coef = a.cfg_coef[r], temperature = a.temperature[r];
-    const int use_sampling = a.use_sampling[r], top_k = a.top_k[r];
-    const float* lr = a.logits + (size_t)r * (a.guided ? 2 : 1) * a.n_q * C;
+    const ReqParams par = a.par[r];
+    const int offset = a.pos[r] + 1;
+    // the whole block leaves together: a request that is idle or between its loop bounds
+    if ((a.live && !a.live[r]) || offset < par.start || offset >= par.steps) return;
+    const float cfg_coef = par.cfg_coef, temperature = par.temperature;
+    const int use_sampling = par.use_sampling, top_k = par.top_k, guided = par.guided;
+    const float* lr = a.logits + (size_t)r * a.cpr * a.n_q * C;
     const float* cond = lr + (size_t)q * C;
     const float* null_l = lr + (size_t)(a.n_q + q) * C;
-    const int offset = *a.pos + 1;
-    float* first = offset == a.start ? a.first_logits + (size_t)r * a.n_q * C : nullptr;
-    float* stepl = a.step_logits ? a.step_logits + (((size_t)r * (a.steps - a.start) + (offset - a.start)) * a.n_q + q) * C : nullptr;
-    const float* uniforms = a.uniforms + (size_t)r * a.steps * a.n_q;
-    int32_t* seq = a.seq + (size_t)r * a.n_q * a.steps;
+    float* first = offset == par.start ? a.first_logits + (size_t)r * a.n_q * C : nullptr;
+    float* stepl = a.step_logits ? a.step_logits + (((size_t)r * a.step_rows + (offset - par.start)) * a.n_q + q) * C : nullptr;
+    const float* uniforms = a.uniforms + (size_t)r * a.seq_len * a.n_q;
+    int32_t* seq = a.seq + (size_t)r * a.n_q * a.seq_len;
+    const uint8_t* mask = a.mask + (size_t)r * a.mask_stride;
     for (int i = tid; i < C; i += 256) {
         float v = cond[i];
-        if (a.guided) v = null_l[i] + (cond[i] - null_l[i]) * cfg_coef;
+        if (guided) v = null_l[i] + (cond[i] - null_l[i]) * cfg_coef;
         lg[i] = v;
         if (first) first[(size_t)q * C + i] = v;
         if (stepl) stepl[i] = v;
     }
     __syncthreads();
-    const bool live = a.mask[(size_t)q * a.steps + offset] != 0;
+    const bool timed = mask[(size_t)q * a.seq_len + offset] != 0;
     int token;
-    if (!live) token = a.special;
+    if (!timed) token = a.special;
     else if (!use_sampling || !(temperature > 0.0f)) {
         // argmax, lowest index on ties
         float best = -__builtin_inff();
@@ -1267,7 +1285,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
         token = pick_sh;
     }
     if (tid == 0) {
-        int32_t* slot = seq + (size_t)q * a.steps + offset;
+        int32_t* slot = seq + (size_t)q * a.seq_len + offset;
         if (*slot == -1) *slot = token;
     }
 }
@@ -1297,7 +1315,13 @@ void launch_embed(const EmbedArgs& a, hipStream_t s) {
     const int nreq = (a.ncol + a.cols_per_req - 1) / a.cols_per_req;
     hipLaunchKernelGGL(k_embed, dim3((a.dim + 255) / 256, nreq), dim3(256), 0, s, a);
 }
-void launch_advance(int* pos, hipStream_t s) { hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, s, pos); }
+void launch_advance(int* pos, int* live, const ReqParams* par, int n_req, hipStream_t s) {
+    hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, pos, live, par, n_req);
+}
+void launch_slot_open(int* pos, int* live, ReqParams* par, int* nc, int r, const ReqParams& p, int n_ctx,
+                      hipStream_t s) {
+    hipLaunchKernelGGL(k_slot_open, dim3(1), dim3(64), 0, s, pos, live, par, nc, r, p, n_ctx);
+}
 void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s) {
     hipLaunchKernelGGL(k_add_bias, dim3((n * ncol + 255) / 256), dim3(256), 0, s, y, b, n, ncol);
 }
@@ -1480,13 +1504,13 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
                 else d.f[(size_t)n * d.stride + row] = ge;
             }
             if (live && a.dst_f) a.dst_f[(size_t)n * d.stride + row] = ge;
-        } else if (live) {
+        } else if (live && (EPI == EPI_QKV || !a.gate || a.gate[a.col0 + n])) {
             if (EPI == EPI_STORE) a.y[(size_t)n * a.y_stride + row] = y;
             else if (EPI == EPI_RESID) a.y[(size_t)n * a.y_stride + row] = a.y[(size_t)n * a.y_stride + row] + y;
             else {
                 const int sec = row / a.dim, wi = row - sec * a.dim, head = wi >> 6, dm = wi & 63;
                 if (sec == 0) a.y[(size_t)n * a.dim + wi] = y;
-                else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + *a.pos) * 64 + dm] = y;
+                else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + a.pos[(a.col0 + n) / a.cpr]) * 64 + dm] = y;
             }
         }
     }
@@ -1617,6 +1641,7 @@ void launch_gemv(const GemvArgs& a0, hipStream_t s) {
             adv(a.dst);
             if (a0.dst_f) a.dst_f = a0.dst_f + (size_t)c0 * a0.dst.stride;
             if (a0.ad_ax) a.ad_ax = a0.ad_ax + (size_t)c0 * a0.ad_rank;
+            a.col0 = a0.col0 + c0;
             if (a0.epi == EPI_QKV) {
                 a.y = a0.y + (size_t)c0 * a0.dim;
                 a.k = a0.k + (size_t)c0 * a0.heads * a0.cap * 64;
@@ -1666,9 +1691,15 @@ void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
 // partials (key mod 16, fmaf in key order) and folds them by the butterfly in registers.
 __global__ __launch_bounds__(64) void k_xattn_w(XAttnArgs a) {
     const int h = blockIdx.x, r = blockIdx.y, H = gridDim.x, lane = threadIdx.x, g = lane >> 4, t = lane & 15;
-    const int nc = a.n_ctx;
-    const float* K = a.k + ((size_t)r * H + h) * nc * 64;
-    const float* V = a.v + ((size_t)r * H + h) * nc * 64;
+    const int nc = a.nc ? a.nc[r] : a.n_ctx;
+    if (nc <= 0) {
+        // no conditioning: zeros (the gated cross.out leaves the residual unchanged)
+        put_act(a.out, r, h * 64 + lane, 0.0f, lane);
+        if (a.out_f) a.out_f[(size_t)r * a.dim + h * 64 + lane] = 0.0f;
+        return;
+    }
+    const float* K = a.k + ((size_t)r * H + h) * a.n_ctx * 64;
+    const float* V = a.v + ((size_t)r * H + h) * a.n_ctx * 64;
     __shared__ float pj[64];
     // every load first: q, the keys' float4s (key 4*it + g), then V column `lane` of each key
     const float4 q = ((const float4*)(a.q + (size_t)r * a.dim + h * 64))[t];
@@ -1724,8 +1755,8 @@ void launch_xattn(const XAttnArgs& a, int heads, int n_req, hipStream_t s) {
     if (a.n_ctx <= 64) hipLaunchKernelGGL(k_xattn_w, dim3(heads, n_req), dim3(64), 0, s, a);
     else hipLaunchKernelGGL(k_xattn, dim3(heads, n_req), dim3(256), 0, s, a);
 }
-void launch_xkv_split(const float* kv, int n_ctx, int dim, float* k, float* v, hipStream_t s) {
-    hipLaunchKernelGGL(k_xkv_split, dim3((n_ctx * 2 * dim + 255) / 256), dim3(256), 0, s, kv, n_ctx, dim, k, v);
+void launch_xkv_split(const float* kv, int n_ctx, int rows, int dim, float* k, float* v, hipStream_t s) {
+    hipLaunchKernelGGL(k_xkv_split, dim3((n_ctx * 2 * dim + 255) / 256), dim3(256), 0, s, kv, n_ctx, rows, dim, k, v);
 }
 void launch_sample(const SampleArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(k_sample, dim3(a.n_q, a.n_req), dim3(256), 0, s, a);

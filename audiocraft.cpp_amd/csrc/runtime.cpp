@@ -145,7 +145,14 @@ struct mgx_stream {
     float *xk = nullptr, *xv = nullptr;      // per layer [n_req][H][n_ctx][64], each request's stream 0
     float* ax = nullptr;                     // adapter A x of the running projection [n_seq][rank]
     float* table = nullptr;                  // sinusoid [cap][dim]
-    int* dpos = nullptr;                     // the position the next step processes
+    int* dpos = nullptr;                     // [n_req] the position the next step processes
+    // Slotted batches: requests join and leave independently. dlive [n_req] (a step advances
+    // and samples only live requests), dpar [n_req] their parameters and loop bounds, dnc [n_req]
+    // their conditioning lengths (0: no cross-attention). All null for lockstep streams.
+    int* dlive = nullptr;
+    mgx::ReqParams* dpar = nullptr;
+    int* dnc = nullptr;
+    float *t5d = nullptr, *ctx = nullptr, *kvp = nullptr;   // memory projection scratch (n_ctx rows)
     float* cmax = nullptr;                   // [n_seq][H][max_chunks * ATT_SUBS] attention score-block maxima
     float *x = nullptr, *qb = nullptr, *scores = nullptr, *opart = nullptr, *logits = nullptr;
     float* qc = nullptr;                     // cross q [n_req][dim]
@@ -300,6 +307,8 @@ enum { PROF_GEMV = 0, PROF_ATTN = 1 };
 void gemv(mgx_stream* s, mgx::GemvArgs a) {
     if (a.pro == mgx::PRO_ACT && a.src.bm && !mgx::gemv_mf_ok(a))
         throw Error(MGX_ERR_INVALID, "internal: a block-major source for a projection the matrix cores cannot run");
+    if (a.epi == mgx::EPI_QKV && (a.cpr < 1 || !a.pos))
+        throw Error(MGX_ERR_INVALID, "internal: a K/V append without its positions");
     a.stamp = s->stamp_slot(PROF_GEMV, (double)a.w.in * a.w.out * bytes_per_weight(a.w.type));
     mgx::launch_gemv(a, s->hs);
 }
@@ -376,11 +385,11 @@ bool mf_src(const mgx::DevMat& w, int ncol, int epi) {
     return mgx::gemv_mf_ok(a);
 }
 
-// One sequence step at the device position *s->dpos for every stream: column n belongs to
-// request n / cpr, whose codebook q id sits at ids[r * ids_req_stride + q * ids_stride + pos -
-// ids_base]. With `heads`, the step's logits land in s->logits. `position` is the host's view
-// of *s->dpos: it sizes the attention grids (the kernels read the exact key count on the
-// device). Ends by advancing the device position.
+// One sequence step: column n belongs to request r = n / cpr, which runs at the device
+// position dpos[r] and whose codebook q id sits at ids[r * ids_req_stride + q * ids_stride + pos
+// - ids_base]. With `heads`, the step's logits land in s->logits. `position` is the host's view
+// of the largest position: it sizes the attention grids (the kernels read each column's exact
+// key count on the device). Ends by advancing the device positions.
 int att_chunks(int position) { return position / mgx::ATT_CHUNK + 1; }
 
 void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int ids_req_stride, bool heads,
@@ -406,14 +415,14 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
             mgx::GemvArgs a = ga(L.w[P_QKV], N);
             pro_ln(a, s->x, D, L.n1w, L.n1b, c.norm_eps);
             a.epi = mgx::EPI_QKV; a.y = s->qb; a.k = Kl; a.v = Vl; a.dim = D; a.heads = c.heads; a.cap = s->kv_rows;
-            a.pos = s->dpos;
+            a.pos = s->dpos; a.cpr = s->cpr;
             gemv_ad(s, a, L.ad[P_QKV]);
         }
         {
             mgx::AttnArgs at{};
             at.q = s->qb; at.k = Kl; at.v = Vl; at.scores = s->scores; at.opart = s->opart; at.cmax = s->cmax;
             at.dim = D; at.heads = c.heads; at.cap = s->kv_rows; at.max_chunks = s->max_chunks; at.ncol = N;
-            at.scale = scale; at.pos = s->dpos; at.out = s->act_o.view(L.w[P_OUT].type, bo);
+            at.scale = scale; at.pos = s->dpos; at.cpr = s->cpr; at.out = s->act_o.view(L.w[P_OUT].type, bo);
             at.out_f = L.ad[P_OUT] ? s->act_o.f : nullptr;
             // f32 K and V of every key attended, every stream
             at.stamp = s->stamp_slot(PROF_ATTN, 2.0 * N * c.heads * (position + 1) * 64 * 4);
@@ -435,12 +444,14 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
             gemv_ad(s, a, L.ad[P_CQ]);
             mgx::XAttnArgs xa{};
             xa.q = s->qc; xa.k = s->xk + xl; xa.v = s->xv + xl; xa.n_ctx = s->n_ctx; xa.dim = D; xa.scale = scale;
+            xa.nc = s->dnc;
             xa.out = s->act_c.view(L.w[P_COUT].type, bc);
             xa.out_f = L.ad[P_COUT] ? s->act_c.f : nullptr;
             mgx::launch_xattn(xa, c.heads, R, s->hs);
             mgx::GemvArgs b = ga(L.w[P_COUT], R);
             pro_act(b, s->act_c.view(L.w[P_COUT].type, bc));
             epi_store(b, s->x, s->cpr * D, true);
+            b.gate = s->dnc;   // a slotted request without conditioning keeps its residual as is
             gemv_ad(s, b, L.ad[P_COUT], s->act_c.f, D);
         }
         // feed-forward: LN2 + ff.0 + GELU (quantized in the epilogue), ff.2 + residual
@@ -463,7 +474,7 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
         gemv_ad(s, a, nullptr);
     }
     if (sample) mgx::launch_sample(*sample, s->hs);
-    mgx::launch_advance(s->dpos, s->hs);
+    mgx::launch_advance(s->dpos, s->dlive, s->dpar, R, s->hs);
 }
 
 void check_config(const mgx_lm_config& c) {
@@ -511,6 +522,33 @@ void validate_tensors(const mgx_lm_config& c, const mgx_tensor* t, int n) {
 // A stream of n_seq columns for n_req requests (n_seq / n_req columns each; column r * cpr is
 // request r's conditional stream). With `cross`, t5[r] [n_ctx][cond_dim] is request r's
 // conditioning: projected through lm.cond_proj once and through every layer's cross.kv once.
+// lm.cond_proj . t5 + bias, stream 0 only (pipeline.cpp:144-180), then every layer's cross.kv
+// of it, for request r: its n_ctx rows of the cross K / V (n_ctx <= the stream's rows per head).
+void project_memory(mgx_stream* s, int r, const float* t5, int nc) {
+    const mgx_model* m = s->m;
+    const mgx_lm_config& c = m->c;
+    const int R = s->n_req, rows = s->n_ctx;
+    HIP_OK(hipMemcpyAsync(s->t5d, t5, sizeof(float) * (size_t)nc * c.cond_dim, hipMemcpyHostToDevice, s->hs));
+    for (int col = 0; col < nc; ++col) {
+        mgx::GemvArgs a = ga(m->cond_proj, 1);
+        pro_f32(a, s->t5d + (size_t)col * c.cond_dim, c.cond_dim);
+        epi_store(a, s->ctx + (size_t)col * c.dim, c.dim);
+        gemv(s, a);
+    }
+    mgx::launch_add_bias(s->ctx, m->cond_proj_b, c.dim, nc, s->hs);
+    for (int l = 0; l < c.layers; ++l) {
+        for (int col = 0; col < nc; ++col) {
+            mgx::GemvArgs a = ga(m->L[(size_t)l].w[P_CKV], 1);
+            pro_f32(a, s->ctx + (size_t)col * c.dim, c.dim);
+            epi_store(a, s->kvp + (size_t)col * 2 * c.dim, 2 * c.dim);
+            gemv_ad(s, a, m->L[(size_t)l].ad[P_CKV]);
+        }
+        const size_t off = ((size_t)l * R + r) * c.heads * rows * 64;
+        mgx::launch_xkv_split(s->kvp, nc, rows, c.dim, s->xk + off, s->xv + off, s->hs);
+    }
+}
+
+// t5: one conditioning per request, or null to project them later (project_memory).
 void make_stream(mgx_model* m, int capacity, int n_seq, int n_req, const float* const* t5, int n_ctx, int cross,
                  mgx_stream** out) {
     const mgx_lm_config& c = m->c;
@@ -518,9 +556,9 @@ void make_stream(mgx_model* m, int capacity, int n_seq, int n_req, const float* 
     if (n_seq > 16) throw Error(MGX_ERR_INVALID, "at most 16 streams per forward");
     if (n_req <= 0 || n_req > mgx::MAX_REQ || n_seq % n_req) throw Error(MGX_ERR_INVALID, "bad request count");
     if (cross && n_ctx <= 0) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
-    if (cross)
+    if (cross && t5)
         for (int r = 0; r < n_req; ++r)
-            if (!t5 || !t5[r]) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
+            if (!t5[r]) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
     if (cross && n_ctx > 256) throw Error(MGX_ERR_INVALID, "at most 256 conditioning tokens");
     HIP_OK(hipSetDevice(m->device));
     auto s = std::make_unique<mgx_stream>();
@@ -540,8 +578,8 @@ void make_stream(mgx_model* m, int capacity, int n_seq, int n_req, const float* 
     s->table = s->mem.alloc<float>((size_t)capacity * c.dim);
     const std::vector<float> tab = sin_table(capacity, c);
     HIP_OK(hipMemcpyAsync(s->table, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice, s->hs));
-    s->dpos = s->mem.alloc<int>(1);
-    HIP_OK(hipMemsetAsync(s->dpos, 0, sizeof(int), s->hs));
+    s->dpos = s->mem.alloc<int>((size_t)n_req);
+    HIP_OK(hipMemsetAsync(s->dpos, 0, sizeof(int) * (size_t)n_req, s->hs));
     s->cmax = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * mgx::ATT_SUBS);
     s->x = s->mem.alloc<float>((size_t)n_seq * c.dim);
     s->qb = s->mem.alloc<float>((size_t)n_seq * c.dim);
@@ -556,34 +594,14 @@ void make_stream(mgx_model* m, int capacity, int n_seq, int n_req, const float* 
     s->ids = s->mem.alloc<int32_t>((size_t)c.n_q * capacity);
     if (m->ad_rank_max > 0) s->ax = s->mem.alloc<float>((size_t)std::max(n_seq, 2) * m->ad_rank_max);
     if (s->cross) {
-        // lm.cond_proj . t5 + bias, stream 0 only (pipeline.cpp:144-180), then every layer's
-        // cross.kv of it, once per request.
         const int nc = s->n_ctx;
-        float* t5d = s->mem.alloc<float>((size_t)nc * c.cond_dim);
-        float* ctx = s->mem.alloc<float>((size_t)nc * c.dim);
-        float* kvp = s->mem.alloc<float>((size_t)nc * 2 * c.dim);
+        s->t5d = s->mem.alloc<float>((size_t)nc * c.cond_dim);
+        s->ctx = s->mem.alloc<float>((size_t)nc * c.dim);
+        s->kvp = s->mem.alloc<float>((size_t)nc * 2 * c.dim);
         s->xk = s->mem.alloc<float>((size_t)c.layers * n_req * c.heads * nc * 64);
         s->xv = s->mem.alloc<float>((size_t)c.layers * n_req * c.heads * nc * 64);
-        for (int r = 0; r < n_req; ++r) {
-            HIP_OK(hipMemcpyAsync(t5d, t5[r], sizeof(float) * (size_t)nc * c.cond_dim, hipMemcpyHostToDevice, s->hs));
-            for (int col = 0; col < nc; ++col) {
-                mgx::GemvArgs a = ga(m->cond_proj, 1);
-                pro_f32(a, t5d + (size_t)col * c.cond_dim, c.cond_dim);
-                epi_store(a, ctx + (size_t)col * c.dim, c.dim);
-                gemv(s.get(), a);
-            }
-            mgx::launch_add_bias(ctx, m->cond_proj_b, c.dim, nc, s->hs);
-            for (int l = 0; l < c.layers; ++l) {
-                for (int col = 0; col < nc; ++col) {
-                    mgx::GemvArgs a = ga(m->L[(size_t)l].w[P_CKV], 1);
-                    pro_f32(a, ctx + (size_t)col * c.dim, c.dim);
-                    epi_store(a, kvp + (size_t)col * 2 * c.dim, 2 * c.dim);
-                    gemv_ad(s.get(), a, m->L[(size_t)l].ad[P_CKV]);
-                }
-                const size_t off = ((size_t)l * n_req + r) * c.heads * nc * 64;
-                mgx::launch_xkv_split(kvp, nc, c.dim, s->xk + off, s->xv + off, s->hs);
-            }
-        }
+        if (t5)
+            for (int r = 0; r < n_req; ++r) project_memory(s.get(), r, t5[r], nc);
     }
     HIP_OK(hipGetLastError());
     HIP_OK(hipStreamSynchronize(s->hs));
@@ -856,6 +874,24 @@ struct mgx_session {
 
 namespace {
 
+mgx::ReqParams req_params(const mgx_generate_params& p, bool guided, int start, int steps) {
+    mgx::ReqParams r{};
+    r.cfg_coef = p.cfg_coef; r.temperature = p.temperature; r.use_sampling = p.use_sampling; r.top_k = p.top_k;
+    r.guided = guided ? 1 : 0; r.start = start; r.steps = steps;
+    return r;
+}
+
+// mg_generate's argument checks (pipeline.cpp:204-212) for one request
+void check_request(const mgx_lm_config& c, const mgx_batch_request& q, int n_ctx, int prompt_len) {
+    const int T = q.params.max_gen_len;
+    if (T <= 0) throw Error(MGX_ERR_INVALID, "max_gen_len must be positive");
+    if (prompt_len < 0 || prompt_len >= T) throw Error(MGX_ERR_INVALID, "the prompt must be shorter than the generation");
+    if (prompt_len > 0 && !q.prompt_codes) throw Error(MGX_ERR_INVALID, "prompt codes do not hold n_q * prompt_len values");
+    if (n_ctx <= 0) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
+    for (int64_t i = 0; i < (int64_t)c.n_q * prompt_len; ++i)
+        if (q.prompt_codes[i] < 0 || q.prompt_codes[i] >= c.card) throw Error(MGX_ERR_INVALID, "prompt code out of range");
+}
+
 void session_create(mgx_model* m, const mgx_batch_request* reqs, int R, int32_t n_ctx, int32_t prompt_len,
                     int keep_steps, mgx_session** out) {
     if (!m || !reqs || !out) throw Error(MGX_ERR_INVALID, "null argument");
@@ -863,16 +899,10 @@ void session_create(mgx_model* m, const mgx_batch_request* reqs, int R, int32_t 
     const mgx_lm_config& c = m->c;
     if (R <= 0 || R > mgx::MAX_REQ) throw Error(MGX_ERR_INVALID, "a batch holds 1 to 16 requests");
     const int K = c.n_q, T = reqs[0].params.max_gen_len;
-    // mg_generate's argument checks (pipeline.cpp:204-212), per request
     for (int r = 0; r < R; ++r) {
         const mgx_batch_request& q = reqs[r];
-        if (q.params.max_gen_len <= 0) throw Error(MGX_ERR_INVALID, "max_gen_len must be positive");
+        check_request(c, q, n_ctx, prompt_len);
         if (q.params.max_gen_len != T) throw Error(MGX_ERR_INVALID, "the requests of a batch share max_gen_len");
-        if (prompt_len < 0 || prompt_len >= T) throw Error(MGX_ERR_INVALID, "the prompt must be shorter than the generation");
-        if (prompt_len > 0 && !q.prompt_codes) throw Error(MGX_ERR_INVALID, "prompt codes do not hold n_q * prompt_len values");
-        if (n_ctx <= 0) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
-        for (int64_t i = 0; i < (int64_t)K * prompt_len; ++i)
-            if (q.prompt_codes[i] < 0 || q.prompt_codes[i] >= c.card) throw Error(MGX_ERR_INVALID, "prompt code out of range");
         if ((mgx_use_guidance(q.params.cfg_coef, q.description_empty) != 0) !=
             (mgx_use_guidance(reqs[0].params.cfg_coef, reqs[0].description_empty) != 0))
             throw Error(MGX_ERR_INVALID, "the requests of a batch are all guided or all unguided");
@@ -895,6 +925,7 @@ void session_create(mgx_model* m, const mgx_batch_request* reqs, int R, int32_t 
     // codebook (pipeline.cpp:278-288, rng.h:20-22); which slots draw depends only on the
     // mask, so each request's whole stream is drawn here.
     std::vector<float> uni((size_t)R * S * K, 0.0f);
+    std::vector<mgx::ReqParams> par((size_t)R);
     mgx::SampleArgs& sa = ss->sa;
     for (int r = 0; r < R; ++r) {
         const mgx_batch_request& rq = reqs[r];
@@ -912,8 +943,7 @@ void session_create(mgx_model* m, const mgx_batch_request* reqs, int R, int32_t 
                 for (int q = 0; q < K; ++q)
                     if (mask[(size_t)q * S + st]) u[(size_t)st * K + q] = ((g() >> 8) + 0.5f) * (1.0f / 16777216.0f);
         }
-        sa.cfg_coef[r] = p.cfg_coef; sa.temperature[r] = p.temperature;
-        sa.use_sampling[r] = p.use_sampling; sa.top_k[r] = p.top_k;
+        par[(size_t)r] = req_params(p, ss->guided, start, S);
     }
     std::vector<const float*> t5s((size_t)R);
     for (int r = 0; r < R; ++r) t5s[(size_t)r] = reqs[r].t5_hidden;
@@ -923,6 +953,8 @@ void session_create(mgx_model* m, const mgx_batch_request* reqs, int R, int32_t 
     mgx_stream* st = ss->s.get();
     ss->dseq = ss->mem.alloc<int32_t>(ss->seq.size());
     uint8_t* dmask = ss->mem.alloc<uint8_t>(mask.size());
+    mgx::ReqParams* dpar = ss->mem.alloc<mgx::ReqParams>(par.size());
+    HIP_OK(hipMemcpyAsync(dpar, par.data(), par.size() * sizeof(mgx::ReqParams), hipMemcpyHostToDevice, st->hs));
     float* duni = ss->mem.alloc<float>(uni.size());
     ss->dfirst = ss->mem.alloc<float>((size_t)R * K * c.card);
     if (keep_steps) ss->dsteps = ss->mem.alloc<float>((size_t)R * (S - start) * K * c.card);
@@ -930,9 +962,10 @@ void session_create(mgx_model* m, const mgx_batch_request* reqs, int R, int32_t 
     HIP_OK(hipMemcpyAsync(dmask, mask.data(), mask.size(), hipMemcpyHostToDevice, st->hs));
     HIP_OK(hipMemcpyAsync(duni, uni.data(), uni.size() * 4, hipMemcpyHostToDevice, st->hs));
     HIP_OK(hipStreamSynchronize(st->hs));
-    sa.logits = st->logits; sa.n_q = K; sa.card = c.card; sa.guided = ss->guided; sa.n_req = R;
-    sa.mask = dmask; sa.steps = S; sa.uniforms = duni; sa.special = c.special_token_id; sa.seq = ss->dseq;
-    sa.start = start; sa.pos = st->dpos; sa.first_logits = ss->dfirst; sa.step_logits = ss->dsteps;
+    sa.logits = st->logits; sa.n_q = K; sa.card = c.card; sa.n_req = R; sa.cpr = st->cpr; sa.par = dpar;
+    sa.pos = st->dpos; sa.live = nullptr; sa.seq_len = S; sa.mask = dmask; sa.mask_stride = 0;
+    sa.special = c.special_token_id; sa.uniforms = duni; sa.seq = ss->dseq;
+    sa.first_logits = ss->dfirst; sa.step_logits = ss->dsteps; sa.step_rows = S - start;
     *out = ss.release();
 }
 
@@ -1157,3 +1190,263 @@ int mgx_generate(mgx_model* m, const float* t5_hidden, int32_t n_ctx, int32_t de
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------------------------------
+// slotted batches: the server's device side (library-internal, declared in slots.h)
+// ------------------------------------------------------------------------------------
+// `n` slots of `cpr` streams (2: guided or not, 1: unguided only) share one stream of n * cpr
+// columns. A request is opened into a free slot between steps: its delay-pattern sequence,
+// mask and uniforms go to the slot's rows, its conditioning to the slot's cross K / V, and its
+// position to 0. Every step then processes each live slot's next position -- its prompt
+// positions first (no sampling), then its loop offsets start..S-1 (sampling) -- and the device
+// retires a slot after its last offset (k_advance). Each request computes exactly what it
+// computes alone: every column's arithmetic depends only on that column's inputs.
+struct mgx_slots {
+    mgx_model* m = nullptr;
+    std::unique_ptr<mgx_stream> s;
+    DevArena mem;
+    int n = 0, cpr = 1, K = 0, seq_len = 0, max_gen = 0, max_ctx = 0, step_rows = 0;
+    int32_t* dseq = nullptr;       // [n][K][seq_len]
+    uint8_t* dmask = nullptr;      // [n][K][seq_len]
+    float* duni = nullptr;         // [n][seq_len][K]
+    float *dfirst = nullptr, *dsteps = nullptr;
+    // pinned staging, one region per slot: a slot's region is reused only after its previous
+    // request's results were read, which waits for the stream
+    int32_t* hseq = nullptr;
+    uint8_t* hmask = nullptr;
+    float *huni = nullptr, *ht5 = nullptr;
+    mgx::SampleArgs sa{};
+    hipGraphExec_t g[mgx::ATT_MAX_CHUNKS] = {};
+    bool use_graphs = true;
+    struct Slot { bool live = false, unread = false; int pos = 0, start = 0, S = 0, T = 0; };
+    std::vector<Slot> slot;
+    ~mgx_slots() {
+        if (s && s->hs) (void)hipStreamSynchronize(s->hs);
+        for (auto& e : g)
+            if (e) (void)hipGraphExecDestroy(e);
+        for (void* p : {(void*)hseq, (void*)hmask, (void*)huni, (void*)ht5})
+            if (p) (void)hipHostFree(p);
+        mem.release();
+    }
+};
+
+namespace {
+
+template <typename T> T* host_alloc(size_t count) {
+    void* p = nullptr;
+    HIP_OK(hipHostMalloc(&p, std::max<size_t>(count, 1) * sizeof(T), hipHostMallocDefault));
+    return (T*)p;
+}
+
+void slots_create(mgx_model* m, int n, int cpr, int max_gen, int max_ctx, int keep_steps, mgx_slots** out) {
+    if (!m || !out) throw Error(MGX_ERR_INVALID, "null argument");
+    *out = nullptr;
+    const mgx_lm_config& c = m->c;
+    if (cpr != 1 && cpr != 2) throw Error(MGX_ERR_INVALID, "streams per slot must be 1 or 2");
+    if (n <= 0 || n * cpr > 16) throw Error(MGX_ERR_INVALID, "at most 16 streams (8 slots of 2)");
+    if (max_gen <= 0) throw Error(MGX_ERR_INVALID, "max_gen_len must be positive");
+    if (max_ctx <= 0 || max_ctx > 256) throw Error(MGX_ERR_INVALID, "the conditioning limit must be 1 to 256 tokens");
+    auto sl = std::make_unique<mgx_slots>();
+    sl->m = m; sl->n = n; sl->cpr = cpr; sl->K = c.n_q; sl->max_gen = max_gen; sl->max_ctx = max_ctx;
+    sl->seq_len = 1 + max_gen + (c.n_q - 1);
+    if (const char* g = std::getenv("MGX_GRAPHS")) sl->use_graphs = std::strcmp(g, "0") != 0;
+    mgx_stream* raw = nullptr;
+    make_stream(m, sl->seq_len, n * cpr, n, nullptr, max_ctx, cpr == 2 ? 1 : 0, &raw);
+    sl->s.reset(raw);
+    mgx_stream* st = sl->s.get();
+    const size_t per = (size_t)sl->K * sl->seq_len;
+    st->dlive = st->mem.alloc<int>((size_t)n);
+    st->dpar = st->mem.alloc<mgx::ReqParams>((size_t)n);
+    st->dnc = st->mem.alloc<int>((size_t)n);
+    HIP_OK(hipMemsetAsync(st->dlive, 0, sizeof(int) * n, st->hs));
+    HIP_OK(hipMemsetAsync(st->dpar, 0, sizeof(mgx::ReqParams) * n, st->hs));
+    HIP_OK(hipMemsetAsync(st->dnc, 0, sizeof(int) * n, st->hs));
+    sl->dseq = sl->mem.alloc<int32_t>(per * n);
+    sl->dmask = sl->mem.alloc<uint8_t>(per * n);
+    sl->duni = sl->mem.alloc<float>(per * n);
+    sl->dfirst = sl->mem.alloc<float>((size_t)n * sl->K * c.card);
+    // an idle slot embeds its row 0: keep it a valid id
+    std::vector<int32_t> init(per * n, c.special_token_id);
+    HIP_OK(hipMemcpy(sl->dseq, init.data(), init.size() * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemsetAsync(sl->dmask, 0, per * n, st->hs));
+    HIP_OK(hipMemsetAsync(sl->duni, 0, per * n * sizeof(float), st->hs));
+    sl->step_rows = sl->seq_len - 1;
+    if (keep_steps) sl->dsteps = sl->mem.alloc<float>((size_t)n * sl->step_rows * sl->K * c.card);
+    sl->hseq = host_alloc<int32_t>(per * n);
+    sl->hmask = host_alloc<uint8_t>(per * n);
+    sl->huni = host_alloc<float>(per * n);
+    if (cpr == 2) sl->ht5 = host_alloc<float>((size_t)n * max_ctx * c.cond_dim);
+    mgx::SampleArgs& sa = sl->sa;
+    sa.logits = st->logits; sa.n_q = sl->K; sa.card = c.card; sa.n_req = n; sa.cpr = cpr; sa.par = st->dpar;
+    sa.pos = st->dpos; sa.live = st->dlive; sa.seq_len = sl->seq_len; sa.mask = sl->dmask; sa.mask_stride = (long long)per;
+    sa.special = c.special_token_id; sa.uniforms = sl->duni; sa.seq = sl->dseq;
+    sa.first_logits = sl->dfirst; sa.step_logits = sl->dsteps; sa.step_rows = sl->step_rows;
+    sl->slot.assign((size_t)n, mgx_slots::Slot{});
+    HIP_OK(hipStreamSynchronize(st->hs));
+    *out = sl.release();
+}
+
+// The checks a request passes before it may wait for a slot (no device work).
+void slot_check(const mgx_slots* sl, const mgx_batch_request& q, int n_ctx, int prompt_len) {
+    if (!sl) throw Error(MGX_ERR_INVALID, "null argument");
+    check_request(sl->m->c, q, n_ctx, prompt_len);
+    if (q.params.max_gen_len > sl->max_gen) throw Error(MGX_ERR_INVALID, "max_gen_len above the server's limit");
+    const bool guided = mgx_use_guidance(q.params.cfg_coef, q.description_empty) != 0;
+    if (guided && sl->cpr != 2) throw Error(MGX_ERR_INVALID, "a guided request needs slots of two streams");
+    if (guided && n_ctx > sl->max_ctx) throw Error(MGX_ERR_INVALID, "conditioning longer than the server's limit");
+    if (guided && !q.t5_hidden) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
+}
+
+void slot_open(mgx_slots* sl, int r, const mgx_batch_request& q, int n_ctx, int prompt_len) {
+    slot_check(sl, q, n_ctx, prompt_len);
+    if (r < 0 || r >= sl->n) throw Error(MGX_ERR_INVALID, "slot index out of range");
+    mgx_slots::Slot& h = sl->slot[(size_t)r];
+    if (h.live || h.unread) throw Error(MGX_ERR_STATE, "the slot is in use");
+    const mgx_lm_config& c = sl->m->c;
+    mgx_stream* st = sl->s.get();
+    HIP_OK(hipSetDevice(sl->m->device));
+    const int K = sl->K, L = sl->seq_len, T = q.params.max_gen_len, S = 1 + T + (K - 1), start = prompt_len + 1;
+    const bool guided = mgx_use_guidance(q.params.cfg_coef, q.description_empty) != 0;
+    const size_t per = (size_t)K * L;
+    int32_t* seq = sl->hseq + per * r;
+    uint8_t* mask = sl->hmask + per * r;
+    float* uni = sl->huni + per * r;
+    // the delay pattern of mg_generate (pattern.h:31-115): timestep t = st - 1 - q, S = T + n_q
+    const auto pat = [T](int qq, int stp) { const int t = stp - 1 - qq; return (stp > 0 && t >= 0 && t < T) ? t : -1; };
+    for (int qq = 0; qq < K; ++qq)
+        for (int stp = 0; stp < L; ++stp) {
+            const int t = stp < S ? pat(qq, stp) : -1;
+            mask[(size_t)qq * L + stp] = t >= 0;
+            seq[(size_t)qq * L + stp] =
+                t < 0 ? c.special_token_id : (t < prompt_len ? q.prompt_codes[(size_t)qq * prompt_len + t] : -1);
+        }
+    std::fill(uni, uni + per, 0.0f);
+    const mgx_generate_params& p = q.params;
+    if (p.use_sampling && p.temperature > 0.0f) {
+        std::mt19937 g((uint32_t)p.seed);
+        for (int stp = start; stp < S; ++stp)
+            for (int qq = 0; qq < K; ++qq)
+                if (mask[(size_t)qq * L + stp]) uni[(size_t)stp * K + qq] = ((g() >> 8) + 0.5f) * (1.0f / 16777216.0f);
+    }
+    HIP_OK(hipMemcpyAsync(sl->dseq + per * r, seq, per * 4, hipMemcpyHostToDevice, st->hs));
+    HIP_OK(hipMemcpyAsync(sl->dmask + per * r, mask, per, hipMemcpyHostToDevice, st->hs));
+    HIP_OK(hipMemcpyAsync(sl->duni + per * r, uni, per * 4, hipMemcpyHostToDevice, st->hs));
+    if (guided) {
+        float* t5 = sl->ht5 + (size_t)r * sl->max_ctx * c.cond_dim;
+        std::memcpy(t5, q.t5_hidden, sizeof(float) * (size_t)n_ctx * c.cond_dim);
+        project_memory(st, r, t5, n_ctx);
+    }
+    mgx::launch_slot_open(st->dpos, st->dlive, st->dpar, st->dnc, r, req_params(p, guided, start, S),
+                          guided ? n_ctx : 0, st->hs);
+    HIP_OK(hipGetLastError());
+    h.live = true; h.unread = true; h.pos = 0; h.start = start; h.S = S; h.T = T;
+}
+
+hipGraphExec_t slots_capture(mgx_slots* sl, int position) {
+    mgx_stream* s = sl->s.get();
+    hipGraph_t g = nullptr;
+    hipGraphExec_t e = nullptr;
+    HIP_OK(hipStreamBeginCapture(s->hs, hipStreamCaptureModeThreadLocal));
+    step(s, sl->dseq, sl->seq_len, 0, sl->K * sl->seq_len, true, &sl->sa, position);
+    HIP_OK(hipStreamEndCapture(s->hs, &g));
+    const hipError_t rc = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    HIP_OK(rc);
+    return e;
+}
+
+// Enqueues `steps` batch steps (no wait). The host mirrors every slot's position: the device
+// advances and retires live slots by the same rule (k_advance).
+void slots_run(mgx_slots* sl, int steps) {
+    mgx_stream* s = sl->s.get();
+    HIP_OK(hipSetDevice(sl->m->device));
+    for (int i = 0; i < steps; ++i) {
+        int top = 0;
+        for (const auto& h : sl->slot)
+            if (h.live) top = std::max(top, h.pos);
+        if (!sl->use_graphs) {
+            step(s, sl->dseq, sl->seq_len, 0, sl->K * sl->seq_len, true, &sl->sa, top);
+        } else {
+            hipGraphExec_t& g = sl->g[att_chunks(top) - 1];
+            if (!g) g = slots_capture(sl, top);
+            HIP_OK(hipGraphLaunch(g, s->hs));
+        }
+        for (auto& h : sl->slot)
+            if (h.live) {
+                if (h.pos + 2 >= h.S) { h.live = false; h.pos = 0; }
+                else ++h.pos;
+            }
+    }
+    HIP_OK(hipGetLastError());
+}
+
+// A retired slot's results (waits for the stream): codes reverted as mg_generate returns them.
+void slot_read(mgx_slots* sl, int r, int32_t* codes_out, float* first_out, float* steps_out) {
+    if (r < 0 || r >= sl->n) throw Error(MGX_ERR_INVALID, "slot index out of range");
+    mgx_slots::Slot& h = sl->slot[(size_t)r];
+    if (h.live || !h.unread) throw Error(MGX_ERR_STATE, "the slot holds no finished request");
+    const mgx_lm_config& c = sl->m->c;
+    mgx_stream* st = sl->s.get();
+    HIP_OK(hipSetDevice(sl->m->device));
+    HIP_OK(hipStreamSynchronize(st->hs));
+    const int K = sl->K, L = sl->seq_len, T = h.T, S = h.S;
+    const size_t per = (size_t)K * L;
+    int32_t* seq = sl->hseq + per * r;
+    HIP_OK(hipMemcpy(seq, sl->dseq + per * r, per * 4, hipMemcpyDeviceToHost));
+    if (first_out)
+        HIP_OK(hipMemcpy(first_out, sl->dfirst + (size_t)r * K * c.card, sizeof(float) * K * c.card,
+                         hipMemcpyDeviceToHost));
+    if (steps_out) {
+        if (!sl->dsteps) throw Error(MGX_ERR_STATE, "per-step logits were not kept");
+        HIP_OK(hipMemcpy(steps_out, sl->dsteps + (size_t)r * sl->step_rows * K * c.card,
+                         sizeof(float) * (size_t)(S - h.start) * K * c.card, hipMemcpyDeviceToHost));
+    }
+    h.unread = false;
+    if (!codes_out) return;
+    // revert_pattern_sequence + the final check (pipeline.cpp:307-313)
+    for (size_t i = 0; i < (size_t)K * T; ++i) codes_out[i] = c.special_token_id;
+    for (int q = 0; q < K; ++q)
+        for (int stp = 0; stp < S; ++stp) {
+            const int t = stp - 1 - q;
+            if (stp > 0 && t >= 0 && t < T) codes_out[(size_t)q * T + t] = seq[(size_t)q * L + stp];
+        }
+    for (size_t i = 0; i < (size_t)K * T; ++i)
+        if (codes_out[i] < 0 || codes_out[i] >= c.card)
+            throw Error(MGX_ERR_INVALID, "the generated sequence has a position the pattern never filled");
+}
+
+}  // namespace
+
+#include "slots.h"
+
+int mgx_internal_slots_create(mgx_model* m, int n, int cpr, int max_gen, int max_ctx, int keep_steps, mgx_slots** out) {
+    return guarded([&] { slots_create(m, n, cpr, max_gen, max_ctx, keep_steps, out); });
+}
+int mgx_internal_slot_check(const mgx_slots* sl, const mgx_batch_request* q, int n_ctx, int prompt_len) {
+    return guarded([&] {
+        if (!q) throw Error(MGX_ERR_INVALID, "null argument");
+        slot_check(sl, *q, n_ctx, prompt_len);
+    });
+}
+int mgx_internal_slot_open(mgx_slots* sl, int r, const mgx_batch_request* q, int n_ctx, int prompt_len) {
+    return guarded([&] {
+        if (!q) throw Error(MGX_ERR_INVALID, "null argument");
+        slot_open(sl, r, *q, n_ctx, prompt_len);
+    });
+}
+int mgx_internal_slots_run(mgx_slots* sl, int steps) { return guarded([&] { slots_run(sl, steps); }); }
+int mgx_internal_slots_sync(mgx_slots* sl) {
+    return guarded([&] {
+        HIP_OK(hipSetDevice(sl->m->device));
+        HIP_OK(hipStreamSynchronize(sl->s->hs));
+    });
+}
+int mgx_internal_slot_read(mgx_slots* sl, int r, int32_t* codes_out, float* first_out, float* steps_out) {
+    return guarded([&] { slot_read(sl, r, codes_out, first_out, steps_out); });
+}
+void mgx_internal_slot_state(const mgx_slots* sl, int r, int* live, int* pos, int* start, int* S) {
+    const mgx_slots::Slot& h = sl->slot[(size_t)r];
+    *live = h.live; *pos = h.pos; *start = h.start; *S = h.S;
+}
+uint64_t mgx_internal_slot_cache_bytes(const mgx_slots* sl) { return mgx_stream_cache_bytes(sl->s.get()) / sl->n; }
+void mgx_internal_slots_destroy(mgx_slots* sl) { delete sl; }

@@ -46,6 +46,20 @@ class BatchRequest(C.Structure):
                 ("params", GenerateParams)]
 
 
+class ServerConfig(C.Structure):
+    """mgx_server_config."""
+    _fields_ = [("slots", C.c_int32), ("guided", C.c_int32), ("max_gen_len", C.c_int32), ("max_ctx", C.c_int32),
+                ("keep_step_logits", C.c_int32), ("steps_per_round", C.c_int32)]
+
+
+class ServerCounters(C.Structure):
+    _fields_ = [("steps", C.c_int64), ("slot_steps", C.c_int64), ("served", C.c_int64), ("active", C.c_int32),
+                ("queued", C.c_int32)]
+
+
+PROGRESS_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int32, C.c_int32)
+
+
 class GenerateReport(C.Structure):
     _fields_ = [("cache_bytes", C.c_uint64), ("prefill_tokens", C.c_int32), ("decode_steps", C.c_int32),
                 ("forwards", C.c_int32), ("prefill_seconds", C.c_double), ("decode_seconds", C.c_double)]
@@ -58,7 +72,8 @@ EXPORTS = ["mgx_model_create", "mgx_model_set_adapters", "mgx_model_destroy", "m
            "mgx_session_profile_read", "mgx_session_hip_stream", "mgx_batch_create", "mgx_batch_finish",
            "mgx_session_requests", "mgx_gguf_open", "mgx_gguf_close", "mgx_gguf_tensor_count", "mgx_gguf_tensor",
            "mgx_gguf_find_tensor", "mgx_gguf_u32", "mgx_gguf_f32", "mgx_gguf_string", "mgx_gguf_lm_config",
-           "mgx_model_create_from_gguf", "mgx_model_set_adapters_from_gguf", "mgx_last_error"]
+           "mgx_model_create_from_gguf", "mgx_model_set_adapters_from_gguf", "mgx_server_create",
+           "mgx_server_generate", "mgx_server_stats", "mgx_server_destroy", "mgx_last_error"]
 
 _lib = None
 
@@ -118,6 +133,12 @@ def load(path=None):
     lib.mgx_gguf_lm_config.argtypes = [P, C.POINTER(LmConfig)]
     lib.mgx_model_create_from_gguf.argtypes = [P, C.POINTER(P)]
     lib.mgx_model_set_adapters_from_gguf.argtypes = [P, P, P, C.c_float]
+    lib.mgx_server_create.argtypes = [P, C.POINTER(ServerConfig), C.POINTER(P)]
+    lib.mgx_server_generate.argtypes = [P, P, C.c_int32, C.c_int32, P, C.c_int32, C.POINTER(GenerateParams),
+                                        PROGRESS_FN, P, P, P, P, C.POINTER(GenerateReport)]
+    lib.mgx_server_stats.argtypes = [P, C.POINTER(ServerCounters)]
+    lib.mgx_server_destroy.argtypes = [P]
+    lib.mgx_server_destroy.restype = None
     if path is None:
         _lib = lib
     return lib
@@ -427,3 +448,56 @@ class Batch(Session):
         _check(self.lib, self.lib.mgx_batch_finish(self.handle, request, _ptr(codes), _ptr(first), _ptr(steps),
                                                    C.byref(rep)))
         return codes, first, rep, steps
+
+
+class Server:
+    """mgx_server_*: concurrent requests sharing one batched decode. generate() blocks the calling
+    thread until its request is done (ctypes releases the GIL meanwhile, so Python threads run
+    requests concurrently)."""
+
+    def __init__(self, model, slots, max_gen_len, max_ctx=64, guided=True, keep_step_logits=False,
+                 steps_per_round=0):
+        self.lib = model.lib
+        self.model = model
+        self.keep = keep_step_logits
+        cfg = ServerConfig(slots, 1 if guided else 0, max_gen_len, max_ctx, 1 if keep_step_logits else 0,
+                           steps_per_round)
+        h = C.c_void_p()
+        _check(self.lib, self.lib.mgx_server_create(model.handle, C.byref(cfg), C.byref(h)))
+        self.handle = h
+
+    def generate(self, t5_hidden, prompt_codes, prompt_len, params, description_empty=False, step_logits=False,
+                 progress=None):
+        """As Model.generate; progress(done, total) is called from the server's worker thread."""
+        c = self.model.config
+        T = params.max_gen_len
+        S = T + c.n_q
+        start = prompt_len + 1
+        codes = np.zeros((c.n_q, T), np.int32)
+        first = np.zeros((c.n_q, c.card), np.float32)
+        steps = np.zeros((S - start, c.n_q, c.card), np.float32) if step_logits else None
+        rep = GenerateReport()
+        t5 = np.ascontiguousarray(t5_hidden, np.float32)
+        prompt = np.ascontiguousarray(prompt_codes, np.int32) if prompt_len else None
+        cb = PROGRESS_FN(lambda user, done, total: progress(done, total)) if progress else PROGRESS_FN()
+        _check(self.lib, self.lib.mgx_server_generate(self.handle, _ptr(t5), t5.shape[0],
+                                                      1 if description_empty else 0, _ptr(prompt), prompt_len,
+                                                      C.byref(params), cb, None, _ptr(codes), _ptr(first),
+                                                      _ptr(steps), C.byref(rep)))
+        return codes, first, rep, steps
+
+    def counters(self):
+        out = ServerCounters()
+        _check(self.lib, self.lib.mgx_server_stats(self.handle, C.byref(out)))
+        return {k: getattr(out, k) for k, _ in ServerCounters._fields_}
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.mgx_server_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

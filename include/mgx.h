@@ -14,7 +14,8 @@
  * 98-99, 204-212; gguf_model.h:425-436), and a C++ caller rethrows the message.
  *
  * Threading: one caller thread per stream; distinct streams may be driven from distinct
- * threads. The reference's server runs one job at a time (src/serve/http.h:201-205).
+ * threads. The reference's server runs one job at a time (src/serve/http.h:201-205); the
+ * request server below (mgx_server_*) takes concurrent callers into one batched decode.
  */
 #ifndef MGX_H
 #define MGX_H
@@ -177,6 +178,50 @@ int mgx_batch_create(mgx_model* model, const mgx_batch_request* requests, int32_
 int mgx_batch_finish(mgx_session* session, int32_t request, int32_t* codes_out, float* first_logits_out,
                      float* step_logits_out, mgx_generate_report* report);
 int32_t mgx_session_requests(const mgx_session* session);
+
+/* A request server: many concurrent callers, one batched decode on the GPU. It replaces the
+   reference services' one-job-at-a-time generation lock (Sessions::gpu() held for the whole
+   of mg_generate, src/serve/http.h:201-205, 254-255, 278-291; the job start of
+   tools/musicgen-server.cpp:321-390): each job thread calls mgx_server_generate where it
+   called mg_generate, and blocks until its result is ready. One worker thread owns `slots`
+   request slots; between rounds of at most steps_per_round batch steps it admits queued
+   requests into free slots (first come, first served). A request's prompt positions run as
+   ordinary batch steps, then its loop; its slot frees after its own last step. Requests in
+   one batch differ in anything: prompt and generation length (up to max_gen_len),
+   conditioning (up to max_ctx tokens), guidance, seed and sampling parameters; each one's
+   codes, first logits and per-step logits equal mgx_generate's for it alone.
+   guided = 1: slots of two streams (guided and unguided requests); 0: one stream per slot
+   (unguided requests only, up to 16 slots). keep_step_logits: mgx_server_generate may ask for
+   per-step logits. steps_per_round 0 means 16.
+   progress, if not NULL, gets (user, done, total) after every loop iteration as the
+   reference's ProgressFn (pipeline.cpp:301), called from the worker thread after the round
+   that ran it. Errors: argument checks fail at once with mg_generate's messages; a device
+   error fails every request in the server and every later call; mgx_server_destroy fails the
+   requests still waiting (MGX_ERR_STATE) and returns once their callers have returned. */
+typedef struct mgx_server mgx_server;
+typedef struct mgx_server_config {
+    int32_t slots;
+    int32_t guided;
+    int32_t max_gen_len;
+    int32_t max_ctx;
+    int32_t keep_step_logits;
+    int32_t steps_per_round;
+} mgx_server_config;
+typedef void (*mgx_progress_fn)(void* user, int32_t done, int32_t total);
+typedef struct mgx_server_counters {
+    int64_t steps;        /* batch steps run */
+    int64_t slot_steps;   /* sum over steps of the requests they advanced */
+    int64_t served;       /* requests completed */
+    int32_t active;       /* requests in slots */
+    int32_t queued;       /* requests waiting for a slot */
+} mgx_server_counters;
+int mgx_server_create(mgx_model* model, const mgx_server_config* config, mgx_server** out);
+int mgx_server_generate(mgx_server* server, const float* t5_hidden, int32_t n_ctx, int32_t description_empty,
+                        const int32_t* prompt_codes, int32_t prompt_len, const mgx_generate_params* params,
+                        mgx_progress_fn progress, void* user, int32_t* codes_out, float* first_logits_out,
+                        float* step_logits_out, mgx_generate_report* report);
+int mgx_server_stats(mgx_server* server, mgx_server_counters* out);
+void mgx_server_destroy(mgx_server* server);
 
 /* Launch timing (no reference counterpart; the reference has wall clocks only,
    pipeline.cpp:15-18): with every > 0, each GEMV (kind 0) and self-attention (kind 1) launch
