@@ -71,8 +71,8 @@ struct GemvArgs {
     int y_stride;
     float *k, *v;         // QKV: caches [col][heads][cap][64]
     int dim, heads, cap;
-    const int* pos;       // QKV: [request] device positions; column n belongs to request n / cpr
-    int cpr;
+    const int* pos;       // QKV: [request] device positions; column n belongs to request n >> cshift
+    int cshift;
     ActBuf dst;           // GELU_ACT destination
     float* dst_f;         // GELU_ACT: optional f32 copy [col][dst.stride] (an adapted consumer's A x reads it)
     // optional adapter on this projection (lora.h:50-83): y = Wx + s*B(Ax), DoRA rows scale
@@ -98,8 +98,8 @@ struct AttnArgs {
     float* cmax;          // [col][heads][max_chunks * ATT_SUBS] score-block maxima
     int dim, heads, cap, max_chunks, ncol;
     float scale;
-    const int* pos;       // [request] device positions: column n attends keys [0, pos[n / cpr]]
-    int cpr;
+    const int* pos;       // [request] device positions: column n attends keys [0, pos[n >> cshift]]
+    int cshift;
     ActBuf out;           // the out-projection's activation
     float* out_f;         // optional f32 copy [col][dim] (an adapted out-projection's A x reads it)
     unsigned long long* stamp;   // optional [64][2]: scores' earliest starts, reduce's latest ends

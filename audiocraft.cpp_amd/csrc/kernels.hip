@@ -725,7 +725,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
         else {
             const int sec = row / a.dim, wi = row - sec * a.dim, head = wi >> 6, dm = wi & 63;
             if (sec == 0) a.y[(size_t)n * a.dim + wi] = r;
-            else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + a.pos[(a.col0 + n) / a.cpr]) * 64 + dm] = r;
+            else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + a.pos[(a.col0 + n) >> a.cshift]) * 64 + dm] = r;
         }
     }
 }
@@ -781,7 +781,7 @@ __device__ __forceinline__ float halving4(const float (&p)[4], int t) {
 __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
     const unsigned long long t0 = stamp_begin(a.stamp);
     const int b = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
-    const int u = a.pos[n / a.cpr] + 1;
+    const int u = a.pos[n >> a.cshift] + 1;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, t = lane & 15;
     const size_t head = (size_t)n * a.heads + h;
     const float* K = a.k + head * a.cap * 64;
@@ -850,7 +850,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_attn_pv(AttnArgs a) {
     const int g = (wave & 3) * 4 + (lane >> 4), dq = lane & 15;
     const float* V = a.v + head * a.cap * 64;
     float4 vv[16];
-    const int u = a.pos[n / a.cpr] + 1;
+    const int u = a.pos[n >> a.cshift] + 1;
     if (wave < 4) {
         // keys past the position re-read the last key (a cache hit, not HBM traffic)
 #pragma unroll
@@ -914,7 +914,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_attn_pv(AttnArgs a) {
 // Chunk results added in order; the head's 64 outputs go to the out-projection activation.
 __global__ __launch_bounds__(64) void k_attn_reduce(AttnArgs a) {
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
-    const int u = a.pos[n / a.cpr] + 1, nch = (u + ATT_CHUNK - 1) / ATT_CHUNK;
+    const int u = a.pos[n >> a.cshift] + 1, nch = (u + ATT_CHUNK - 1) / ATT_CHUNK;
     const size_t head = (size_t)n * a.heads + h;
     float part[ATT_MAX_CHUNKS];
 #pragma unroll
@@ -1510,7 +1510,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
             else {
                 const int sec = row / a.dim, wi = row - sec * a.dim, head = wi >> 6, dm = wi & 63;
                 if (sec == 0) a.y[(size_t)n * a.dim + wi] = y;
-                else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + a.pos[(a.col0 + n) / a.cpr]) * 64 + dm] = y;
+                else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + a.pos[(a.col0 + n) >> a.cshift]) * 64 + dm] = y;
             }
         }
     }

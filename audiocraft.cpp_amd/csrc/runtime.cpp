@@ -138,6 +138,7 @@ struct mgx_stream {
     mgx_model* m = nullptr;
     int cap = 0, n_seq = 0, cross = 0, n_ctx = 0, used = 0, forwards = 0, max_chunks = 0;
     int n_req = 1, cpr = 1;                  // requests, and columns (streams) per request
+    int cshift = 0;                          // column n belongs to request n >> cshift
     int kv_rows = 0;                         // cache rows per head: cap rounded up to whole 256-key chunks
     hipStream_t hs = nullptr;
     DevArena mem;
@@ -307,7 +308,7 @@ enum { PROF_GEMV = 0, PROF_ATTN = 1 };
 void gemv(mgx_stream* s, mgx::GemvArgs a) {
     if (a.pro == mgx::PRO_ACT && a.src.bm && !mgx::gemv_mf_ok(a))
         throw Error(MGX_ERR_INVALID, "internal: a block-major source for a projection the matrix cores cannot run");
-    if (a.epi == mgx::EPI_QKV && (a.cpr < 1 || !a.pos))
+    if (a.epi == mgx::EPI_QKV && !a.pos)
         throw Error(MGX_ERR_INVALID, "internal: a K/V append without its positions");
     a.stamp = s->stamp_slot(PROF_GEMV, (double)a.w.in * a.w.out * bytes_per_weight(a.w.type));
     mgx::launch_gemv(a, s->hs);
@@ -415,14 +416,14 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
             mgx::GemvArgs a = ga(L.w[P_QKV], N);
             pro_ln(a, s->x, D, L.n1w, L.n1b, c.norm_eps);
             a.epi = mgx::EPI_QKV; a.y = s->qb; a.k = Kl; a.v = Vl; a.dim = D; a.heads = c.heads; a.cap = s->kv_rows;
-            a.pos = s->dpos; a.cpr = s->cpr;
+            a.pos = s->dpos; a.cshift = s->cshift;
             gemv_ad(s, a, L.ad[P_QKV]);
         }
         {
             mgx::AttnArgs at{};
             at.q = s->qb; at.k = Kl; at.v = Vl; at.scores = s->scores; at.opart = s->opart; at.cmax = s->cmax;
             at.dim = D; at.heads = c.heads; at.cap = s->kv_rows; at.max_chunks = s->max_chunks; at.ncol = N;
-            at.scale = scale; at.pos = s->dpos; at.cpr = s->cpr; at.out = s->act_o.view(L.w[P_OUT].type, bo);
+            at.scale = scale; at.pos = s->dpos; at.cshift = s->cshift; at.out = s->act_o.view(L.w[P_OUT].type, bo);
             at.out_f = L.ad[P_OUT] ? s->act_o.f : nullptr;
             // f32 K and V of every key attended, every stream
             at.stamp = s->stamp_slot(PROF_ATTN, 2.0 * N * c.heads * (position + 1) * 64 * 4);
@@ -566,6 +567,9 @@ void make_stream(mgx_model* m, int capacity, int n_seq, int n_req, const float* 
     m->live.fetch_add(1);
     s->cap = capacity; s->n_seq = n_seq; s->cross = cross ? 1 : 0; s->n_ctx = cross ? n_ctx : 0;
     s->n_req = n_req; s->cpr = n_seq / n_req;
+    // one request: every column (at most 16) maps to 0; batches have 1 or 2 columns a request
+    if (n_req > 1 && s->cpr > 2) throw Error(MGX_ERR_INVALID, "at most 2 streams per request");
+    s->cshift = n_req == 1 ? 4 : s->cpr - 1;
     s->max_chunks = (capacity + mgx::ATT_CHUNK - 1) / mgx::ATT_CHUNK;
     s->kv_rows = s->max_chunks * mgx::ATT_CHUNK;
     if (s->max_chunks > mgx::ATT_MAX_CHUNKS) throw Error(MGX_ERR_INVALID, "capacity above 4096 positions");
