@@ -48,6 +48,12 @@ WORKLOADS = {
                                        "rank-16 DoRA rows on qkv/ff.0/ff.2, 500-frame prompts + 1500-frame "
                                        "continuations"),
 }
+# The request server: 12 guided requests of mixed lengths submitted at once to 8 slots (request
+# i: prompt 250 + (53 i mod 251) frames, continuation 500 + (97 i mod 501) frames, memory,
+# prompt and sampling seeded 1 + i), against the same requests generated one after another.
+SERVER = dict(shape="medium", wtype=8, slots=8, requests=12, n_ctx=24, seed=1,
+              desc="musicgen-medium-shaped LM, Q8_0, 12 guided requests (prompts 250-500 frames, continuations "
+                   "500-1000 frames) served by 8 slots vs one at a time")
 BPW = {8: 34 / 32, 2: 18 / 32, 1: 2.0, 0: 4.0}
 HBM_PEAK_GBS = 8000.0
 
@@ -125,12 +131,77 @@ def cpu_baseline(w, model, t5, prompt, seconds, adapters=None):
                        f"({rep.decode_seconds:.1f} s, prefill {rep.prefill_seconds:.1f} s)")
 
 
+def serve_bench(mgx):
+    """Served throughput: every request submitted at t = 0 from its own thread to a server of
+    8 slots; continuation frames of all requests over the wall time from the first submission
+    to the last result (prefills included). The one-at-a-time figure runs the same requests
+    through mgx_generate back to back -- the reference server's policy, on these kernels."""
+    import threading
+    w = SERVER
+    model = mgx.SyntheticModel(w["shape"], w["wtype"], seed=w["seed"])
+    c = model.config
+    gm = mgx.Model(c, model.tensors)
+    reqs = []
+    for i in range(w["requests"]):
+        P, G = 250 + (53 * i) % 251, 500 + (97 * i) % 501
+        reqs.append(dict(P=P, G=G, t5=mgx.synth_memory(w["seed"] + i, w["n_ctx"]),
+                         prompt=mgx.synth_codes(w["seed"] + i, c.n_q, P, c.card),
+                         params=mgx.GenerateParams(P + G, 1, 1.0, 250, 3.0, w["seed"] + i)))
+    frames = sum(r["G"] for r in reqs)
+    srv = mgx.Server(gm, w["slots"], max(r["P"] + r["G"] for r in reqs), max_ctx=w["n_ctx"])
+    # warm the graphs of every chunk count on one request, untimed
+    r0 = reqs[-1]
+    srv.generate(r0["t5"], r0["prompt"], r0["P"], r0["params"])
+    before = srv.counters()
+    out = [None] * len(reqs)
+
+    def work(i):
+        r = reqs[i]
+        out[i] = srv.generate(r["t5"], r["prompt"], r["P"], r["params"])
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(len(reqs))]
+    hip_sync()
+    t0 = time.perf_counter()
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    served = time.perf_counter() - t0
+    after = srv.counters()
+    srv.close()
+    steps = after["steps"] - before["steps"]
+    occupancy = (after["slot_steps"] - before["slot_steps"]) / max(steps, 1)
+    print(f"[bench] served {len(reqs)} requests in {served:.2f} s", file=sys.stderr, flush=True)
+    hip_sync()
+    t0 = time.perf_counter()
+    for i, r in enumerate(reqs):
+        codes = gm.generate(r["t5"], r["prompt"], r["P"], r["params"])[0]
+        if not (codes == out[i][0]).all():
+            raise RuntimeError(f"request {i}: served codes differ from generating alone")
+    alone = time.perf_counter() - t0
+    print(f"[bench] one at a time: {alone:.2f} s", file=sys.stderr, flush=True)
+    print(json.dumps({
+        "metric": "served LM frames/sec, MusicGen-medium Q8_0 CFG=2, mixed-length requests",
+        "value": round(frames / served, 3), "unit": "frames/s", "n_gpus": 1, "steps": steps,
+        "warmup": 1, "ms_per_step": round(1000.0 * served / max(steps, 1), 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8xq8_0+f32", "data": "synthetic (seeded random N(0,0.02) weights, N(0,1) memory, uniform "
+                                          "prompt codes)",
+        "config": {"workload": w["desc"], "requests": len(reqs), "slots": w["slots"], "layers": c.layers,
+                   "dim": c.dim, "frames": frames, "prompt_frames": [r["P"] for r in reqs],
+                   "continuation_frames": [r["G"] for r in reqs], "parallelism": "single GPU"},
+        "served_seconds": round(served, 3),
+        "one_at_a_time": {"value": round(frames / alone, 3), "unit": "frames/s", "seconds": round(alone, 3)},
+        "speedup": round(alone / served, 3),
+        "mean_occupancy": round(occupancy, 2),
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1500)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="medium-q8", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="medium-q8", choices=sorted(WORKLOADS) + ["server-medium-q8"])
     ap.add_argument("--profile-every", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -144,6 +215,9 @@ def main():
               "The decode step shards by request; see DESIGN.md.", file=sys.stderr)
         sys.exit(2)
     import mgx
+    if args.workload == "server-medium-q8":
+        serve_bench(mgx)
+        return
     w = dict(WORKLOADS[args.workload])
     if args.prompt is not None:
         w["prompt"] = args.prompt
