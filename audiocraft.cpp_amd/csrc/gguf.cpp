@@ -294,6 +294,21 @@ mgx_lm_config lm_config(const mgx_gguf* g) {
     return c;
 }
 
+// T5EncoderConfig::from (t5.h:31-43): the ac.t5.* keys, each required
+mgx_t5_config t5_config(const mgx_gguf* g) {
+    mgx_t5_config c{};
+    c.dim = (int32_t)u32(g, "ac.t5.dim");
+    c.layers = (int32_t)u32(g, "ac.t5.layers");
+    c.heads = (int32_t)u32(g, "ac.t5.heads");
+    c.head_dim = (int32_t)u32(g, "ac.t5.head_dim");
+    c.intermediate = (int32_t)u32(g, "ac.t5.intermediate");
+    c.vocab = (int32_t)u32(g, "ac.t5.vocab");
+    c.relative_buckets = (int32_t)u32(g, "ac.t5.relative_buckets");
+    c.relative_max_distance = (int32_t)u32(g, "ac.t5.relative_max_distance");
+    c.eps = f32(g, "ac.t5.eps");
+    return c;
+}
+
 template <typename F> int guarded(F&& f) {
     try {
         f();
@@ -404,6 +419,27 @@ int mgx_model_create_from_gguf(const mgx_gguf* g, mgx_model** out) {
     });
     if (rc != MGX_OK) return rc;
     return mgx_model_create(&c, ts.data(), (int32_t)ts.size(), out);
+}
+
+int mgx_gguf_t5_config(const mgx_gguf* g, mgx_t5_config* out) {
+    return guarded([&] {
+        if (!g || !out) throw GgufError("null argument");
+        *out = t5_config(g);
+    });
+}
+
+int mgx_t5_create_from_gguf(const mgx_gguf* g, mgx_t5** out) {
+    mgx_t5_config c{};
+    std::vector<mgx_tensor> ts;
+    const int rc = guarded([&] {
+        if (!g || !out) throw GgufError("null argument");
+        *out = nullptr;
+        c = t5_config(g);
+        ts.reserve(g->tensors.size());
+        for (const TensorInfo& t : g->tensors) ts.push_back(view(g, t));
+    });
+    if (rc != MGX_OK) return rc;
+    return mgx_t5_create(&c, ts.data(), (int32_t)ts.size(), out);
 }
 
 int mgx_model_set_adapters_from_gguf(mgx_model* model, const mgx_gguf* g, const mgx_gguf* base, float strength) {

@@ -112,6 +112,10 @@ struct XAttnArgs {
     const float* v;
     int n_ctx, dim;   // n_ctx: the rows per head (every request's count when nc is null)
     const int* nc;    // optional [n_req] conditioning tokens per request (0: writes zeros)
+    // optional additive score bias: query r of head h adds bias[(h * n_req + r) * bias_stride + key]
+    const float* bias;
+    int bias_stride;
+    int shared_kv;    // every query attends the same keys (k, v of request 0)
     float scale;
     ActBuf out;       // cross.out's activation, column r
     float* out_f;     // optional f32 copy [n_req][dim]
@@ -186,5 +190,15 @@ void launch_stamp_init(unsigned long long* p, int n, hipStream_t s);
 void launch_dora_norm(const DevMat& w, const float* A, const float* B, int rank, float scale, float* norm, int* bad,
                       hipStream_t s);
 void launch_repack(int type, const uint8_t* raw, int64_t rows, int in, void* q, uint16_t* d, hipStream_t s);
+
+// T5 encoder pieces (src/ac/t5.h:85-140):
+// rows of a matrix (ggml get_rows): out[t][i] = m row ids[t], element i, for n ids
+void launch_rows(const DevMat& m, const int32_t* ids, int n, float* out, hipStream_t s);
+// RMS norm of ncol columns of n elements (stride apart): (x * (1 / sqrtf(mean(x^2) + eps))) * w
+void launch_rms(const float* x, int n, int ncol, int stride, const float* w, float eps, float* y, hipStream_t s);
+// bias[(h * seq + q) * seq + k] = table row buckets[q * seq + k], element h, + 0
+void launch_t5_bias(const DevMat& table, const int32_t* buckets, int seq, int heads, float* bias, hipStream_t s);
+// ReLU of ncol columns of n f32 values into the activation form of the consumer's weights
+void launch_relu_act(const float* x, int n, int ncol, const ActBuf& dst, hipStream_t s);
 
 }  // namespace mgx

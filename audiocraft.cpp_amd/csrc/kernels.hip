@@ -941,7 +941,8 @@ __global__ __launch_bounds__(64) void k_attn_reduce(AttnArgs a) {
 // the block must call it (it holds block barriers); threads >= 256 only take part in those.
 template <int KEYQ>
 __device__ __forceinline__ void xattn_head(const float* qh, const float* K, const float* V, int nc, float scale,
-                                           const ActBuf& out, float* out_f, int dim, int h, int r) {
+                                           const float* bias, const ActBuf& out, float* out_f, int dim, int h,
+                                           int r) {
     __shared__ float el[256];
     __shared__ float red_f[4];
     __shared__ float4 vred[16][16];
@@ -974,7 +975,8 @@ __device__ __forceinline__ void xattn_head(const float* qh, const float* K, cons
         }
     }
     const int jt = t * 16 + (wave & 3) * 4 + g;
-    const float sc = halving16(p, t) * scale;
+    float sc = halving16(p, t) * scale;
+    if (bias && jt < nc) sc = sc + bias[jt];
     float mx = jt < nc ? sc : -__builtin_inff();
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(mx, off); mx = mx > o ? mx : o; }
@@ -1022,8 +1024,10 @@ __device__ __forceinline__ void xattn_head(const float* qh, const float* K, cons
 __global__ __launch_bounds__(256) void k_xattn(XAttnArgs a) {
     const int h = blockIdx.x, r = blockIdx.y, H = gridDim.x;
     const int nc = a.nc ? a.nc[r] : a.n_ctx;
-    xattn_head<16>(a.q + (size_t)r * a.dim + h * 64, a.k + ((size_t)r * H + h) * a.n_ctx * 64,
-                   a.v + ((size_t)r * H + h) * a.n_ctx * 64, nc, a.scale, a.out, a.out_f, a.dim, h, r);
+    const size_t kr = a.shared_kv ? 0 : (size_t)r;
+    const float* bias = a.bias ? a.bias + ((size_t)h * gridDim.y + r) * a.bias_stride : nullptr;
+    xattn_head<16>(a.q + (size_t)r * a.dim + h * 64, a.k + (kr * H + h) * a.n_ctx * 64,
+                   a.v + (kr * H + h) * a.n_ctx * 64, nc, a.scale, bias, a.out, a.out_f, a.dim, h, r);
 }
 
 // The hoisted cross K/V: projected [n_ctx][2*dim] -> K [H][rows][64], V [H][rows][64] (first n_ctx rows).
@@ -1698,8 +1702,10 @@ __global__ __launch_bounds__(64) void k_xattn_w(XAttnArgs a) {
         if (a.out_f) a.out_f[(size_t)r * a.dim + h * 64 + lane] = 0.0f;
         return;
     }
-    const float* K = a.k + ((size_t)r * H + h) * a.n_ctx * 64;
-    const float* V = a.v + ((size_t)r * H + h) * a.n_ctx * 64;
+    const size_t kr = a.shared_kv ? 0 : (size_t)r;
+    const float* K = a.k + (kr * H + h) * a.n_ctx * 64;
+    const float* V = a.v + (kr * H + h) * a.n_ctx * 64;
+    const float* bias = a.bias ? a.bias + ((size_t)h * gridDim.y + r) * a.bias_stride : nullptr;
     __shared__ float pj[64];
     // every load first: q, the keys' float4s (key 4*it + g), then V column `lane` of each key
     const float4 q = ((const float4*)(a.q + (size_t)r * a.dim + h * 64))[t];
@@ -1725,7 +1731,9 @@ __global__ __launch_bounds__(64) void k_xattn_w(XAttnArgs a) {
         v = v + take_up<4>(v);
         v = v + take_up<2>(v);
         v = v + take_up<1>(v);
-        if (t == 0) pj[4 * it + g] = v * a.scale;
+        float sc = v * a.scale;
+        if (bias && 4 * it + g < nc) sc = sc + bias[4 * it + g];
+        if (t == 0) pj[4 * it + g] = sc;
     }
     __syncthreads();
     const float sc = lane < nc ? pj[lane] : -__builtin_inff();
@@ -1957,6 +1965,72 @@ void launch_dora_norm(const DevMat& w, const float* A, const float* B, int rank,
 void launch_repack(int type, const uint8_t* raw, int64_t rows, int in, void* q, uint16_t* d, hipStream_t s) {
     const int64_t nblocks = rows * (in / 32);
     hipLaunchKernelGGL(k_repack, dim3((unsigned)((nblocks + 255) / 256)), dim3(256), 0, s, type, raw, nblocks, (int8_t*)q, d);
+}
+
+// ------------------------------------------------------------------------------------
+// T5 encoder pieces (src/ac/t5.h:85-140)
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_rows(DevMat m, const int32_t* ids, int n, float* out) {
+    const int i = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
+    if (i >= m.in || t >= n) return;
+    out[(size_t)t * m.in + i] = mat_elem(m, ids[t], i);
+}
+void launch_rows(const DevMat& m, const int32_t* ids, int n, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(k_rows, dim3((m.in + 255) / 256, n), dim3(256), 0, s, m, ids, n, out);
+}
+
+// One column per 256-thread block. Thread i owns partial i: float4 groups i, i+256, ... of the
+// column, x*x (f32) summed in element order in double; the 256 partials folded by the butterfly
+// (the same order as the LayerNorm prologue's sums).
+__global__ __launch_bounds__(256) void k_rms(const float* x, int n, int stride, const float* w, float eps, float* y) {
+    __shared__ double red[256];
+    const int tid = threadIdx.x, lane = tid & 63, col = blockIdx.x, nf = n / 4;
+    const float4* xs = (const float4*)(x + (size_t)col * stride);
+    double acc = 0.0;
+    for (int f = tid; f < nf; f += 256) {
+        const float4 v = xs[f];
+        acc = acc + (double)(v.x * v.x); acc = acc + (double)(v.y * v.y);
+        acc = acc + (double)(v.z * v.z); acc = acc + (double)(v.w * v.w);
+    }
+    red[tid] = acc;
+    __syncthreads();
+    const float mean = (float)(fold256(red, lane) / (double)n);
+    const float scale = 1.0f / __builtin_sqrtf(mean + eps);
+    const float4* ws = (const float4*)w;
+    float4* ys = (float4*)(y + (size_t)col * stride);
+    for (int f = tid; f < nf; f += 256) {
+        const float4 v = xs[f], g = ws[f];
+        float4 o;
+        o.x = v.x * scale; o.y = v.y * scale; o.z = v.z * scale; o.w = v.w * scale;
+        o.x = o.x * g.x; o.y = o.y * g.y; o.z = o.z * g.z; o.w = o.w * g.w;
+        ys[f] = o;
+    }
+}
+void launch_rms(const float* x, int n, int ncol, int stride, const float* w, float eps, float* y, hipStream_t s) {
+    hipLaunchKernelGGL(k_rms, dim3(ncol), dim3(256), 0, s, x, n, stride, w, eps, y);
+}
+
+__global__ __launch_bounds__(256) void k_t5_bias(DevMat table, const int32_t* buckets, int seq, int heads,
+                                                 float* bias) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= seq * seq * heads) return;
+    const int h = i / (seq * seq), qk = i - h * seq * seq;
+    bias[i] = mat_elem(table, buckets[qk], h) + 0.0f;
+}
+void launch_t5_bias(const DevMat& table, const int32_t* buckets, int seq, int heads, float* bias, hipStream_t s) {
+    hipLaunchKernelGGL(k_t5_bias, dim3((seq * seq * heads + 255) / 256), dim3(256), 0, s, table, buckets, seq, heads,
+                       bias);
+}
+
+// n is a multiple of 32, so each 32-element block is one half-wave (the Q8 form's scale group).
+__global__ __launch_bounds__(256) void k_relu_act(const float* x, int n, ActBuf dst) {
+    const int i = blockIdx.x * 256 + threadIdx.x, col = blockIdx.y;
+    if (i >= n) return;
+    const float v = x[(size_t)col * n + i];
+    put_act(dst, col, i, v > 0.0f ? v : 0.0f, threadIdx.x & 63);
+}
+void launch_relu_act(const float* x, int n, int ncol, const ActBuf& dst, hipStream_t s) {
+    hipLaunchKernelGGL(k_relu_act, dim3((n + 255) / 256, ncol), dim3(256), 0, s, x, n, dst);
 }
 
 }  // namespace mgx

@@ -7,6 +7,7 @@
 // (src/mg/pattern.h:31-115).
 #include "mgx.h"
 #include "kernels.h"
+#include "host.h"
 
 #include <hip/hip_runtime.h>
 
@@ -24,55 +25,9 @@
 #include <string>
 #include <vector>
 
+using namespace mgxh;
+
 namespace {
-
-thread_local std::string g_error;
-
-struct Error : std::runtime_error {
-    int code;
-    Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
-};
-
-#define HIP_OK(expr)                                                                            \
-    do {                                                                                        \
-        hipError_t e_ = (expr);                                                                 \
-        if (e_ != hipSuccess)                                                                   \
-            throw Error(MGX_ERR_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_));     \
-    } while (0)
-
-template <typename F> int guarded(F&& f) {
-    try {
-        f();
-        return MGX_OK;
-    } catch (const Error& e) {
-        g_error = e.what();
-        return e.code;
-    } catch (const std::exception& e) {
-        g_error = e.what();
-        return MGX_ERR_INVALID;
-    }
-}
-
-double now_s() {
-    using clock = std::chrono::steady_clock;
-    return std::chrono::duration<double>(clock::now().time_since_epoch()).count();
-}
-
-// Device allocations owned by one object, freed together.
-struct DevArena {
-    std::vector<void*> ptrs;
-    template <typename T> T* alloc(size_t count) {
-        void* p = nullptr;
-        if (count == 0) count = 1;
-        HIP_OK(hipMalloc(&p, count * sizeof(T)));
-        ptrs.push_back(p);
-        return (T*)p;
-    }
-    void release() {
-        for (void* p : ptrs) (void)hipFree(p);
-        ptrs.clear();
-    }
-};
 
 enum { P_QKV, P_OUT, P_CQ, P_CKV, P_COUT, P_FF0, P_FF2, P_COUNT };
 const char* const PROJ[P_COUNT] = {"self.qkv", "self.out", "cross.q", "cross.kv", "cross.out", "ff.0", "ff.2"};
@@ -196,85 +151,6 @@ struct mgx_stream {
 
 namespace {
 
-size_t row_bytes(int type, int64_t in) {
-    switch (type) {
-    case mgx::T_F32: return (size_t)in * 4;
-    case mgx::T_F16: return (size_t)in * 2;
-    case mgx::T_Q8_0: return (size_t)(in / 32) * 34;
-    case mgx::T_Q4_0: return (size_t)(in / 32) * 18;
-    }
-    return 0;
-}
-
-const mgx_tensor* find(const mgx_tensor* t, int n, const std::string& name) {
-    for (int i = 0; i < n; ++i)
-        if (t[i].name && name == t[i].name) return &t[i];
-    return nullptr;
-}
-
-const mgx_tensor& need(const mgx_tensor* t, int n, const std::string& name, int64_t ne0, int64_t ne1) {
-    const mgx_tensor* x = find(t, n, name);
-    if (!x) throw Error(MGX_ERR_INVALID, "missing tensor " + name);
-    if (x->ne[0] != ne0 || x->ne[1] != ne1 || (x->ne[2] > 1) || (x->ne[3] > 1))
-        throw Error(MGX_ERR_INVALID, "bad shape for " + name);
-    if (!x->data) throw Error(MGX_ERR_INVALID, "no data for " + name);
-    const size_t rb = row_bytes(x->type, ne0);
-    if (!rb) throw Error(MGX_ERR_INVALID, "unsupported tensor type for " + name);
-    if ((x->type == mgx::T_Q8_0 || x->type == mgx::T_Q4_0) && ne0 % 32)
-        throw Error(MGX_ERR_INVALID, name + ": quantized rows must hold whole 32-blocks");
-    if (x->nbytes && x->nbytes < rb * (size_t)ne1) throw Error(MGX_ERR_INVALID, "short data for " + name);
-    return *x;
-}
-
-// Uploads `rows` rows of one ggml tensor into `dst` starting at row `row0` (dst already sized).
-void upload_rows(mgx_model* m, const mgx_tensor& t, mgx::DevMat& dst, int64_t row0, hipStream_t s) {
-    const int64_t rows = t.ne[1];
-    const int in = (int)t.ne[0];
-    const size_t rb = row_bytes(t.type, in);
-    if (t.type == mgx::T_F32 || t.type == mgx::T_F16) {
-        const size_t es = t.type == mgx::T_F32 ? 4 : 2;
-        HIP_OK(hipMemcpyAsync((uint8_t*)dst.q + (size_t)row0 * in * es, t.data, rb * rows, hipMemcpyHostToDevice, s));
-        return;
-    }
-    uint8_t* raw = nullptr;
-    HIP_OK(hipMalloc(&raw, rb * rows));
-    HIP_OK(hipMemcpyAsync(raw, t.data, rb * rows, hipMemcpyHostToDevice, s));
-    const size_t qrow = t.type == mgx::T_Q8_0 ? (size_t)in : (size_t)in / 2;
-    mgx::launch_repack(t.type, raw, rows, in, (uint8_t*)dst.q + (size_t)row0 * qrow,
-                       (uint16_t*)dst.d + (size_t)row0 * (in / 32), s);
-    HIP_OK(hipGetLastError());
-    HIP_OK(hipStreamSynchronize(s));
-    HIP_OK(hipFree(raw));
-}
-
-mgx::DevMat alloc_mat(mgx_model* m, int type, int in, int out) {
-    mgx::DevMat d{};
-    d.type = type; d.in = in; d.out = out;
-    switch (type) {
-    case mgx::T_Q8_0: d.q = m->mem.alloc<int8_t>((size_t)in * out); d.d = m->mem.alloc<uint16_t>((size_t)(in / 32) * out); break;
-    case mgx::T_Q4_0: d.q = m->mem.alloc<uint8_t>((size_t)in / 2 * out); d.d = m->mem.alloc<uint16_t>((size_t)(in / 32) * out); break;
-    case mgx::T_F16: d.q = m->mem.alloc<uint16_t>((size_t)in * out); break;
-    default: d.q = m->mem.alloc<float>((size_t)in * out); break;
-    }
-    return d;
-}
-
-mgx::DevMat load_mat(mgx_model* m, const mgx_tensor* t, int n, const std::string& name, int in, int out, hipStream_t s) {
-    const mgx_tensor& x = need(t, n, name, in, out);
-    mgx::DevMat d = alloc_mat(m, x.type, in, out);
-    upload_rows(m, x, d, 0, s);
-    return d;
-}
-
-const float* load_vec(mgx_model* m, const mgx_tensor* t, int n, const std::string& name, int len, hipStream_t s) {
-    const mgx_tensor* x = find(t, n, name);
-    if (!x || x->type != mgx::T_F32 || x->ne[0] != len || !x->data)
-        throw Error(MGX_ERR_INVALID, "missing or bad f32 vector " + name);
-    float* d = m->mem.alloc<float>((size_t)len);
-    HIP_OK(hipMemcpyAsync(d, x->data, sizeof(float) * (size_t)len, hipMemcpyHostToDevice, s));
-    return d;
-}
-
 // sin_positions (lm.h:102-116) for positions 0..n-1, computed on the host exactly as the
 // reference does (double pow/cos/sin, rounded to float) and kept resident.
 std::vector<float> sin_table(int n, const mgx_lm_config& c) {
@@ -314,27 +190,6 @@ void gemv(mgx_stream* s, mgx::GemvArgs a) {
     mgx::launch_gemv(a, s->hs);
 }
 
-mgx::GemvArgs ga(const mgx::DevMat& w, int ncol) {
-    mgx::GemvArgs a{};
-    a.w = w; a.ncol = ncol;
-    return a;
-}
-mgx::GemvArgs& pro_ln(mgx::GemvArgs& a, const float* x, int stride, const float* w, const float* b, float eps) {
-    a.pro = mgx::PRO_LN; a.x = x; a.x_stride = stride; a.ln_w = w; a.ln_b = b; a.eps = eps;
-    return a;
-}
-mgx::GemvArgs& pro_f32(mgx::GemvArgs& a, const float* x, int stride) {
-    a.pro = mgx::PRO_F32; a.x = x; a.x_stride = stride;
-    return a;
-}
-mgx::GemvArgs& pro_act(mgx::GemvArgs& a, const mgx::ActBuf& src) {
-    a.pro = mgx::PRO_ACT; a.src = src;
-    return a;
-}
-mgx::GemvArgs& epi_store(mgx::GemvArgs& a, float* y, int stride, bool resid = false) {
-    a.epi = resid ? mgx::EPI_RESID : mgx::EPI_STORE; a.y = y; a.y_stride = stride;
-    return a;
-}
 
 // A projection with its adapter, if any: A x first, from the column the projection builds
 // (its LayerNorm or f32 source; for an activation-form source, `xf` holds the same column in
@@ -652,34 +507,34 @@ int mgx_model_create(const mgx_lm_config* cfg, const mgx_tensor* t, int32_t n, m
         HIP_OK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
         struct StreamGuard { hipStream_t s; ~StreamGuard() { (void)hipStreamSynchronize(s); (void)hipStreamDestroy(s); } } sg{s};
         for (int q = 0; q < c.n_q; ++q)
-            m->emb[q] = load_mat(m.get(), t, n, "lm.emb." + std::to_string(q) + ".weight", c.dim, c.card + 1, s);
+            m->emb[q] = load_mat(m->mem, t, n, "lm.emb." + std::to_string(q) + ".weight", c.dim, c.card + 1, s);
         // The n_q heads as one [n_q*card][dim] matrix: logits land as [n_q][card] per stream.
         {
             const mgx_tensor& h0 = need(t, n, "lm.head.0.weight", c.dim, c.card);
-            m->heads = alloc_mat(m.get(), h0.type, c.dim, c.n_q * c.card);
+            m->heads = alloc_mat(m->mem, h0.type, c.dim, c.n_q * c.card);
             for (int q = 0; q < c.n_q; ++q) {
                 const mgx_tensor& h = need(t, n, "lm.head." + std::to_string(q) + ".weight", c.dim, c.card);
                 if (h.type != h0.type) throw Error(MGX_ERR_INVALID, "the output heads must share one type");
-                upload_rows(m.get(), h, m->heads, (int64_t)q * c.card, s);
+                upload_rows(h, m->heads, (int64_t)q * c.card, s);
             }
         }
-        m->cond_proj = load_mat(m.get(), t, n, "lm.cond_proj.weight", c.cond_dim, c.dim, s);
-        m->cond_proj_b = load_vec(m.get(), t, n, "lm.cond_proj.bias", c.dim, s);
-        m->out_w = load_vec(m.get(), t, n, "lm.out_norm.weight", c.dim, s);
-        m->out_b = load_vec(m.get(), t, n, "lm.out_norm.bias", c.dim, s);
+        m->cond_proj = load_mat(m->mem, t, n, "lm.cond_proj.weight", c.cond_dim, c.dim, s);
+        m->cond_proj_b = load_vec(m->mem, t, n, "lm.cond_proj.bias", c.dim, s);
+        m->out_w = load_vec(m->mem, t, n, "lm.out_norm.weight", c.dim, s);
+        m->out_b = load_vec(m->mem, t, n, "lm.out_norm.bias", c.dim, s);
         m->L.resize((size_t)c.layers);
         for (int i = 0; i < c.layers; ++i) {
             LayerW& L = m->L[(size_t)i];
             const std::string p = "lm." + std::to_string(i) + ".";
             const int ins[P_COUNT] = {c.dim, c.dim, c.dim, c.dim, c.dim, c.dim, c.ff_dim};
             const int outs[P_COUNT] = {3 * c.dim, c.dim, c.dim, 2 * c.dim, c.dim, c.ff_dim, c.dim};
-            for (int k = 0; k < P_COUNT; ++k) L.w[k] = load_mat(m.get(), t, n, p + PROJ[k] + ".weight", ins[k], outs[k], s);
-            L.n1w = load_vec(m.get(), t, n, p + "norm1.weight", c.dim, s);
-            L.n1b = load_vec(m.get(), t, n, p + "norm1.bias", c.dim, s);
-            L.ncw = load_vec(m.get(), t, n, p + "norm_cross.weight", c.dim, s);
-            L.ncb = load_vec(m.get(), t, n, p + "norm_cross.bias", c.dim, s);
-            L.n2w = load_vec(m.get(), t, n, p + "norm2.weight", c.dim, s);
-            L.n2b = load_vec(m.get(), t, n, p + "norm2.bias", c.dim, s);
+            for (int k = 0; k < P_COUNT; ++k) L.w[k] = load_mat(m->mem, t, n, p + PROJ[k] + ".weight", ins[k], outs[k], s);
+            L.n1w = load_vec(m->mem, t, n, p + "norm1.weight", c.dim, s);
+            L.n1b = load_vec(m->mem, t, n, p + "norm1.bias", c.dim, s);
+            L.ncw = load_vec(m->mem, t, n, p + "norm_cross.weight", c.dim, s);
+            L.ncb = load_vec(m->mem, t, n, p + "norm_cross.bias", c.dim, s);
+            L.n2w = load_vec(m->mem, t, n, p + "norm2.weight", c.dim, s);
+            L.n2b = load_vec(m->mem, t, n, p + "norm2.bias", c.dim, s);
         }
         // every Q8_0 projection's matrix-core copies: tile-transposed scales, operand-order quants
         auto with_dt = [&](mgx::DevMat& w) {

@@ -102,3 +102,20 @@ def write_adapter(path, adapters, base_name=None, kv_extra=()):
             m = np.ascontiguousarray(a["magnitude"], np.float32)
             ts.append((a["target"] + ".magnitude", 0, [m.shape[0]], m))
     write(path, kv, ts)
+
+
+def t5_kv(config, max_length=256, weight_type="F16"):
+    """The encoder keys tools/convert_t5.py:67-81 writes (tokenizer keys left out)."""
+    c = config
+    return [("general.architecture", STR, "ac-t5"), ("ac.t5.dim", U32, c.dim), ("ac.t5.layers", U32, c.layers),
+            ("ac.t5.heads", U32, c.heads), ("ac.t5.head_dim", U32, c.head_dim),
+            ("ac.t5.intermediate", U32, c.intermediate), ("ac.t5.vocab", U32, c.vocab),
+            ("ac.t5.relative_buckets", U32, c.relative_buckets),
+            ("ac.t5.relative_max_distance", U32, c.relative_max_distance), ("ac.t5.eps", F32, c.eps),
+            ("ac.t5.max_length", U32, max_length), ("ac.t5.weight_type", STR, weight_type)]
+
+
+def write_t5(path, model, kv=None):
+    """A SyntheticT5 as a T5 encoder GGUF file."""
+    write(path, kv if kv is not None else t5_kv(model.config),
+          [(n, t, [ne0, ne1] if ne1 > 1 else [ne0], data) for n, t, ne0, ne1, data in model.tensors])

@@ -24,6 +24,12 @@ class LmConfig(C.Structure):
                [(n, C.c_float) for n in ("max_period", "norm_eps", "cfg_coef")]
 
 
+class T5Config(C.Structure):
+    """mgx_t5_config = ac::T5EncoderConfig (src/ac/t5.h:20-44)."""
+    _fields_ = [(n, C.c_int32) for n in ("dim", "layers", "heads", "head_dim", "intermediate", "vocab",
+                                         "relative_buckets", "relative_max_distance")] + [("eps", C.c_float)]
+
+
 class Tensor(C.Structure):
     _fields_ = [("name", C.c_char_p), ("type", C.c_int32), ("ne", C.c_int64 * 4), ("data", C.c_void_p),
                 ("nbytes", C.c_uint64)]
@@ -73,7 +79,8 @@ EXPORTS = ["mgx_model_create", "mgx_model_set_adapters", "mgx_model_destroy", "m
            "mgx_session_requests", "mgx_gguf_open", "mgx_gguf_close", "mgx_gguf_tensor_count", "mgx_gguf_tensor",
            "mgx_gguf_find_tensor", "mgx_gguf_u32", "mgx_gguf_f32", "mgx_gguf_string", "mgx_gguf_lm_config",
            "mgx_model_create_from_gguf", "mgx_model_set_adapters_from_gguf", "mgx_server_create",
-           "mgx_server_generate", "mgx_server_stats", "mgx_server_destroy", "mgx_last_error"]
+           "mgx_server_generate", "mgx_server_stats", "mgx_server_destroy", "mgx_t5_create", "mgx_gguf_t5_config",
+           "mgx_t5_create_from_gguf", "mgx_t5_encode", "mgx_t5_destroy", "mgx_t5_relative_bucket", "mgx_last_error"]
 
 _lib = None
 
@@ -139,6 +146,13 @@ def load(path=None):
     lib.mgx_server_stats.argtypes = [P, C.POINTER(ServerCounters)]
     lib.mgx_server_destroy.argtypes = [P]
     lib.mgx_server_destroy.restype = None
+    lib.mgx_t5_create.argtypes = [C.POINTER(T5Config), C.POINTER(Tensor), C.c_int32, C.POINTER(P)]
+    lib.mgx_gguf_t5_config.argtypes = [P, C.POINTER(T5Config)]
+    lib.mgx_t5_create_from_gguf.argtypes = [P, C.POINTER(P)]
+    lib.mgx_t5_encode.argtypes = [P, P, C.c_int32, P]
+    lib.mgx_t5_destroy.argtypes = [P]
+    lib.mgx_t5_destroy.restype = None
+    lib.mgx_t5_relative_bucket.argtypes = [C.c_int32, C.c_int32, C.c_int32]
     if path is None:
         _lib = lib
     return lib
@@ -157,22 +171,33 @@ def use_guidance(cfg_coef, description_empty):
     return bool(load().mgx_use_guidance(cfg_coef, 1 if description_empty else 0))
 
 
+def _tensor_array(tensors, names):
+    """(name, ggml type, ne0, ne1, bytes) tuples as an mgx_tensor array; names keeps the
+    encoded names alive."""
+    arr = (Tensor * len(tensors))()
+    for i, (name, ttype, ne0, ne1, data) in enumerate(tensors):
+        b = name.encode()
+        names.append(b)
+        arr[i].name = b
+        arr[i].type = ttype
+        arr[i].ne[0], arr[i].ne[1], arr[i].ne[2], arr[i].ne[3] = ne0, ne1, 1, 1
+        arr[i].data = data.ctypes.data
+        arr[i].nbytes = data.nbytes
+    return arr
+
+
+def t5_relative_bucket(relative_position, num_buckets=32, max_distance=128):
+    return load().mgx_t5_relative_bucket(int(relative_position), num_buckets, max_distance)
+
+
 class Model:
     """mgx_model: the weights of one LM uploaded to the current HIP device."""
 
     def __init__(self, config, tensors):
         self.lib = load()
         self.config = config
-        arr = (Tensor * len(tensors))()
         self._names = []
-        for i, (name, ttype, ne0, ne1, data) in enumerate(tensors):
-            b = name.encode()
-            self._names.append(b)
-            arr[i].name = b
-            arr[i].type = ttype
-            arr[i].ne[0], arr[i].ne[1], arr[i].ne[2], arr[i].ne[3] = ne0, ne1, 1, 1
-            arr[i].data = data.ctypes.data
-            arr[i].nbytes = data.nbytes
+        arr = _tensor_array(tensors, self._names)
         h = C.c_void_p()
         _check(self.lib, self.lib.mgx_model_create(C.byref(config), arr, len(tensors), C.byref(h)))
         self.handle = h
@@ -281,6 +306,11 @@ class Gguf:
     def lm_config(self):
         c = LmConfig()
         _check(self.lib, self.lib.mgx_gguf_lm_config(self.handle, C.byref(c)))
+        return c
+
+    def t5_config(self):
+        c = T5Config()
+        _check(self.lib, self.lib.mgx_gguf_t5_config(self.handle, C.byref(c)))
         return c
 
     def close(self):
@@ -494,6 +524,47 @@ class Server:
     def close(self):
         if getattr(self, "handle", None):
             self.lib.mgx_server_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class T5:
+    """mgx_t5: the T5-base encoder resident on the current HIP device."""
+
+    def __init__(self, config, tensors):
+        self.lib = load()
+        self.config = config
+        names = []
+        arr = _tensor_array(tensors, names)
+        h = C.c_void_p()
+        _check(self.lib, self.lib.mgx_t5_create(C.byref(config), arr, len(tensors), C.byref(h)))
+        self.handle = h
+
+    @classmethod
+    def from_gguf(cls, gguf):
+        t = cls.__new__(cls)
+        t.lib = load()
+        t.config = gguf.t5_config()
+        h = C.c_void_p()
+        _check(t.lib, t.lib.mgx_t5_create_from_gguf(gguf.handle, C.byref(h)))
+        t.handle = h
+        return t
+
+    def encode(self, ids):
+        """last_hidden_state [n_tokens][dim] of token ids [n_tokens]."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.zeros((ids.size, self.config.dim), np.float32)
+        _check(self.lib, self.lib.mgx_t5_encode(self.handle, _ptr(ids), ids.size, _ptr(out)))
+        return out
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.mgx_t5_destroy(self.handle)
             self.handle = None
 
     def __del__(self):

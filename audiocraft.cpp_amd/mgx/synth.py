@@ -10,7 +10,7 @@ import os
 
 import numpy as np
 
-from .lib import LmConfig
+from .lib import LmConfig, T5Config
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 SYNTH_PATH = os.path.join(os.path.dirname(_HERE), "libmgx_synth.so")
@@ -183,3 +183,66 @@ class SyntheticModel:
 
     def nbytes(self):
         return sum(t[4].nbytes for t in self.tensors)
+
+
+# T5 encoder shapes: T5-base (t5.h:20-29) and small ones for tests.
+T5_SHAPES = {
+    "t5-tiny": dict(dim=128, layers=2, heads=2, intermediate=256, vocab=300),
+    "t5-mini": dict(dim=768, layers=1, heads=12, intermediate=3072, vocab=1000),
+    "t5-base": dict(dim=768, layers=12, heads=12, intermediate=3072, vocab=32128),
+}
+
+
+def make_t5_config(shape, **over):
+    s = dict(T5_SHAPES[shape]) if isinstance(shape, str) else dict(shape)
+    s.update(over)
+    c = T5Config()
+    c.dim, c.layers, c.heads, c.head_dim = s["dim"], s["layers"], s["heads"], s.get("head_dim", 64)
+    c.intermediate, c.vocab = s["intermediate"], s["vocab"]
+    c.relative_buckets, c.relative_max_distance = s.get("relative_buckets", 32), s.get("relative_max_distance", 128)
+    c.eps = s.get("eps", 1e-6)
+    return c
+
+
+class SyntheticT5:
+    """Tensors of one synthetic T5 encoder (names of tools/convert_t5.py:107-119): embedding
+    N(0, 1) and linears N(0, 0.04) (wi, wo N(0, 0.03)) in the requested ggml type, the relative
+    bias table [buckets][heads] N(0, 1) and RMS norm weights 1 + N(0, 0.1), f32."""
+
+    def __init__(self, shape, wtype, seed=0, **over):
+        self.config = c = make_t5_config(shape, **over)
+        self.wtype = wtype
+        L = _lib()
+        self.tensors = []
+
+        def mat(name, ne0, ne1, sd, ttype=wtype):
+            buf = np.empty(int(L.mgx_row_bytes(ttype, ne0)) * ne1, np.uint8)
+            if L.mgx_synth_tensor(L.mgx_synth_seed(seed, name.encode()), ttype, ne0, ne1, sd, 0.0, buf.ctypes.data):
+                raise ValueError(f"cannot synthesize {name}")
+            self.tensors.append((name, ttype, ne0, ne1, buf))
+
+        def norm(name, n):
+            v = np.empty(n, np.float32)
+            L.mgx_synth_normal(L.mgx_synth_seed(seed, name.encode()), 0.1, v.ctypes.data, n)
+            self.tensors.append((name, 0, n, 1, (v + np.float32(1.0)).view(np.uint8).copy()))
+
+        d, inner, F = c.dim, c.heads * c.head_dim, c.intermediate
+        mat("te.embed.weight", d, c.vocab, 1.0)
+        mat("te.relative_attention_bias.weight", c.heads, c.relative_buckets, 1.0, ttype=0)
+        for i in range(c.layers):
+            p = f"te.{i}."
+            norm(p + "attn_norm.weight", d)
+            for w in ("q", "k", "v"):
+                mat(p + w + ".weight", d, inner, 0.04)
+            mat(p + "o.weight", inner, d, 0.04)
+            norm(p + "ffn_norm.weight", d)
+            mat(p + "wi.weight", d, F, 0.03)
+            mat(p + "wo.weight", F, d, 0.03)
+        norm("te.norm.weight", d)
+
+
+def synth_ids(seed, n, vocab):
+    """Token ids [n] uniform in [0, vocab)."""
+    out = np.empty(n, np.int32)
+    _lib().mgx_synth_codes(_lib().mgx_synth_seed(seed, b"t5.ids"), vocab, out.ctypes.data, n)
+    return out

@@ -263,6 +263,30 @@ int mgx_model_set_adapters_from_gguf(mgx_model* model, const mgx_gguf* adapter, 
 /* The message of the last failed call on this thread. */
 const char* mgx_last_error(void);
 
+/* The T5-base text encoder (ac::T5EncoderConfig / ac::t5_encode, src/ac/t5.h:20-140, as
+   ac::encode_prompt runs it, src/ac/conditioner.h:56-108: one prompt at its own token count,
+   no padding). The reference loads the encoder from its GGUF and frees it in every call; an
+   mgx_t5 stays resident on the current HIP device and mgx_t5_encode is only the forward:
+   ids [n_tokens] (the tokenizer's output, 1 to 256 tokens) -> hidden_out [n_tokens][dim], the
+   last hidden state TextCondition::hidden holds. Tensors as tools/convert_t5.py:107-119 names
+   them: te.embed.weight, te.relative_attention_bias.weight (F32 or F16), te.<i>.{attn_norm,
+   q,k,v,o,ffn_norm,wi,wo}.weight, te.norm.weight; matrices F32 / F16 / Q8_0 / Q4_0, norms F32.
+   head_dim must be 64. One encode at a time per encoder (calls from several threads wait for
+   each other). */
+typedef struct mgx_t5_config {
+    int32_t dim, layers, heads, head_dim, intermediate, vocab, relative_buckets, relative_max_distance;
+    float eps;
+} mgx_t5_config;
+typedef struct mgx_t5 mgx_t5;
+int mgx_t5_create(const mgx_t5_config* config, const mgx_tensor* tensors, int32_t n_tensors, mgx_t5** out);
+/* T5EncoderConfig::from (t5.h:31-43) and the encoder straight from its GGUF file. */
+int mgx_gguf_t5_config(const mgx_gguf* file, mgx_t5_config* out);
+int mgx_t5_create_from_gguf(const mgx_gguf* file, mgx_t5** out);
+int mgx_t5_encode(mgx_t5* t5, const int32_t* ids, int32_t n_tokens, float* hidden_out);
+void mgx_t5_destroy(mgx_t5* t5);
+/* t5_relative_position_bucket (t5.h:46-61): relative_position = key - query. */
+int32_t mgx_t5_relative_bucket(int32_t relative_position, int32_t num_buckets, int32_t max_distance);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,6 +21,7 @@
  *   sampling ................. src/mg/sampling.h:32-105
  *   Rng ...................... src/rng.h:15-33
  *   DelayPattern ............. src/mg/pattern.h:31-115
+ *   t5_encode / buckets ...... src/ac/t5.h:46-140 (T5-base encoder, conditioner.h:56-108)
  *
  * The reference does every tensor op through ggml (submodule betweentwomidnights/ggml @
  * e3db5210), which is not vendored, so the ggml CPU kernels' bit-level behaviour cannot be
@@ -1148,6 +1149,124 @@ REF_API int ref_generate(const ref_model* m, const float* t5_hidden, int n_ctx, 
 }
 
 /* Bumped whenever a documented reduction order changes; fixtures record it. */
+/* ------------------------------------------------------------------------------------ */
+/* T5-base encoder (src/ac/t5.h:20-140, src/ac/conditioner.h:56-108)                     */
+/* ------------------------------------------------------------------------------------ */
+/* Conventions beyond the decode path's: rms_norm = mean of squares as a double sum
+   (element i -> partial (i/4) mod 256 of (double)(x*x), 256-wide butterfly), then
+   (x * (1.0f / sqrtf(mean + eps))) * w, each product rounded in f32 (ggml_rms_norm then
+   ggml_mul). The learned position bias is added to the unscaled q.k score (t5.h:120-121:
+   mul_mat, then add of bias + mask, the mask all zeros), soft_max and V as in attend(). ReLU
+   maps everything not above zero to 0. */
+typedef struct {
+    int dim, layers, heads, head_dim, intermediate, vocab, relative_buckets, relative_max_distance;
+    float eps;
+} ref_t5_config;
+
+/* transformers' T5Attention._relative_position_bucket, bidirectional (t5.h:46-61):
+   relative position = key - query; the upper half of the buckets holds keys after the query;
+   distances below a quarter of the buckets map one to one, longer ones logarithmically up to
+   max_distance. The logarithm is taken in f32 as the reference does. */
+REF_API int ref_t5_bucket(int relative_position, int num_buckets, int max_distance) {
+    const int half = num_buckets / 2, exact = half / 2;
+    const int base = relative_position > 0 ? half : 0;
+    const int dist = relative_position < 0 ? -relative_position : relative_position;
+    if (dist < exact) return base + dist;
+    int far = exact;
+    const float span = logf((float)max_distance / (float)exact);
+    if (span > 0.0f) far += (int)(logf((float)dist / (float)exact) / span * (float)(half - exact));
+    return base + (far < half - 1 ? far : half - 1);
+}
+
+static void rms_norm(const float* x, int n, const float* w, float eps, float* y) {
+    double part[256];
+    for (int l = 0; l < 256; ++l) part[l] = 0.0;
+    for (int i = 0; i < n; ++i) part[(i >> 2) & 255] = part[(i >> 2) & 255] + (double)(x[i] * x[i]);
+    const float mean = (float)(fold_d(part, 256) / (double)n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int i = 0; i < n; ++i) {
+        const float v = x[i] * scale;
+        y[i] = v * w[i];
+    }
+}
+
+REF_API void ref_rms_norm(const float* x, int n, const float* w, float eps, float* y) { rms_norm(x, n, w, eps, y); }
+
+/* last_hidden_state [seq][dim] of ids [seq] (t5_encode, t5.h:85-140, as encode_prompt runs it:
+   no padding, an all-zero mask). Returns 0, or -1 with ref_last_error. */
+REF_API int ref_t5_encode(const ref_t5_config* c, const ref_tensor* t, int n, const int32_t* ids, int seq,
+                          float* out) {
+    const int D = c->dim, H = c->heads, hd = c->head_dim, inner = c->heads * c->head_dim, F = c->intermediate;
+    if (seq <= 0) { set_err("no tokens"); return -1; }
+    mat_t emb, rel;
+    if (get_mat(t, n, "te.embed.weight", D, c->vocab, &emb) ||
+        get_mat(t, n, "te.relative_attention_bias.weight", H, c->relative_buckets, &rel))
+        return -1;
+    const float* fnorm = get_vec(t, n, "te.norm.weight", D);
+    if (!fnorm) return -1;
+    for (int i = 0; i < seq; ++i)
+        if (ids[i] < 0 || ids[i] >= c->vocab) { set_err("token id out of range"); return -1; }
+    float* x = (float*)malloc(sizeof(float) * (size_t)seq * D);
+    float* h = (float*)malloc(sizeof(float) * (size_t)seq * (D > inner ? D : inner));
+    float* q = (float*)malloc(sizeof(float) * (size_t)seq * inner);
+    float* k = (float*)malloc(sizeof(float) * (size_t)seq * inner);
+    float* v = (float*)malloc(sizeof(float) * (size_t)seq * inner);
+    float* vt = (float*)malloc(sizeof(float) * (size_t)inner * seq);
+    float* o = (float*)malloc(sizeof(float) * (size_t)seq * inner);
+    float* y = (float*)malloc(sizeof(float) * (size_t)seq * D);
+    float* f = (float*)malloc(sizeof(float) * (size_t)seq * F);
+    float* bias = (float*)malloc(sizeof(float) * (size_t)H * seq * seq);
+    float* rowbuf = (float*)malloc(sizeof(float) * (size_t)(D > H ? D : H));
+    float* sc = (float*)malloc(sizeof(float) * (size_t)seq);
+    int rc = -1;
+    for (int i = 0; i < seq; ++i) dequant_row(&emb, ids[i], x + (size_t)i * D);
+    /* bias[h][q][k] = table[bucket(k - q)][h] + 0 (the zero mask added, t5.h:100) */
+    for (int qi = 0; qi < seq; ++qi)
+        for (int ki = 0; ki < seq; ++ki) {
+            dequant_row(&rel, ref_t5_bucket(ki - qi, c->relative_buckets, c->relative_max_distance), rowbuf);
+            for (int hh = 0; hh < H; ++hh) bias[((size_t)hh * seq + qi) * seq + ki] = rowbuf[hh] + 0.0f;
+        }
+    for (int l = 0; l < c->layers; ++l) {
+        char name[96];
+        mat_t wq, wk, wv, wo, wi, w2;
+        const float *an, *fn;
+#define T5M(field, stem, in_, out_) \
+        snprintf(name, sizeof name, "te.%d." stem ".weight", l); \
+        if (get_mat(t, n, name, in_, out_, &field)) goto done;
+        T5M(wq, "q", D, inner) T5M(wk, "k", D, inner) T5M(wv, "v", D, inner) T5M(wo, "o", inner, D)
+        T5M(wi, "wi", D, F) T5M(w2, "wo", F, D)
+#undef T5M
+        snprintf(name, sizeof name, "te.%d.attn_norm.weight", l);
+        if (!(an = get_vec(t, n, name, D))) goto done;
+        snprintf(name, sizeof name, "te.%d.ffn_norm.weight", l);
+        if (!(fn = get_vec(t, n, name, D))) goto done;
+        for (int i = 0; i < seq; ++i) rms_norm(x + (size_t)i * D, D, an, c->eps, h + (size_t)i * D);
+        matmul(&wq, NULL, h, seq, q);
+        matmul(&wk, NULL, h, seq, k);
+        matmul(&wv, NULL, h, seq, v);
+        for (int j = 0; j < seq; ++j)
+            for (int d = 0; d < inner; ++d) vt[(size_t)d * seq + j] = v[(size_t)j * inner + d];
+        for (int hh = 0; hh < H; ++hh)
+            for (int qi = 0; qi < seq; ++qi)
+                attend(q + (size_t)qi * inner + hh * hd, hd, seq, k + hh * hd, (size_t)inner,
+                       vt + (size_t)hh * hd * seq, (size_t)seq, bias + ((size_t)hh * seq + qi) * seq, 1.0f,
+                       o + (size_t)qi * inner + hh * hd, sc);
+        matmul(&wo, NULL, o, seq, y);
+        for (size_t i = 0; i < (size_t)seq * D; ++i) x[i] = x[i] + y[i];
+        for (int i = 0; i < seq; ++i) rms_norm(x + (size_t)i * D, D, fn, c->eps, h + (size_t)i * D);
+        matmul(&wi, NULL, h, seq, f);
+        for (size_t i = 0; i < (size_t)seq * F; ++i) f[i] = f[i] > 0.0f ? f[i] : 0.0f;
+        matmul(&w2, NULL, f, seq, y);
+        for (size_t i = 0; i < (size_t)seq * D; ++i) x[i] = x[i] + y[i];
+    }
+    for (int i = 0; i < seq; ++i) rms_norm(x + (size_t)i * D, D, fnorm, c->eps, out + (size_t)i * D);
+    rc = 0;
+done:
+    free(x); free(h); free(q); free(k); free(v); free(vt); free(o); free(y); free(f); free(bias); free(rowbuf);
+    free(sc);
+    return rc;
+}
+
 REF_API int ref_convention(void) { return 3; }
 
 REF_API void ref_set_threads(int n) {

@@ -23,6 +23,11 @@ class RefConfig(C.Structure):
                [(n, C.c_float) for n in ("max_period", "norm_eps", "cfg_coef")]
 
 
+class RefT5Config(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("dim", "layers", "heads", "head_dim", "intermediate", "vocab",
+                                         "relative_buckets", "relative_max_distance")] + [("eps", C.c_float)]
+
+
 class RefTensor(C.Structure):
     _fields_ = [("name", C.c_char_p), ("type", C.c_int32), ("ne0", C.c_int64), ("ne1", C.c_int64),
                 ("data", C.c_void_p)]
@@ -98,6 +103,9 @@ def lib():
         L.ref_generate.argtypes = [P, P, C.c_int, C.c_int, P, C.c_int, C.POINTER(RefGenParams), C.c_int, C.c_int, P, P,
                                    P, C.POINTER(RefReport)]
         L.ref_set_threads.argtypes = [C.c_int]
+        L.ref_t5_bucket.argtypes = [C.c_int, C.c_int, C.c_int]
+        L.ref_rms_norm.argtypes = [P, C.c_int, P, C.c_float, P]
+        L.ref_t5_encode.argtypes = [C.POINTER(RefT5Config), C.POINTER(RefTensor), C.c_int, P, C.c_int, P]
         L.ref_convention.restype = C.c_int
         _lib = L
     return _lib
@@ -253,3 +261,33 @@ class RefRng:
 
     def uniform(self):
         return lib().ref_rng_uniform(self.buf)
+
+
+def t5_bucket(relative_position, num_buckets=32, max_distance=128):
+    return lib().ref_t5_bucket(int(relative_position), num_buckets, max_distance)
+
+
+def rms_norm(x, w, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    y = np.empty_like(x)
+    lib().ref_rms_norm(ptr(x), x.size, ptr(w), eps, ptr(y))
+    return y
+
+
+def t5_encode(config, tensors, ids):
+    """The oracle's T5 encoder: last_hidden_state [seq][dim] of ids [seq] (t5.h:85-140)."""
+    cfg = RefT5Config()
+    for name, _ in RefT5Config._fields_:
+        setattr(cfg, name, getattr(config, name))
+    keep = []
+    arr = (RefTensor * len(tensors))()
+    for i, (name, ttype, ne0, ne1, data) in enumerate(tensors):
+        b = name.encode()
+        keep.append(b)
+        arr[i].name, arr[i].type, arr[i].ne0, arr[i].ne1, arr[i].data = b, ttype, ne0, ne1, data.ctypes.data
+    ids = np.ascontiguousarray(ids, np.int32)
+    out = np.zeros((ids.size, config.dim), np.float32)
+    if lib().ref_t5_encode(C.byref(cfg), arr, len(tensors), ptr(ids), ids.size, ptr(out)):
+        raise RuntimeError(err())
+    return out

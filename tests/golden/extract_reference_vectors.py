@@ -2,7 +2,9 @@
 """Copies the golden vectors that the reference's own unit tests hold -- as data -- into
 tests/golden/*.json: the softmax / top-k / argmax fixtures of tests/sampling_test.cpp
 (generated there by tests/gen_sampling_fixture.py from audiocraft's sample_top_k) and the
-delay-pattern fixtures of tests/pattern_test.cpp (from audiocraft's DelayedPatternProvider).
+delay-pattern fixtures of tests/pattern_test.cpp (from audiocraft's DelayedPatternProvider),
+and the T5 relative-position buckets of tests/t5_bucket_test.cpp (from transformers'
+T5Attention._relative_position_bucket, bidirectional, 32 buckets, max distance 128).
 
 Reads the reference tree as text (default /root/reference); run once, outputs committed."""
 import json
@@ -53,8 +55,18 @@ def pattern():
     return {"source": "tests/pattern_test.cpp:90-146", "cases": cases}
 
 
+def t5_buckets():
+    text = open(os.path.join(REF, "tests", "t5_bucket_test.cpp")).read()
+    body = text[text.index("static const Case cases[] = {"):]
+    body = body[:body.index("};")]
+    pairs = [(int(a), int(b)) for a, b in re.findall(r"\{(-?\d+),\s*(-?\d+)\}", body)]
+    return {"source": "tests/t5_bucket_test.cpp:26-31", "num_buckets": 32, "max_distance": 128,
+            "cases": [{"relative_position": a, "bucket": b} for a, b in pairs]}
+
+
 if __name__ == "__main__":
-    for name, fn in (("sampling_cases.json", sampling), ("pattern_cases.json", pattern)):
+    for name, fn in (("sampling_cases.json", sampling), ("pattern_cases.json", pattern),
+                     ("t5_bucket_cases.json", t5_buckets)):
         with open(os.path.join(HERE, name), "w") as f:
             json.dump(fn(), f, indent=1)
         print("wrote", name)
