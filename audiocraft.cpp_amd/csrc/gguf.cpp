@@ -294,6 +294,53 @@ mgx_lm_config lm_config(const mgx_gguf* g) {
     return c;
 }
 
+std::vector<int32_t> i32s(const mgx_gguf* g, const std::string& k) {
+    const Value& v = key(g, k);
+    if (v.type != G_ARR || v.arr_type != G_I32) throw GgufError("key is not an i32 array: " + k);
+    std::vector<int32_t> out((size_t)v.count);
+    if (v.count) std::memcpy(out.data(), v.data, 4 * (size_t)v.count);
+    return out;
+}
+
+// SeanetConfig::from (seanet.h:60-92)
+mgx_codec_config codec_config(const mgx_gguf* g) {
+    if (str(g, "ac.architecture") != "audiocraft") throw GgufError("not an audiocraft GGUF");
+    if (u32(g, "ac.format_version") != 1) throw GgufError("unsupported audiocraft GGUF version");
+    mgx_codec_config c{};
+    const std::string quantizer = str(g, "ac.codec.quantizer");
+    c.elu = str(g, "ac.codec.activation") == "ELU" ? 1 : 0;
+    c.channels = (int32_t)u32(g, "ac.codec.channels");
+    c.n_filters = (int32_t)u32(g, "ac.codec.n_filters");
+    c.n_residual_layers = (int32_t)u32(g, "ac.codec.n_residual_layers");
+    c.kernel_size = (int32_t)u32(g, "ac.codec.kernel_size");
+    c.residual_kernel_size = (int32_t)u32(g, "ac.codec.residual_kernel_size");
+    c.last_kernel_size = (int32_t)u32(g, "ac.codec.last_kernel_size");
+    c.dilation_base = (int32_t)u32(g, "ac.codec.dilation_base");
+    c.compress = (int32_t)u32(g, "ac.codec.compress");
+    c.lstm_layers = (int32_t)u32(g, "ac.codec.lstm_layers");
+    c.latent_dim = (int32_t)u32(g, "ac.codec.latent_dim");
+    (void)u32(g, "ac.codec.encoder_dim");
+    c.sample_rate = (int32_t)u32(g, "ac.codec.sample_rate");
+    c.hop_length = (int32_t)u32(g, "ac.codec.hop_length");
+    if (quantizer == "rvq") {
+        c.rvq = 1;
+        c.rvq_n_q = (int32_t)u32(g, "ac.codec.rvq_n_q");
+        c.rvq_bins = (int32_t)u32(g, "ac.codec.rvq_bins");
+    }
+    c.frame_rate = (int32_t)u32(g, "ac.codec.frame_rate");
+    const std::vector<int32_t> r = i32s(g, "ac.codec.ratios");
+    if (r.empty()) throw GgufError("codec has no ratios");
+    if (r.size() > 8) throw GgufError("codec has more than 8 ratios");
+    int hop = 1;
+    for (size_t i = 0; i < r.size(); ++i) {
+        c.ratios[i] = r[i];
+        hop *= r[i];
+    }
+    c.n_ratios = (int32_t)r.size();
+    if (hop != c.hop_length) throw GgufError("codec ratio product disagrees with the declared hop length");
+    return c;
+}
+
 // T5EncoderConfig::from (t5.h:31-43): the ac.t5.* keys, each required
 mgx_t5_config t5_config(const mgx_gguf* g) {
     mgx_t5_config c{};
@@ -440,6 +487,27 @@ int mgx_t5_create_from_gguf(const mgx_gguf* g, mgx_t5** out) {
     });
     if (rc != MGX_OK) return rc;
     return mgx_t5_create(&c, ts.data(), (int32_t)ts.size(), out);
+}
+
+int mgx_gguf_codec_config(const mgx_gguf* g, mgx_codec_config* out) {
+    return guarded([&] {
+        if (!g || !out) throw GgufError("null argument");
+        *out = codec_config(g);
+    });
+}
+
+int mgx_codec_create_from_gguf(const mgx_gguf* g, mgx_codec** out) {
+    mgx_codec_config c{};
+    std::vector<mgx_tensor> ts;
+    const int rc = guarded([&] {
+        if (!g || !out) throw GgufError("null argument");
+        *out = nullptr;
+        c = codec_config(g);
+        ts.reserve(g->tensors.size());
+        for (const TensorInfo& t : g->tensors) ts.push_back(view(g, t));
+    });
+    if (rc != MGX_OK) return rc;
+    return mgx_codec_create(&c, ts.data(), (int32_t)ts.size(), out);
 }
 
 int mgx_model_set_adapters_from_gguf(mgx_model* model, const mgx_gguf* g, const mgx_gguf* base, float strength) {

@@ -119,3 +119,27 @@ def write_t5(path, model, kv=None):
     """A SyntheticT5 as a T5 encoder GGUF file."""
     write(path, kv if kv is not None else t5_kv(model.config),
           [(n, t, [ne0, ne1] if ne1 > 1 else [ne0], data) for n, t, ne0, ne1, data in model.tensors])
+
+
+def codec_kv(cfg):
+    """The codec keys tools/convert_seanet.py:395-415 writes, from a SeanetConfig-like dict."""
+    kv = [("general.architecture", STR, "ac-seanet"), ("ac.architecture", STR, "audiocraft"),
+          ("ac.format_version", U32, 1), ("ac.codec.quantizer", STR, cfg.get("quantizer", "rvq")),
+          ("ac.codec.activation", STR, cfg.get("activation", "ELU")), ("ac.codec.channels", U32, cfg["channels"]),
+          ("ac.codec.n_filters", U32, cfg["n_filters"]), ("ac.codec.n_residual_layers", U32, cfg["n_residual_layers"]),
+          ("ac.codec.ratios", ARR, (I32, list(cfg["ratios"]))), ("ac.codec.kernel_size", U32, cfg["kernel_size"]),
+          ("ac.codec.residual_kernel_size", U32, cfg["residual_kernel_size"]),
+          ("ac.codec.last_kernel_size", U32, cfg["last_kernel_size"]),
+          ("ac.codec.dilation_base", U32, cfg["dilation_base"]), ("ac.codec.compress", U32, cfg["compress"]),
+          ("ac.codec.lstm_layers", U32, cfg["lstm_layers"]), ("ac.codec.latent_dim", U32, cfg["latent_dim"]),
+          ("ac.codec.encoder_dim", U32, cfg["encoder_dim"]), ("ac.codec.sample_rate", U32, cfg["sample_rate"]),
+          ("ac.codec.hop_length", U32, cfg["hop_length"]), ("ac.codec.frame_rate", U32, cfg["frame_rate"]),
+          ("ac.codec.weight_type", STR, "F32")]
+    if cfg.get("quantizer", "rvq") == "rvq":
+        kv += [("ac.codec.rvq_n_q", U32, cfg["rvq_n_q"]), ("ac.codec.rvq_bins", U32, cfg["rvq_bins"])]
+    return kv
+
+
+def write_codec(path, codec, kv=None):
+    """A SyntheticCodec as a codec GGUF file."""
+    write(path, kv if kv is not None else codec_kv(codec.config), codec.tensors)

@@ -30,6 +30,29 @@ class T5Config(C.Structure):
                                          "relative_buckets", "relative_max_distance")] + [("eps", C.c_float)]
 
 
+class CodecConfig(C.Structure):
+    """mgx_codec_config = ac::SeanetConfig (src/ac/seanet.h:32-92)."""
+    _fields_ = [(n, C.c_int32) for n in ("channels", "n_filters", "n_residual_layers", "kernel_size",
+                                         "residual_kernel_size", "last_kernel_size", "dilation_base", "compress",
+                                         "lstm_layers", "latent_dim", "sample_rate", "hop_length", "frame_rate",
+                                         "rvq", "rvq_n_q", "rvq_bins", "elu", "n_ratios")] + \
+               [("ratios", C.c_int32 * 8)]
+
+    @classmethod
+    def of(cls, d):
+        """From a SeanetConfig-like dict (mgx.synth.make_codec_config)."""
+        c = cls()
+        for n, _ in cls._fields_:
+            if n in d and n != "ratios":
+                setattr(c, n, int(d[n]))
+        c.rvq = 1 if d.get("quantizer", "rvq") == "rvq" else 0
+        c.elu = 1 if d.get("activation", "ELU") == "ELU" else 0
+        c.n_ratios = len(d["ratios"])
+        for i, r in enumerate(d["ratios"]):
+            c.ratios[i] = r
+        return c
+
+
 class Tensor(C.Structure):
     _fields_ = [("name", C.c_char_p), ("type", C.c_int32), ("ne", C.c_int64 * 4), ("data", C.c_void_p),
                 ("nbytes", C.c_uint64)]
@@ -80,7 +103,9 @@ EXPORTS = ["mgx_model_create", "mgx_model_set_adapters", "mgx_model_destroy", "m
            "mgx_gguf_find_tensor", "mgx_gguf_u32", "mgx_gguf_f32", "mgx_gguf_string", "mgx_gguf_lm_config",
            "mgx_model_create_from_gguf", "mgx_model_set_adapters_from_gguf", "mgx_server_create",
            "mgx_server_generate", "mgx_server_stats", "mgx_server_destroy", "mgx_t5_create", "mgx_gguf_t5_config",
-           "mgx_t5_create_from_gguf", "mgx_t5_encode", "mgx_t5_destroy", "mgx_t5_relative_bucket", "mgx_last_error"]
+           "mgx_t5_create_from_gguf", "mgx_t5_encode", "mgx_t5_destroy", "mgx_t5_relative_bucket", "mgx_codec_create",
+           "mgx_gguf_codec_config", "mgx_codec_create_from_gguf", "mgx_codec_decode", "mgx_codec_decode_latent",
+           "mgx_codec_destroy", "mgx_last_error"]
 
 _lib = None
 
@@ -153,6 +178,13 @@ def load(path=None):
     lib.mgx_t5_destroy.argtypes = [P]
     lib.mgx_t5_destroy.restype = None
     lib.mgx_t5_relative_bucket.argtypes = [C.c_int32, C.c_int32, C.c_int32]
+    lib.mgx_codec_create.argtypes = [C.POINTER(CodecConfig), C.POINTER(Tensor), C.c_int32, C.POINTER(P)]
+    lib.mgx_gguf_codec_config.argtypes = [P, C.POINTER(CodecConfig)]
+    lib.mgx_codec_create_from_gguf.argtypes = [P, C.POINTER(P)]
+    lib.mgx_codec_decode.argtypes = [P, P, C.c_int32, P]
+    lib.mgx_codec_decode_latent.argtypes = [P, P, C.c_int32, P]
+    lib.mgx_codec_destroy.argtypes = [P]
+    lib.mgx_codec_destroy.restype = None
     if path is None:
         _lib = lib
     return lib
@@ -306,6 +338,11 @@ class Gguf:
     def lm_config(self):
         c = LmConfig()
         _check(self.lib, self.lib.mgx_gguf_lm_config(self.handle, C.byref(c)))
+        return c
+
+    def codec_config(self):
+        c = CodecConfig()
+        _check(self.lib, self.lib.mgx_gguf_codec_config(self.handle, C.byref(c)))
         return c
 
     def t5_config(self):
@@ -565,6 +602,63 @@ class T5:
     def close(self):
         if getattr(self, "handle", None):
             self.lib.mgx_t5_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Codec:
+    """mgx_codec: the EnCodec decoder resident on the current HIP device. tensors: (name, ggml
+    type, ne list, bytes) -- the codec's tensors are up to 3-D."""
+
+    def __init__(self, config, tensors):
+        self.lib = load()
+        self.config = config if isinstance(config, CodecConfig) else CodecConfig.of(config)
+        names = []
+        arr = (Tensor * len(tensors))()
+        for i, (name, ttype, ne, data) in enumerate(tensors):
+            b = name.encode()
+            names.append(b)
+            arr[i].name, arr[i].type = b, ttype
+            for d in range(4):
+                arr[i].ne[d] = ne[d] if d < len(ne) else 1
+            arr[i].data, arr[i].nbytes = data.ctypes.data, data.nbytes
+        h = C.c_void_p()
+        _check(self.lib, self.lib.mgx_codec_create(C.byref(self.config), arr, len(tensors), C.byref(h)))
+        self.handle = h
+
+    @classmethod
+    def from_gguf(cls, gguf):
+        k = cls.__new__(cls)
+        k.lib = load()
+        k.config = gguf.codec_config()
+        h = C.c_void_p()
+        _check(k.lib, k.lib.mgx_codec_create_from_gguf(gguf.handle, C.byref(h)))
+        k.handle = h
+        return k
+
+    def decode(self, codes):
+        """codes [n_q][frames] -> audio [channels][frames * hop_length]."""
+        codes = np.ascontiguousarray(codes, np.int32)
+        frames = codes.shape[1]
+        out = np.zeros((self.config.channels, frames * self.config.hop_length), np.float32)
+        _check(self.lib, self.lib.mgx_codec_decode(self.handle, _ptr(codes), frames, _ptr(out)))
+        return out
+
+    def decode_latent(self, latent):
+        latent = np.ascontiguousarray(latent, np.float32)
+        frames = latent.shape[1]
+        out = np.zeros((self.config.channels, frames * self.config.hop_length), np.float32)
+        _check(self.lib, self.lib.mgx_codec_decode_latent(self.handle, _ptr(latent), frames, _ptr(out)))
+        return out
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.mgx_codec_destroy(self.handle)
             self.handle = None
 
     def __del__(self):

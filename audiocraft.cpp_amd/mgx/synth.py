@@ -246,3 +246,74 @@ def synth_ids(seed, n, vocab):
     out = np.empty(n, np.int32)
     _lib().mgx_synth_codes(_lib().mgx_synth_seed(seed, b"t5.ids"), vocab, out.ctypes.data, n)
     return out
+
+
+# SEANet codec shapes (SeanetConfig, src/ac/seanet.h:32-58): MusicGen's EnCodec 32 kHz and a
+# tiny one whose odd ratio exercises the asymmetric transposed-conv trim.
+CODEC_SHAPES = {
+    "codec-tiny": dict(n_filters=4, ratios=[2, 3], latent_dim=8, rvq_n_q=2, rvq_bins=16, sample_rate=6000),
+    "codec-mini": dict(n_filters=16, ratios=[4, 5], latent_dim=32, rvq_n_q=4, rvq_bins=64, sample_rate=32000),
+    "encodec-32k": dict(n_filters=64, ratios=[8, 5, 4, 4], latent_dim=128, rvq_n_q=4, rvq_bins=2048,
+                        sample_rate=32000),
+}
+
+
+def make_codec_config(shape, **over):
+    s = dict(quantizer="rvq", activation="ELU", channels=1, n_residual_layers=1, kernel_size=7,
+             residual_kernel_size=3, last_kernel_size=7, dilation_base=2, compress=2, lstm_layers=2)
+    s.update(CODEC_SHAPES[shape] if isinstance(shape, str) else shape)
+    s.update(over)
+    hop = 1
+    for r in s["ratios"]:
+        hop *= r
+    s["hop_length"] = hop
+    s["frame_rate"] = s["sample_rate"] // hop
+    s["encoder_dim"] = s["latent_dim"]
+    return s
+
+
+class SyntheticCodec:
+    """The decoder half of a SEANet / EnCodec checkpoint as tools/convert_seanet.py names it
+    (weight norm already fused): conv weights N(0, 1/sqrt(in * k)), biases N(0, 0.1), LSTM
+    matrices U(-1/sqrt(H), 1/sqrt(H)), codebooks N(0, 1), all f32. `weights` maps names to
+    numpy arrays in row-major ggml order (conv [out][in][k], transposed conv [out*k][in]);
+    `tensors` lists (name, type, ne list, bytes) for the library."""
+
+    def __init__(self, shape, seed=0, **over):
+        self.config = c = make_codec_config(shape, **over)
+        rng = np.random.default_rng(seed)
+        W = {}
+
+        def conv(name, cin, cout, k):
+            W[name + ".weight"] = rng.normal(0, 1 / np.sqrt(cin * k), (cout, cin, k)).astype(np.float32)
+            W[name + ".bias"] = rng.normal(0, 0.1, cout).astype(np.float32)
+
+        bott = c["n_filters"] * 2 ** len(c["ratios"])
+        conv("codec.decoder.in", c["latent_dim"], bott, c["kernel_size"])
+        for l in range(c["lstm_layers"]):
+            a = 1 / np.sqrt(bott)
+            for m in ("w_ih", "w_hh"):
+                W[f"codec.decoder.lstm.{l}.{m}"] = rng.uniform(-a, a, (4 * bott, bott)).astype(np.float32)
+            W[f"codec.decoder.lstm.{l}.bias"] = rng.uniform(-2 * a, 2 * a, 4 * bott).astype(np.float32)
+        mult = 2 ** len(c["ratios"])
+        for s, ratio in enumerate(c["ratios"]):
+            cin = c["n_filters"] * mult
+            cout = cin // 2
+            k = 2 * ratio
+            p = f"codec.decoder.stage.{s}."
+            W[p + "up.weight_col2im"] = rng.normal(0, 1 / np.sqrt(cin * 2), (cout * k, cin)).astype(np.float32)
+            W[p + "up.bias"] = rng.normal(0, 0.1, cout).astype(np.float32)
+            for j in range(c["n_residual_layers"]):
+                hid = cout // c["compress"]
+                conv(p + f"res.{j}.conv1", cout, hid, c["residual_kernel_size"])
+                conv(p + f"res.{j}.conv2", hid, cout, 1)
+            mult //= 2
+        conv("codec.decoder.out", c["n_filters"], c["channels"], c["last_kernel_size"])
+        for i in range(c["rvq_n_q"]):
+            W[f"codec.rvq.{i}.embed"] = rng.normal(0, 1, (c["rvq_bins"], c["latent_dim"])).astype(np.float32)
+        self.weights = W
+        self.tensors = [(n, 0, list(a.shape[::-1]), a.view(np.uint8).reshape(-1)) for n, a in W.items()]
+
+    def codes(self, seed, frames):
+        rng = np.random.default_rng(seed)
+        return rng.integers(0, self.config["rvq_bins"], (self.config["rvq_n_q"], frames)).astype(np.int32)

@@ -287,6 +287,33 @@ void mgx_t5_destroy(mgx_t5* t5);
 /* t5_relative_position_bucket (t5.h:46-61): relative_position = key - query. */
 int32_t mgx_t5_relative_bucket(int32_t relative_position, int32_t num_buckets, int32_t max_distance);
 
+/* The EnCodec decoder: RVQ codes -> audio (rvq_decode, src/mg/encodec.h:69-84; codec_decode,
+   src/ac/codec.h:127-146, over seanet_decode_pre / lstm_graph / seanet_decode_post,
+   src/ac/seanet.h:282-317, src/ac/lstm.h:44-101), resident on the current HIP device. The
+   config is SeanetConfig (seanet.h:32-92); only ELU codecs (MusicGen's EnCodec) are accepted.
+   Tensors as tools/convert_seanet.py names them, all f32: codec.decoder.in.{weight,bias},
+   codec.decoder.lstm.<l>.{w_ih,w_hh,bias}, codec.decoder.stage.<s>.up.{weight_col2im,bias},
+   codec.decoder.stage.<s>.res.<j>.conv{1,2}.{weight,bias}, codec.decoder.out.{weight,bias},
+   codec.rvq.<i>.embed. codes [rvq_n_q][frames] -> audio_out [channels][frames * hop_length];
+   mgx_codec_decode_latent takes the latent [latent_dim][frames] instead. f32 throughout; the
+   result equals the reference's within f32 rounding. One decode at a time per codec. */
+typedef struct mgx_codec_config {
+    int32_t channels, n_filters, n_residual_layers, kernel_size, residual_kernel_size, last_kernel_size;
+    int32_t dilation_base, compress, lstm_layers, latent_dim, sample_rate, hop_length, frame_rate;
+    int32_t rvq, rvq_n_q, rvq_bins;   /* rvq: 1 when the quantizer is "rvq" */
+    int32_t elu;                      /* 1 when the activation is "ELU" */
+    int32_t n_ratios;
+    int32_t ratios[8];                /* decoder order */
+} mgx_codec_config;
+typedef struct mgx_codec mgx_codec;
+int mgx_codec_create(const mgx_codec_config* config, const mgx_tensor* tensors, int32_t n_tensors, mgx_codec** out);
+/* SeanetConfig::from (seanet.h:60-92) and the decoder straight from the codec's GGUF file. */
+int mgx_gguf_codec_config(const mgx_gguf* file, mgx_codec_config* out);
+int mgx_codec_create_from_gguf(const mgx_gguf* file, mgx_codec** out);
+int mgx_codec_decode(mgx_codec* codec, const int32_t* codes, int32_t frames, float* audio_out);
+int mgx_codec_decode_latent(mgx_codec* codec, const float* latent, int32_t frames, float* audio_out);
+void mgx_codec_destroy(mgx_codec* codec);
+
 #ifdef __cplusplus
 }
 #endif

@@ -3,8 +3,11 @@
 tests/golden/*.json: the softmax / top-k / argmax fixtures of tests/sampling_test.cpp
 (generated there by tests/gen_sampling_fixture.py from audiocraft's sample_top_k) and the
 delay-pattern fixtures of tests/pattern_test.cpp (from audiocraft's DelayedPatternProvider),
-and the T5 relative-position buckets of tests/t5_bucket_test.cpp (from transformers'
-T5Attention._relative_position_bucket, bidirectional, 32 buckets, max distance 128).
+the T5 relative-position buckets of tests/t5_bucket_test.cpp (from transformers'
+T5Attention._relative_position_bucket, bidirectional, 32 buckets, max distance 128), the
+torch.nn.LSTM vectors of tests/lstm_test.cpp (tests/gen_lstm_fixture.py) and the residual
+vector quantizer vectors of tests/codec_test.cpp (transformers' EncodecResidualVectorQuantizer,
+tests/gen_codec_fixture.py).
 
 Reads the reference tree as text (default /root/reference); run once, outputs committed."""
 import json
@@ -64,9 +67,28 @@ def t5_buckets():
             "cases": [{"relative_position": a, "bucket": b} for a, b in pairs]}
 
 
+def lstm():
+    text = open(os.path.join(REF, "tests", "lstm_test.cpp")).read()
+    fa = arrays(text, "float")
+    m = re.search(r"constexpr int H = (\d+), T = (\d+), L = (\d+);", text)
+    H, T, L = (int(v) for v in m.groups())
+    return {"source": "tests/lstm_test.cpp:57-111 (torch.nn.LSTM, tests/gen_lstm_fixture.py)", "hidden": H,
+            "frames": T, "layers": L, "arrays": fa}
+
+
+def rvq():
+    text = open(os.path.join(REF, "tests", "codec_test.cpp")).read()
+    fa, ia = arrays(text, "float"), arrays(text, "int32_t")
+    m = re.search(r"constexpr int RVQ_NQ = (\d+), RVQ_BINS = (\d+), RVQ_DIM = (\d+), RVQ_FRAMES = (\d+);", text)
+    nq, bins, dim, frames = (int(v) for v in m.groups())
+    return {"source": "tests/codec_test.cpp:82-181 (EncodecResidualVectorQuantizer, tests/gen_codec_fixture.py)",
+            "n_q": nq, "bins": bins, "dim": dim, "frames": frames, "embed": fa["rvq_embed"],
+            "latent": fa["rvq_latent"], "codes": ia["rvq_codes"], "quantized": fa["rvq_quantized"]}
+
+
 if __name__ == "__main__":
     for name, fn in (("sampling_cases.json", sampling), ("pattern_cases.json", pattern),
-                     ("t5_bucket_cases.json", t5_buckets)):
+                     ("t5_bucket_cases.json", t5_buckets), ("lstm_cases.json", lstm), ("rvq_cases.json", rvq)):
         with open(os.path.join(HERE, name), "w") as f:
             json.dump(fn(), f, indent=1)
         print("wrote", name)
