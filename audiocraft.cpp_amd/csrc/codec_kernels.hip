@@ -176,6 +176,53 @@ __global__ __launch_bounds__(256) void k_lstm_step(LstmStepArgs a) {
     }
 }
 
+// The same step with one wave per hidden unit: the wave loads its unit's four gate rows as
+// float4s, PER per lane per row (H = 256 * PER), every load issued before the first product;
+// 4 units per block, H / 4 blocks.
+template <int PER>
+__global__ __launch_bounds__(256) void k_lstm_step_w(LstmStepArgs a) {
+    extern __shared__ float hs[];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, H = a.H, j = blockIdx.x * 4 + wave;
+    float4 wv[4][PER];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float4* row = (const float4*)(a.w_hh + (size_t)(g * H + j) * H);
+#pragma unroll
+        for (int p = 0; p < PER; ++p) wv[g][p] = row[lane + 64 * p];
+    }
+    float pj[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) pj[g] = a.proj[(size_t)(g * H + j) * a.T + a.t];
+    for (int e = tid; e < H; e += 256) hs[e] = a.h_prev[e];
+    __syncthreads();
+    const float4* h4 = (const float4*)hs;
+    float acc[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        float v = 0.0f;
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const float4 h = h4[lane + 64 * p];
+            v = __builtin_fmaf(wv[g][p].x, h.x, v);
+            v = __builtin_fmaf(wv[g][p].y, h.y, v);
+            v = __builtin_fmaf(wv[g][p].z, h.z, v);
+            v = __builtin_fmaf(wv[g][p].w, h.w, v);
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+        acc[g] = v;
+    }
+    if (lane == 0) {
+        const float ig = sigmoid_f(pj[0] + acc[0]), fg = sigmoid_f(pj[1] + acc[1]);
+        const float gg = tanhf(pj[2] + acc[2]), og = sigmoid_f(pj[3] + acc[3]);
+        const float c = fg * a.c[j] + ig * gg;
+        const float h = og * tanhf(c);
+        a.c[j] = c;
+        a.h_next[j] = h;
+        a.out[(size_t)j * a.T + a.t] = a.skip ? h + a.skip[(size_t)j * a.T + a.t] : h;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_rvq_decode(const float* embed, const int32_t* codes, int n_q, int bins,
                                                     int dim, int frames, float* latent) {
     const int i = blockIdx.x * 256 + threadIdx.x;
@@ -213,7 +260,14 @@ void launch_conv_transpose1d(const ConvTArgs& a, hipStream_t s) {
 }
 
 void launch_lstm_step(const LstmStepArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_lstm_step, dim3((a.H + 7) / 8), dim3(256), sizeof(float) * (size_t)a.H, s, a);
+    const size_t lds = sizeof(float) * (size_t)a.H;
+    switch (a.H % 256 ? 0 : a.H / 256) {
+    case 1: hipLaunchKernelGGL(k_lstm_step_w<1>, dim3(a.H / 4), dim3(256), lds, s, a); break;
+    case 2: hipLaunchKernelGGL(k_lstm_step_w<2>, dim3(a.H / 4), dim3(256), lds, s, a); break;
+    case 4: hipLaunchKernelGGL(k_lstm_step_w<4>, dim3(a.H / 4), dim3(256), lds, s, a); break;
+    case 8: hipLaunchKernelGGL(k_lstm_step_w<8>, dim3(a.H / 4), dim3(256), lds, s, a); break;
+    default: hipLaunchKernelGGL(k_lstm_step, dim3((a.H + 7) / 8), dim3(256), lds, s, a); break;
+    }
 }
 
 void launch_rvq_decode(const float* embed, const int32_t* codes, int n_q, int bins, int dim, int frames,

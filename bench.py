@@ -196,12 +196,87 @@ def serve_bench(mgx):
     }), flush=True)
 
 
+def t5_bench(mgx, reps, cpu):
+    """The T5-base encoder (12 layers, 768 wide, F16 weights as tools/convert_t5.py writes them)
+    over a 24-token prompt: encodes per second with the weights resident, against the oracle's
+    CPU restatement of the same encode."""
+    from mgx import synth
+    m = synth.SyntheticT5("t5-base", 1, seed=1)
+    ids = synth.synth_ids(1, 24, m.config.vocab)
+    t5 = mgx.T5(m.config, m.tensors)
+    for _ in range(3):
+        t5.encode(ids)
+    hip_sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        t5.encode(ids)
+    el = time.perf_counter() - t0
+    out = {"metric": "T5-base encodes/sec, 24-token prompt, F16", "value": round(reps / el, 3), "unit": "encodes/s",
+           "n_gpus": 1, "steps": reps, "warmup": 3, "ms_per_step": round(1000 * el / reps, 4),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16xf32",
+           "data": "synthetic (seeded random weights and token ids)",
+           "config": {"workload": "T5-base encoder, 12 layers, dim 768, 12 heads, FFN 3072, vocab 32128, F16, "
+                                  "24 tokens, weights resident", "parallelism": "single GPU"}}
+    if cpu:
+        from oracle import cpu_ref as R
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+        R.set_threads(threads)
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < 10.0:
+            R.t5_encode(m.config, m.tensors, ids)
+            n += 1
+        el = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(n / el, 3), "unit": "encodes/s", "cores": R.lib().ref_get_threads(),
+                               "kind": "port", "sample": f"oracle CPU restatement, {n} encodes of the same prompt "
+                                                          f"({el:.1f} s)"}
+    t5.close()
+    print(json.dumps(out), flush=True)
+
+
+def codec_bench(mgx, reps, cpu):
+    """The EnCodec 32 kHz decoder over 1500 frames (30 s of audio): seconds of audio decoded per
+    second, codes on the host to audio on the host, against the float64 oracle on a bounded
+    sample."""
+    from mgx import synth
+    m = synth.SyntheticCodec("encodec-32k", seed=1)
+    frames = 1500
+    codes = m.codes(2, frames)
+    k = mgx.Codec(m.config, m.tensors)
+    k.decode(codes)
+    hip_sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        k.decode(codes)
+    el = time.perf_counter() - t0
+    audio_s = frames / m.config["frame_rate"]
+    out = {"metric": "EnCodec 32 kHz decode, seconds of audio per second", "value": round(reps * audio_s / el, 3),
+           "unit": "audio s/s", "n_gpus": 1, "steps": reps, "warmup": 1, "ms_per_step": round(1000 * el / reps, 3),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+           "data": "synthetic (seeded random weights and codes)",
+           "config": {"workload": "EnCodec 32 kHz decoder (ratios 8,5,4,4, 64 filters, 2-layer LSTM 1024, 4 x 2048 "
+                                  "codebooks), 1500 frames = 30 s, codes to audio", "parallelism": "single GPU"}}
+    if cpu:
+        from oracle import codec_ref as K
+        n = 100
+        t0 = time.perf_counter()
+        K.decode_codes(m.config, m.weights, codes[:, :n])
+        el = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(n / m.config["frame_rate"] / el, 4), "unit": "audio s/s",
+                               "cores": os.cpu_count(), "kind": "port",
+                               "sample": f"float64 numpy oracle (numpy's BLAS threads), {n} frames = "
+                                         f"{n / m.config['frame_rate']:.0f} s of audio ({el:.1f} s)"}
+    k.close()
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1500)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="medium-q8", choices=sorted(WORKLOADS) + ["server-medium-q8"])
+    ap.add_argument("--workload", default="medium-q8",
+                    choices=sorted(WORKLOADS) + ["server-medium-q8", "t5-base", "encodec-decode"])
     ap.add_argument("--profile-every", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -217,6 +292,12 @@ def main():
     import mgx
     if args.workload == "server-medium-q8":
         serve_bench(mgx)
+        return
+    if args.workload == "t5-base":
+        t5_bench(mgx, args.steps if args.steps != 1500 else 200, not args.no_cpu)
+        return
+    if args.workload == "encodec-decode":
+        codec_bench(mgx, args.steps if args.steps != 1500 else 5, not args.no_cpu)
         return
     w = dict(WORKLOADS[args.workload])
     if args.prompt is not None:
