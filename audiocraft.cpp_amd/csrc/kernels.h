@@ -73,6 +73,7 @@ struct GemvArgs {
     int dim, heads, cap;
     const int* pos;       // QKV: [request] device positions; column n belongs to request n >> cshift
     int cshift;
+    int kv_cols;          // QKV: 0, or the cache column count when columns share caches (column n -> n % kv_cols)
     ActBuf dst;           // GELU_ACT destination
     float* dst_f;         // GELU_ACT: optional f32 copy [col][dst.stride] (an adapted consumer's A x reads it)
     // optional adapter on this projection (lora.h:50-83): y = Wx + s*B(Ax), DoRA rows scale
@@ -100,6 +101,7 @@ struct AttnArgs {
     float scale;
     const int* pos;       // [request] device positions: column n attends keys [0, pos[n >> cshift]]
     int cshift;
+    int kv_cols;          // 0, or the cache column count when columns share caches (column n -> n % kv_cols)
     ActBuf out;           // the out-projection's activation
     float* out_f;         // optional f32 copy [col][dim] (an adapted out-projection's A x reads it)
     unsigned long long* stamp;   // optional [64][2]: scores' earliest starts, reduce's latest ends
@@ -177,6 +179,8 @@ void launch_sample(const SampleArgs& a, hipStream_t s);
 // live set only live requests advance, and one whose next offset would reach par.steps
 // retires (live 0, position 0).
 void launch_advance(int* pos, int* live, const ReqParams* par, int n_req, hipStream_t s);
+// pos[r] = p0 + r for r < n (n <= 64): the positions of a multi-position prefill group.
+void launch_set_positions(int* pos, int n, int p0, hipStream_t s);
 // Opens request r of a slotted batch: position 0, live, its parameters and conditioning length.
 void launch_slot_open(int* pos, int* live, ReqParams* par, int* nc, int r, const ReqParams& p, int n_ctx,
                       hipStream_t s);

@@ -134,6 +134,13 @@ __device__ __forceinline__ size_t bm_off(int col, int i) {
     return (size_t)(i >> 5) * 512 + ((i >> 3) & 3) * 128 + col * 8 + (i & 7);
 }
 
+// The KV-cache column a QKV launch's column n appends to: its own column in the caller's
+// numbering, or that modulo kv_cols when several columns share caches (a multi-position prefill).
+__device__ __forceinline__ int kv_col(const GemvArgs& a, int n) {
+    const int c = a.col0 + n;
+    return a.kv_cols ? c % a.kv_cols : c;
+}
+
 // Writes element i (of a column) in the activation form the consumer's weights want.
 __device__ __forceinline__ void put_act(const ActBuf& a, int col, int i, float v, int lane) {
     if (a.kind == ACT_Q8 && a.bm)
@@ -725,7 +732,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
         else {
             const int sec = row / a.dim, wi = row - sec * a.dim, head = wi >> 6, dm = wi & 63;
             if (sec == 0) a.y[(size_t)n * a.dim + wi] = r;
-            else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + a.pos[(a.col0 + n) >> a.cshift]) * 64 + dm] = r;
+            else (sec == 1 ? a.k : a.v)[(((size_t)kv_col(a, n) * a.heads + head) * a.cap + a.pos[(a.col0 + n) >> a.cshift]) * 64 + dm] = r;
         }
     }
 }
@@ -784,7 +791,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
     const int u = a.pos[n >> a.cshift] + 1;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, t = lane & 15;
     const size_t head = (size_t)n * a.heads + h;
-    const float* K = a.k + head * a.cap * 64;
+    const float* K = a.k + ((size_t)(a.kv_cols ? n % a.kv_cols : n) * a.heads + h) * a.cap * 64;
     float* S = a.scores + head * a.cap;
     __shared__ float red_f[4];
     const float4 q = ((const float4*)(a.q + (size_t)n * a.dim + h * 64))[t];
@@ -848,7 +855,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_attn_pv(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < NCH * ATT_SUBS; ++i) cm[i] = a.cmax[head * a.max_chunks * ATT_SUBS + i];
     const int g = (wave & 3) * 4 + (lane >> 4), dq = lane & 15;
-    const float* V = a.v + head * a.cap * 64;
+    const float* V = a.v + ((size_t)(a.kv_cols ? n % a.kv_cols : n) * a.heads + h) * a.cap * 64;
     float4 vv[16];
     const int u = a.pos[n >> a.cshift] + 1;
     if (wave < 4) {
@@ -1322,6 +1329,13 @@ void launch_embed(const EmbedArgs& a, hipStream_t s) {
 void launch_advance(int* pos, int* live, const ReqParams* par, int n_req, hipStream_t s) {
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, pos, live, par, n_req);
 }
+__global__ __launch_bounds__(64) void k_set_positions(int* pos, int n, int p0) {
+    const int r = threadIdx.x;
+    if (r < n) pos[r] = p0 + r;
+}
+void launch_set_positions(int* pos, int n, int p0, hipStream_t s) {
+    hipLaunchKernelGGL(k_set_positions, dim3(1), dim3(64), 0, s, pos, n, p0);
+}
 void launch_slot_open(int* pos, int* live, ReqParams* par, int* nc, int r, const ReqParams& p, int n_ctx,
                       hipStream_t s) {
     hipLaunchKernelGGL(k_slot_open, dim3(1), dim3(64), 0, s, pos, live, par, nc, r, p, n_ctx);
@@ -1514,7 +1528,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
             else {
                 const int sec = row / a.dim, wi = row - sec * a.dim, head = wi >> 6, dm = wi & 63;
                 if (sec == 0) a.y[(size_t)n * a.dim + wi] = y;
-                else (sec == 1 ? a.k : a.v)[(((size_t)n * a.heads + head) * a.cap + a.pos[(a.col0 + n) >> a.cshift]) * 64 + dm] = y;
+                else (sec == 1 ? a.k : a.v)[(((size_t)kv_col(a, n) * a.heads + head) * a.cap + a.pos[(a.col0 + n) >> a.cshift]) * 64 + dm] = y;
             }
         }
     }
@@ -1647,9 +1661,7 @@ void launch_gemv(const GemvArgs& a0, hipStream_t s) {
             if (a0.ad_ax) a.ad_ax = a0.ad_ax + (size_t)c0 * a0.ad_rank;
             a.col0 = a0.col0 + c0;
             if (a0.epi == EPI_QKV) {
-                a.y = a0.y + (size_t)c0 * a0.dim;
-                a.k = a0.k + (size_t)c0 * a0.heads * a0.cap * 64;
-                a.v = a0.v + (size_t)c0 * a0.heads * a0.cap * 64;
+                a.y = a0.y + (size_t)c0 * a0.dim;   // the caches stay: the epilogue maps col0 + n
             } else if (a0.y) {
                 a.y = a0.y + (size_t)c0 * a0.y_stride;
             }

@@ -124,10 +124,16 @@ struct mgx_stream {
     std::vector<Mark> marks;
     unsigned long long* stamps = nullptr;
     double clock_khz = 0.0;
+    // A prefill view (make_prefill_view) borrows the caches, the memory, the sinusoid table and
+    // the HIP stream of the stream it serves: columns map to caches modulo kv_cols and every
+    // request reads memory 0.
+    int kv_cols = 0;
+    bool shared_mem = false, owns_hs = true;
+    int mem_reqs = 0;                        // requests the cross K / V hold (n_req unless a view)
     ~mgx_stream() {
         if (hs) (void)hipStreamSynchronize(hs);
         mem.release();
-        if (hs) (void)hipStreamDestroy(hs);
+        if (hs && owns_hs) (void)hipStreamDestroy(hs);
         if (m) m->live.fetch_sub(1);
     }
     // the next timing slot, or null when profiling is off or the slots are used up
@@ -136,7 +142,9 @@ struct mgx_stream {
         marks.push_back({(int)marks.size(), kind, bytes});
         return stamps + 2 * 64 * (size_t)marks.back().slot;
     }
-    size_t layer_kv() const { return (size_t)n_seq * m->c.heads * kv_rows * 64; }
+    // one layer's K (or V) cache: every cache column's heads x rows (a prefill view's columns
+    // share the kv_cols caches of the stream it serves)
+    size_t layer_kv() const { return (size_t)(kv_cols ? kv_cols : n_seq) * m->c.heads * kv_rows * 64; }
     void alloc_act(ActStore& a, int cols, int stride) {
         if (n_seq >= 3) cols = std::max(cols, 16);   // block-major Q8 has 16 column slots
         a.stride = stride;
@@ -249,10 +257,10 @@ bool mf_src(const mgx::DevMat& w, int ncol, int epi) {
 int att_chunks(int position) { return position / mgx::ATT_CHUNK + 1; }
 
 void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int ids_req_stride, bool heads,
-          const mgx::SampleArgs* sample, int position) {
+          const mgx::SampleArgs* sample, int position, int ncol = 0) {
     const mgx_model* m = s->m;
     const mgx_lm_config& c = m->c;
-    const int N = s->n_seq, D = c.dim, R = s->n_req;
+    const int N = ncol > 0 ? ncol : s->n_seq, D = c.dim, R = N / s->cpr;
     mgx::EmbedArgs e{};
     for (int q = 0; q < c.n_q; ++q) e.emb[q] = m->emb[q];
     e.n_q = c.n_q; e.ids = ids; e.ids_stride = ids_stride; e.ids_base = ids_base; e.table = s->table;
@@ -271,14 +279,14 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
             mgx::GemvArgs a = ga(L.w[P_QKV], N);
             pro_ln(a, s->x, D, L.n1w, L.n1b, c.norm_eps);
             a.epi = mgx::EPI_QKV; a.y = s->qb; a.k = Kl; a.v = Vl; a.dim = D; a.heads = c.heads; a.cap = s->kv_rows;
-            a.pos = s->dpos; a.cshift = s->cshift;
+            a.pos = s->dpos; a.cshift = s->cshift; a.kv_cols = s->kv_cols;
             gemv_ad(s, a, L.ad[P_QKV]);
         }
         {
             mgx::AttnArgs at{};
             at.q = s->qb; at.k = Kl; at.v = Vl; at.scores = s->scores; at.opart = s->opart; at.cmax = s->cmax;
             at.dim = D; at.heads = c.heads; at.cap = s->kv_rows; at.max_chunks = s->max_chunks; at.ncol = N;
-            at.scale = scale; at.pos = s->dpos; at.cshift = s->cshift; at.out = s->act_o.view(L.w[P_OUT].type, bo);
+            at.scale = scale; at.pos = s->dpos; at.cshift = s->cshift; at.kv_cols = s->kv_cols; at.out = s->act_o.view(L.w[P_OUT].type, bo);
             at.out_f = L.ad[P_OUT] ? s->act_o.f : nullptr;
             // f32 K and V of every key attended, every stream
             at.stamp = s->stamp_slot(PROF_ATTN, 2.0 * N * c.heads * (position + 1) * 64 * 4);
@@ -293,7 +301,7 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
         // cross-attention, each request's conditional stream only (the null stream's
         // contribution is exactly 0): column r * cpr of x
         if (s->cross) {
-            const size_t xl = (size_t)l * R * c.heads * s->n_ctx * 64;
+            const size_t xl = (size_t)l * s->mem_reqs * c.heads * s->n_ctx * 64;
             mgx::GemvArgs a = ga(L.w[P_CQ], R);
             pro_ln(a, s->x, s->cpr * D, L.ncw, L.ncb, c.norm_eps);
             epi_store(a, s->qc, D);
@@ -301,6 +309,7 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
             mgx::XAttnArgs xa{};
             xa.q = s->qc; xa.k = s->xk + xl; xa.v = s->xv + xl; xa.n_ctx = s->n_ctx; xa.dim = D; xa.scale = scale;
             xa.nc = s->dnc;
+            xa.shared_kv = s->shared_mem ? 1 : 0;
             xa.out = s->act_c.view(L.w[P_COUT].type, bc);
             xa.out_f = L.ad[P_COUT] ? s->act_c.f : nullptr;
             mgx::launch_xattn(xa, c.heads, R, s->hs);
@@ -421,7 +430,7 @@ void make_stream(mgx_model* m, int capacity, int n_seq, int n_req, const float* 
     s->m = m;
     m->live.fetch_add(1);
     s->cap = capacity; s->n_seq = n_seq; s->cross = cross ? 1 : 0; s->n_ctx = cross ? n_ctx : 0;
-    s->n_req = n_req; s->cpr = n_seq / n_req;
+    s->n_req = n_req; s->cpr = n_seq / n_req; s->mem_reqs = n_req;
     // one request: every column (at most 16) maps to 0; batches have 1 or 2 columns a request
     if (n_req > 1 && s->cpr > 2) throw Error(MGX_ERR_INVALID, "at most 2 streams per request");
     s->cshift = n_req == 1 ? 4 : s->cpr - 1;
@@ -465,6 +474,43 @@ void make_stream(mgx_model* m, int capacity, int n_seq, int n_req, const float* 
     HIP_OK(hipGetLastError());
     HIP_OK(hipStreamSynchronize(s->hs));
     *out = s.release();
+}
+
+}  // namespace
+
+namespace {
+
+// A view of single-request stream `main` that runs `g` prompt positions at once: g * cpr columns,
+// column r * cpr + s is stream s at position dpos[r], appending to and attending main's caches
+// (kv_cols = cpr) and reading main's memory. Only the per-column working buffers are its own.
+std::unique_ptr<mgx_stream> make_prefill_view(mgx_stream* main, int g) {
+    const mgx_model* m = main->m;
+    const mgx_lm_config& c = m->c;
+    if (main->n_req != 1) throw Error(MGX_ERR_INVALID, "internal: a prefill view serves one request");
+    const int cpr = main->cpr, n_seq = g * cpr;
+    if (g < 2 || n_seq > 16) throw Error(MGX_ERR_INVALID, "internal: a prefill view has 2 to 16 columns");
+    auto s = std::make_unique<mgx_stream>();
+    s->m = main->m;
+    s->m->live.fetch_add(1);
+    s->cap = main->cap; s->n_seq = n_seq; s->cross = main->cross; s->n_ctx = main->n_ctx;
+    s->n_req = g; s->cpr = cpr; s->cshift = cpr - 1; s->mem_reqs = main->mem_reqs;
+    s->max_chunks = main->max_chunks; s->kv_rows = main->kv_rows;
+    s->hs = main->hs; s->owns_hs = false;
+    s->K = main->K; s->V = main->V; s->xk = main->xk; s->xv = main->xv; s->table = main->table;
+    s->kv_cols = cpr; s->shared_mem = true;
+    s->dpos = s->mem.alloc<int>((size_t)g);
+    s->cmax = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * mgx::ATT_SUBS);
+    s->x = s->mem.alloc<float>((size_t)n_seq * c.dim);
+    s->qb = s->mem.alloc<float>((size_t)n_seq * c.dim);
+    s->scores = s->mem.alloc<float>((size_t)n_seq * c.heads * s->kv_rows);
+    s->opart = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * 64);
+    s->qc = s->mem.alloc<float>((size_t)g * c.dim);
+    s->alloc_act(s->act_o, n_seq, c.dim);
+    s->alloc_act(s->act_c, g, c.dim);
+    s->alloc_act(s->act_f, n_seq, c.ff_dim);
+    s->alloc_act(s->act_ln, n_seq, c.dim);
+    if (m->ad_rank_max > 0) s->ax = s->mem.alloc<float>((size_t)n_seq * m->ad_rank_max);
+    return s;
 }
 
 }  // namespace
@@ -704,6 +750,9 @@ void mgx_stream_destroy(mgx_stream* s) { delete s; }
 struct mgx_session {
     mgx_model* m = nullptr;
     std::unique_ptr<mgx_stream> s;
+    // Single-request sessions run the prompt positions before the loop's first forward in groups
+    // (the prefill view: up to 16 columns, 8 positions of a guided pair, 16 unguided).
+    std::unique_ptr<mgx_stream> pf;
     DevArena mem;
     int R = 1, K = 0, T = 0, S = 0, start = 0, next = 0;   // next: the next loop offset to run
     bool guided = false;
@@ -810,6 +859,7 @@ void session_create(mgx_model* m, const mgx_batch_request* reqs, int R, int32_t 
     make_stream(m, S, R * (ss->guided ? 2 : 1), R, t5s.data(), n_ctx, ss->guided ? 1 : 0, &raw);
     ss->s.reset(raw);
     mgx_stream* st = ss->s.get();
+    if (R == 1 && start - 1 >= 2) ss->pf = make_prefill_view(st, std::min(16 / st->cpr, start - 1));
     ss->dseq = ss->mem.alloc<int32_t>(ss->seq.size());
     uint8_t* dmask = ss->mem.alloc<uint8_t>(mask.size());
     mgx::ReqParams* dpar = ss->mem.alloc<mgx::ReqParams>(par.size());
@@ -871,7 +921,19 @@ int session_step(mgx_session* ss, int n) {
         const int offset = ss->next++;
         const bool profiled = ss->prof_every > 0 && (offset - ss->start) % ss->prof_every == 0;
         if (offset == ss->start) {
-            for (int pos = 0; pos < ss->start - 1; ++pos) run_position(ss, false, false, pos);
+            if (ss->pf) {
+                // prompt positions g at a time (causal: each column attends keys up to its own
+                // position, all appended by the same launch), then the loop's first forward
+                const int G = ss->pf->n_req;
+                for (int p0 = 0; p0 < ss->start - 1; p0 += G) {
+                    const int g = std::min(G, ss->start - 1 - p0);
+                    mgx::launch_set_positions(ss->pf->dpos, g, p0, s->hs);
+                    step(ss->pf.get(), ss->dseq, ss->S, 0, 0, false, nullptr, p0 + g - 1, g * ss->pf->cpr);
+                }
+                mgx::launch_set_positions(s->dpos, 1, ss->start - 1, s->hs);
+            } else {
+                for (int pos = 0; pos < ss->start - 1; ++pos) run_position(ss, false, false, pos);
+            }
             run_position(ss, true, false, ss->start - 1);
             HIP_OK(hipGetLastError());
             HIP_OK(hipStreamSynchronize(s->hs));

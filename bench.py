@@ -333,6 +333,7 @@ def main():
     attn = [0.0, 0.0, 0]
     warm_left = args.warmup
     sess = None
+    prefill_s = []
     while timed_steps < args.steps:
         if sess is None or sess.remaining() == 0:
             if sess is not None:
@@ -342,8 +343,12 @@ def main():
                 sess.close()
             sess = mgx.Batch(gm, reqs, w["prompt"]) if R > 1 else mgx.Session(gm, t5, prompt, w["prompt"],
                                                                                reqs[0]["params"])
-            sess.step(1)                                   # prefill, untimed
-            print(f"[bench] session prefilled ({start} tokens x {R} requests)", file=sys.stderr, flush=True)
+            hip_sync()
+            tp = time.perf_counter()
+            sess.step(1)                                   # prefill, outside the timed steps
+            prefill_s.append(time.perf_counter() - tp)
+            print(f"[bench] session prefilled ({start} tokens x {R} requests) in {prefill_s[-1]:.3f} s",
+                  file=sys.stderr, flush=True)
         if warm_left > 0:
             warm_left -= sess.step(min(warm_left, sess.remaining()))
             continue
@@ -395,6 +400,8 @@ def main():
                      "avg_launch_us": round(1000.0 * gemv[0] / max(gemv[2], 1), 3)},
         "attention": {"achieved": round(attn_gbs, 1), "unit": "GB/s", "launches_timed": attn[2],
                       "avg_launch_us": round(1000.0 * attn[0] / max(attn[2], 1), 3)},
+        # the prompt's prefill (the loop's first forward, start tokens), outside `value`
+        "prefill_ms": round(1000.0 * min(prefill_s), 2) if prefill_s else None,
     }
     if not args.no_cpu:
         try:
