@@ -130,7 +130,9 @@ struct mgx_stream {
     int kv_cols = 0;
     bool shared_mem = false, owns_hs = true;
     int mem_reqs = 0;                        // requests the cross K / V hold (n_req unless a view)
+    std::unique_ptr<mgx_stream> pf;          // this stream's prefill view, once a prefill used one
     ~mgx_stream() {
+        pf.reset();                          // it runs on this stream's hs
         if (hs) (void)hipStreamSynchronize(hs);
         mem.release();
         if (hs && owns_hs) (void)hipStreamDestroy(hs);
@@ -488,12 +490,14 @@ std::unique_ptr<mgx_stream> make_prefill_view(mgx_stream* main, int g) {
     const mgx_lm_config& c = m->c;
     if (main->n_req != 1) throw Error(MGX_ERR_INVALID, "internal: a prefill view serves one request");
     const int cpr = main->cpr, n_seq = g * cpr;
-    if (g < 2 || n_seq > 16) throw Error(MGX_ERR_INVALID, "internal: a prefill view has 2 to 16 columns");
+    if (g < 2 || n_seq > 16 || (cpr & (cpr - 1))) throw Error(MGX_ERR_INVALID, "internal: bad prefill view shape");
     auto s = std::make_unique<mgx_stream>();
     s->m = main->m;
     s->m->live.fetch_add(1);
     s->cap = main->cap; s->n_seq = n_seq; s->cross = main->cross; s->n_ctx = main->n_ctx;
-    s->n_req = g; s->cpr = cpr; s->cshift = cpr - 1; s->mem_reqs = main->mem_reqs;
+    s->n_req = g; s->cpr = cpr; s->mem_reqs = main->mem_reqs;
+    s->cshift = 0;
+    while ((1 << s->cshift) < cpr) ++s->cshift;   // log2(cpr): 1, 2, 4 or 8 streams
     s->max_chunks = main->max_chunks; s->kv_rows = main->kv_rows;
     s->hs = main->hs; s->owns_hs = false;
     s->K = main->K; s->V = main->V; s->xk = main->xk; s->xv = main->xv; s->table = main->table;
@@ -511,6 +515,26 @@ std::unique_ptr<mgx_stream> make_prefill_view(mgx_stream* main, int g) {
     s->alloc_act(s->act_ln, n_seq, c.dim);
     if (m->ad_rank_max > 0) s->ax = s->mem.alloc<float>((size_t)n_seq * m->ad_rank_max);
     return s;
+}
+
+// Runs positions first .. first + count - 1 of single-request stream s without heads (the
+// positions of a prefill before its last), 16 / cpr at a time through s's prefill view: each
+// column at its own position, causal by key count, all of a group's K / V appended by the same
+// launch before any column attends. Leaves s's device position at first + count. Returns false,
+// running nothing, when a view cannot serve s: several requests, or a stream count that is not
+// 1, 2, 4 or 8 (a view's column n is at position n >> log2(streams)).
+bool run_prefill(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int first, int count) {
+    if (s->n_req != 1 || s->cpr > 8 || (s->cpr & (s->cpr - 1)) || count < 2) return false;
+    if (!s->pf) s->pf = make_prefill_view(s, 16 / s->cpr);
+    mgx_stream* pf = s->pf.get();
+    const int G = pf->n_req;
+    for (int p0 = 0; p0 < count; p0 += G) {
+        const int g = std::min(G, count - p0);
+        mgx::launch_set_positions(pf->dpos, g, first + p0, s->hs);
+        step(pf, ids, ids_stride, ids_base, 0, false, nullptr, first + p0 + g - 1, g * pf->cpr);
+    }
+    mgx::launch_set_positions(s->dpos, 1, first + count, s->hs);
+    return true;
 }
 
 }  // namespace
@@ -714,8 +738,12 @@ int mgx_forward(mgx_stream* s, const int32_t* ids, int32_t n_tokens, float* logi
         const int used = s->used;
         HIP_OK(hipMemcpyAsync(s->dpos, &used, sizeof(int), hipMemcpyHostToDevice, s->hs));
         // A prefill is the same per-position arithmetic as single steps (its causal mask only
-        // adds exact zeros), so the tokens run one position at a time.
-        for (int t = 0; t < n_tokens; ++t) step(s, s->ids, n_tokens, used, 0, t == n_tokens - 1, nullptr, used + t);
+        // adds exact zeros): the positions before the last run in groups of columns, the last
+        // (the only one whose logits are read) as a single step.
+        if (run_prefill(s, s->ids, n_tokens, used, used, n_tokens - 1))
+            step(s, s->ids, n_tokens, used, 0, true, nullptr, used + n_tokens - 1);
+        else
+            for (int t = 0; t < n_tokens; ++t) step(s, s->ids, n_tokens, used, 0, t == n_tokens - 1, nullptr, used + t);
         HIP_OK(hipGetLastError());
         if (logits_out)
             HIP_OK(hipMemcpyAsync(logits_out, s->logits, sizeof(float) * (size_t)s->n_seq * c.n_q * c.card,
@@ -750,9 +778,6 @@ void mgx_stream_destroy(mgx_stream* s) { delete s; }
 struct mgx_session {
     mgx_model* m = nullptr;
     std::unique_ptr<mgx_stream> s;
-    // Single-request sessions run the prompt positions before the loop's first forward in groups
-    // (the prefill view: up to 16 columns, 8 positions of a guided pair, 16 unguided).
-    std::unique_ptr<mgx_stream> pf;
     DevArena mem;
     int R = 1, K = 0, T = 0, S = 0, start = 0, next = 0;   // next: the next loop offset to run
     bool guided = false;
@@ -859,7 +884,7 @@ void session_create(mgx_model* m, const mgx_batch_request* reqs, int R, int32_t 
     make_stream(m, S, R * (ss->guided ? 2 : 1), R, t5s.data(), n_ctx, ss->guided ? 1 : 0, &raw);
     ss->s.reset(raw);
     mgx_stream* st = ss->s.get();
-    if (R == 1 && start - 1 >= 2) ss->pf = make_prefill_view(st, std::min(16 / st->cpr, start - 1));
+    if (R == 1 && start - 1 >= 2) st->pf = make_prefill_view(st, 16 / st->cpr);
     ss->dseq = ss->mem.alloc<int32_t>(ss->seq.size());
     uint8_t* dmask = ss->mem.alloc<uint8_t>(mask.size());
     mgx::ReqParams* dpar = ss->mem.alloc<mgx::ReqParams>(par.size());
@@ -921,19 +946,10 @@ int session_step(mgx_session* ss, int n) {
         const int offset = ss->next++;
         const bool profiled = ss->prof_every > 0 && (offset - ss->start) % ss->prof_every == 0;
         if (offset == ss->start) {
-            if (ss->pf) {
-                // prompt positions g at a time (causal: each column attends keys up to its own
-                // position, all appended by the same launch), then the loop's first forward
-                const int G = ss->pf->n_req;
-                for (int p0 = 0; p0 < ss->start - 1; p0 += G) {
-                    const int g = std::min(G, ss->start - 1 - p0);
-                    mgx::launch_set_positions(ss->pf->dpos, g, p0, s->hs);
-                    step(ss->pf.get(), ss->dseq, ss->S, 0, 0, false, nullptr, p0 + g - 1, g * ss->pf->cpr);
-                }
-                mgx::launch_set_positions(s->dpos, 1, ss->start - 1, s->hs);
-            } else {
+            // prompt positions in groups, then the loop's first forward (one position at a time
+            // through the captured body steps where a group cannot serve: batches of requests)
+            if (!run_prefill(s, ss->dseq, ss->S, 0, 0, ss->start - 1))
                 for (int pos = 0; pos < ss->start - 1; ++pos) run_position(ss, false, false, pos);
-            }
             run_position(ss, true, false, ss->start - 1);
             HIP_OK(hipGetLastError());
             HIP_OK(hipStreamSynchronize(s->hs));
