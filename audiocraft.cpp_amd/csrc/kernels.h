@@ -21,9 +21,10 @@ constexpr int MAX_CARD = 2048;   // sampler's LDS rows
 
 // A weight matrix in device layout: `out` rows of `in`. Q8_0: int8 q[out][in] + fp16
 // d[out][in/32]; Q4_0: the 16 nibble bytes of each block q[out][in/2] + d; F16 / F32: q only.
-// For the matrix-core GEMV (Q8_0, or null): dt, the scales tile-transposed [out/16][in/32][16];
-// qm, the quants again in operand order [out/16][in/32][64 lanes][8]: lane 16g + c holds row
-// 16 * tile + c, bytes 8g..8g+7 of the block -- one wave load is 512 contiguous bytes.
+// For the matrix-core GEMV (Q8_0 and Q4_0, or null): dt, the scales tile-transposed
+// [out/16][in/32][16]; qm, the quants again in operand order [out/16][in/32][64 lanes][8 or 4
+// bytes]: lane 16g + c holds row 16 * tile + c, elements 8g..8g+7 of the block (Q4_0: byte m
+// holds element 8g + m in its low nibble and 8g + m + 4 in its high one).
 struct DevMat {
     int type, in, out;
     const void* q;
@@ -168,6 +169,8 @@ void launch_act_prep(const GemvArgs& a, hipStream_t s);
 // dt from d, and qm from q, for a Q8_0 matrix (out a multiple of 16)
 void launch_scales_t(const DevMat& w, uint16_t* dt, hipStream_t s);
 void launch_weights_mf(const DevMat& w, int8_t* qm, hipStream_t s);
+// the Q4_0 operand-order copy (one word of 8 nibbles per lane and block) for a Q4_0 matrix
+void launch_weights_mf4(const DevMat& w, uint32_t* qm, hipStream_t s);
 // nch: the 256-key chunks of the position the launch runs at (the grid covers exactly these)
 void launch_attention(const AttnArgs& a, int nch, hipStream_t s);
 void launch_xattn(const XAttnArgs& a, int heads, int n_req, hipStream_t s);

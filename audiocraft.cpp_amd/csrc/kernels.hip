@@ -1375,7 +1375,26 @@ __host__ __device__ constexpr int bitrev(int j) {
 template <int N>
 __host__ __device__ constexpr int ilog2() { return N <= 1 ? 0 : 1 + ilog2<N / 2>(); }
 
-template <int NB, int KW, int TILES, int EPI>
+// One lane's A operand (16 rows x 32 of a block: row lane % 16, elements 8 (lane / 16) .. + 7).
+// Q8_0: the 8 quants. Q4_0: one word whose byte m holds element m (low nibble) and element m + 4
+// (high nibble), unpacked to int8 nib - 8 per byte ((x + 0x78) ^ 0x80 never carries out of a byte).
+template <int WT> struct MfW;
+template <> struct MfW<T_Q8_0> {
+    using T = uint2;
+    static __device__ __forceinline__ T load(const int8_t* qm, size_t i) { return ((const uint2*)qm)[i]; }
+    static __device__ __forceinline__ long op(T w) { return (long)(((unsigned long long)w.y << 32) | w.x); }
+};
+template <> struct MfW<T_Q4_0> {
+    using T = uint32_t;
+    static __device__ __forceinline__ T load(const int8_t* qm, size_t i) { return ((const uint32_t*)qm)[i]; }
+    static __device__ __forceinline__ long op(T w) {
+        const uint32_t lo = ((w & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+        const uint32_t hi = (((w >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+        return (long)(((unsigned long long)hi << 32) | lo);
+    }
+};
+
+template <int WT, int NB, int KW, int TILES, int EPI>
 __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     constexpr int M = 64 / KW;                        // leaves (partials) per wave
     constexpr int LB = ilog2<M>();
@@ -1395,7 +1414,8 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     const int8_t* Wm = a.w.qm;
     // 1. every load of the wave, in visiting order (a leaf's weights, activations and scales
     //    together, so its products can start while later leaves are still loading)
-    uint2 wa[TILES][M][S], xb[M][S], dw[TILES][M][S];
+    typename MfW<WT>::T wa[TILES][M][S];
+    uint2 xb[M][S], dw[TILES][M][S];
     float xd[M][S];
 #pragma unroll
     for (int j = 0; j < M; ++j) {
@@ -1406,7 +1426,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
             const int b = w + KW * i + 64 * s;
 #pragma unroll
             for (int t = 0; t < TILES; ++t)
-                wa[t][j][s] = *(const uint2*)(Wm + (((size_t)(row0 / 16 + t) * NB + b) * 64 + lane) * 8);
+                wa[t][j][s] = MfW<WT>::load(Wm, ((size_t)(row0 / 16 + t) * NB + b) * 64 + lane);
             xb[j][s] = *(const uint2*)(x.q + ((size_t)b * 64 + lane) * 8);
             xd[j][s] = x.d[(size_t)b * 16 + c16];
 #pragma unroll
@@ -1449,7 +1469,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
                 for (int t = 0; t < TILES; ++t) {
                     const mf_v4i z = {0, 0, 0, 0};
                     const mf_v4i r = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                        (long)(((unsigned long long)wa[t][j][s].y << 32) | wa[t][j][s].x),
+                        MfW<WT>::op(wa[t][j][s]),
                         (long)(((unsigned long long)xb[j][s].y << 32) | xb[j][s].x), z, 0, 0, 0);
                     const float dx = xd[j][s];
                     const float d0 = h2f((uint16_t)(dw[t][j][s].x & 0xffffu)) * dx;
@@ -1602,40 +1622,47 @@ static bool mf_width(int nb) {
 }
 bool gemv_mf_ok(const GemvArgs& a) {
     const int rows = a.epi == EPI_GELU_ACT ? 32 : 16;
-    return a.w.type == T_Q8_0 && a.w.dt && a.w.qm && a.pro == PRO_ACT && a.src.kind == ACT_Q8 && a.src.bm &&
+    return (a.w.type == T_Q8_0 || a.w.type == T_Q4_0) && a.w.dt && a.w.qm && a.pro == PRO_ACT && a.src.kind == ACT_Q8 &&
+           a.src.bm &&
            a.src.stride == a.w.in &&
-           a.ncol >= 3 && a.ncol <= 16 && a.w.in % 32 == 0 && mf_width(a.w.in / 32) && a.w.out % rows == 0 &&
+           a.ncol >= 3 && a.ncol <= 16 && a.w.in % 32 == 0 &&
+           (mf_width(a.w.in / 32) || (a.w.type == T_Q4_0 && a.w.in / 32 == 256)) && a.w.out % rows == 0 &&
            (a.epi != EPI_GELU_ACT || a.w.in <= 2048);
 }
-template <int NB, int KW, int TILES, int EPI> static void mf_go(const GemvArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((k_gemv_mf<NB, KW, TILES, EPI>), dim3(a.w.out / (16 * TILES)), dim3(64 * KW), 0, s, a);
+template <int WT, int NB, int KW, int TILES, int EPI> static void mf_go(const GemvArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((k_gemv_mf<WT, NB, KW, TILES, EPI>), dim3(a.w.out / (16 * TILES)), dim3(64 * KW), 0, s, a);
 }
-template <int NB, int KW> static void mf_epi(const GemvArgs& a, hipStream_t s) {
+template <int WT, int NB, int KW> static void mf_epi(const GemvArgs& a, hipStream_t s) {
     switch (a.epi) {
-    case EPI_STORE: mf_go<NB, KW, 1, EPI_STORE>(a, s); break;
-    case EPI_RESID: mf_go<NB, KW, 1, EPI_RESID>(a, s); break;
-    case EPI_QKV: mf_go<NB, KW, 1, EPI_QKV>(a, s); break;
-    default: if constexpr (NB <= 64) mf_go<NB, KW, 2, EPI_GELU_ACT>(a, s); break;
+    case EPI_STORE: mf_go<WT, NB, KW, 1, EPI_STORE>(a, s); break;
+    case EPI_RESID: mf_go<WT, NB, KW, 1, EPI_RESID>(a, s); break;
+    case EPI_QKV: mf_go<WT, NB, KW, 1, EPI_QKV>(a, s); break;
+    default: if constexpr (NB <= 64) mf_go<WT, NB, KW, 2, EPI_GELU_ACT>(a, s); break;
     }
 }
-template <int NB> static void mf_nb(const GemvArgs& a, hipStream_t s) {
-    // mf_kw gives 4 only below 128 blocks, 8 only at 128 / 192, 16 only when it divides NB
+template <int WT, int NB> static void mf_nb(const GemvArgs& a, hipStream_t s) {
+    // mf_kw gives 4 only below 128 blocks, 8 only at 128 and up, 16 only when it divides NB
     switch (mf_kw(NB, a.w.out / (a.epi == EPI_GELU_ACT ? 32 : 16))) {
-    case 4: if constexpr (NB < 128) mf_epi<NB, 4>(a, s); break;
-    case 8: if constexpr (NB == 128 || NB == 192) mf_epi<NB, 8>(a, s); break;
-    default: if constexpr (NB % 16 == 0) mf_epi<NB, 16>(a, s); break;
+    case 4: if constexpr (NB < 128) mf_epi<WT, NB, 4>(a, s); break;
+    case 8: if constexpr (NB >= 128) mf_epi<WT, NB, 8>(a, s); break;
+    default: if constexpr (NB % 16 == 0) mf_epi<WT, NB, 16>(a, s); break;
+    }
+}
+template <int WT> static void mf_wt(const GemvArgs& a, hipStream_t s) {
+    switch (a.w.in / 32) {
+    case 4: mf_nb<WT, 4>(a, s); break;
+    case 16: mf_nb<WT, 16>(a, s); break;
+    case 32: mf_nb<WT, 32>(a, s); break;
+    case 48: mf_nb<WT, 48>(a, s); break;
+    case 64: mf_nb<WT, 64>(a, s); break;
+    case 128: mf_nb<WT, 128>(a, s); break;
+    case 192: mf_nb<WT, 192>(a, s); break;
+    default: if constexpr (WT == T_Q4_0) mf_nb<WT, 256>(a, s); break;   // 4-bit weights: half the registers
     }
 }
 static void launch_gemv_mf(const GemvArgs& a, hipStream_t s) {
-    switch (a.w.in / 32) {
-    case 4: mf_nb<4>(a, s); break;
-    case 16: mf_nb<16>(a, s); break;
-    case 32: mf_nb<32>(a, s); break;
-    case 48: mf_nb<48>(a, s); break;
-    case 64: mf_nb<64>(a, s); break;
-    case 128: mf_nb<128>(a, s); break;
-    default: mf_nb<192>(a, s); break;
-    }
+    if (a.w.type == T_Q4_0) mf_wt<T_Q4_0>(a, s);
+    else mf_wt<T_Q8_0>(a, s);
 }
 
 void launch_gemv(const GemvArgs& a0, hipStream_t s) {
@@ -1926,6 +1953,28 @@ __global__ void k_weights_mf(const int8_t* q, int in, int out, int8_t* qm) {
 void launch_weights_mf(const DevMat& w, int8_t* qm, hipStream_t s) {
     const size_t n = (size_t)w.out * (w.in / 32) * 4;
     hipLaunchKernelGGL(k_weights_mf, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const int8_t*)w.q, w.in, w.out, qm);
+}
+// Q4_0 quants in operand order, one word per lane and block: byte m of lane (16g + r%16)'s word
+// holds element 8g + m of row r's block (low nibble) and element 8g + m + 4 (high nibble); the
+// device layout keeps ggml's block bytes (byte j: element j low, element j + 16 high).
+__global__ void k_weights_mf4(const uint8_t* qs, int in, int out, uint32_t* qm) {
+    const size_t u = (size_t)blockIdx.x * 256 + threadIdx.x;   // one 4-byte word
+    const int nb = in / 32;
+    if (u >= (size_t)out * nb * 4) return;
+    const int lanei = (int)(u & 63);
+    const size_t tb = u >> 6;
+    const int b = (int)(tb % nb), tile = (int)(tb / nb);
+    const int g = lanei >> 4, c = lanei & 15;
+    const uint8_t* blk = qs + (size_t)(tile * 16 + c) * (in / 2) + b * 16;
+    const auto nib = [&](int e) { return e < 16 ? (blk[e] & 15u) : (blk[e - 16] >> 4); };
+    uint32_t w = 0;
+    for (int m = 0; m < 4; ++m) w |= (nib(8 * g + m) | (nib(8 * g + m + 4) << 4)) << (8 * m);
+    qm[u] = w;
+}
+void launch_weights_mf4(const DevMat& w, uint32_t* qm, hipStream_t s) {
+    const size_t n = (size_t)w.out * (w.in / 32) * 4;
+    hipLaunchKernelGGL(k_weights_mf4, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint8_t*)w.q, w.in,
+                       w.out, qm);
 }
 void launch_scales_t(const DevMat& w, uint16_t* dt, hipStream_t s) {
     const int nb = w.in / 32;

@@ -608,14 +608,20 @@ int mgx_model_create(const mgx_lm_config* cfg, const mgx_tensor* t, int32_t n, m
         }
         // every Q8_0 projection's matrix-core copies: tile-transposed scales, operand-order quants
         auto with_dt = [&](mgx::DevMat& w) {
-            if (w.type != mgx::T_Q8_0 || w.out % 16 || w.in % 32) return;
+            if ((w.type != mgx::T_Q8_0 && w.type != mgx::T_Q4_0) || w.out % 16 || w.in % 32) return;
             uint16_t* dt = m->mem.alloc<uint16_t>((size_t)w.out * (w.in / 32));
-            int8_t* qm = m->mem.alloc<int8_t>((size_t)w.out * w.in);
             mgx::launch_scales_t(w, dt, s);
-            mgx::launch_weights_mf(w, qm, s);
+            if (w.type == mgx::T_Q8_0) {
+                int8_t* qm = m->mem.alloc<int8_t>((size_t)w.out * w.in);
+                mgx::launch_weights_mf(w, qm, s);
+                w.qm = qm;
+            } else {
+                uint32_t* qm = m->mem.alloc<uint32_t>((size_t)w.out * w.in / 8);
+                mgx::launch_weights_mf4(w, qm, s);
+                w.qm = (int8_t*)qm;
+            }
             HIP_OK(hipGetLastError());
             w.dt = dt;
-            w.qm = qm;
         };
         with_dt(m->heads);
         for (LayerW& L : m->L)
