@@ -601,7 +601,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
             ch[k] = *p;
         }
     }
-    if constexpr (PRO != PRO_ACT) __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PRO != PRO_ACT) {
+        // every wave's column loads enter the memory pipeline before any wave's weight loads
+        asm volatile("s_barrier" ::: "memory");
+    }
     // 2. weights
     WUnit<WT> w[U > 0 ? U : 1];
     if constexpr (U > 0) {
