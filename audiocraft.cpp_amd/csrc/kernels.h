@@ -18,6 +18,7 @@ constexpr int ATT_MAX_CHUNKS = 16;  // capacity up to 4096 positions
 constexpr int ATT_SUB = 64;         // keys per score block
 constexpr int ATT_SUBS = ATT_CHUNK / ATT_SUB;
 constexpr int MAX_CARD = 2048;   // sampler's LDS rows
+constexpr int MF_MAX_COLS = 64;  // matrix-core GEMV columns per launch (16-column groups; 16 with an adapter)
 
 // A weight matrix in device layout: `out` rows of `in`. Q8_0: int8 q[out][in] + fp16
 // d[out][in/32]; Q4_0: the 16 nibble bytes of each block q[out][in/2] + d; F16 / F32: q only.

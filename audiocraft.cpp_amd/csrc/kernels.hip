@@ -128,10 +128,15 @@ __device__ __forceinline__ void quant_q8_lane(float v, int lane, int8_t* qdst, f
     if ((lane & 31) == 0) *ddst = h2f(f2h(d));
 }
 
-// Byte offset of element i of column col in a block-major Q8 buffer: block i / 32 holds 512
-// bytes in matrix-core operand order [g = (i % 32) / 8][col][i % 8].
-__device__ __forceinline__ size_t bm_off(int col, int i) {
-    return (size_t)(i >> 5) * 512 + ((i >> 3) & 3) * 128 + col * 8 + (i & 7);
+// Byte offset of element i of column col in a block-major Q8 buffer of `stride` elements per
+// column: columns go in groups of 16 (group col / 16 at stride * 16 bytes), and in a group block
+// i / 32 holds 512 bytes in matrix-core operand order [g = (i % 32) / 8][col % 16][i % 8].
+__device__ __forceinline__ size_t bm_off(int col, int i, int stride) {
+    return (size_t)(col >> 4) * stride * 16 + (size_t)(i >> 5) * 512 + ((i >> 3) & 3) * 128 + (col & 15) * 8 + (i & 7);
+}
+// Index of the scale of element i's block: [group][block][col % 16].
+__device__ __forceinline__ size_t bm_doff(int col, int i, int stride) {
+    return (size_t)(col >> 4) * (stride / 32) * 16 + (size_t)(i >> 5) * 16 + (col & 15);
 }
 
 // The KV-cache column a QKV launch's column n appends to: its own column in the caller's
@@ -144,7 +149,7 @@ __device__ __forceinline__ int kv_col(const GemvArgs& a, int n) {
 // Writes element i (of a column) in the activation form the consumer's weights want.
 __device__ __forceinline__ void put_act(const ActBuf& a, int col, int i, float v, int lane) {
     if (a.kind == ACT_Q8 && a.bm)
-        quant_q8_lane(v, lane, a.q + bm_off(col, i), a.d + (size_t)(i / 32) * 16 + col);
+        quant_q8_lane(v, lane, a.q + bm_off(col, i, a.stride), a.d + bm_doff(col, i, a.stride));
     else if (a.kind == ACT_Q8) quant_q8_lane(v, lane, a.q + (size_t)col * a.stride + i, a.d + (size_t)col * (a.stride / 32) + i / 32);
     else if (a.kind == ACT_F16) a.h[(size_t)col * a.stride + i] = f2h(v);
     else a.f[(size_t)col * a.stride + i] = v;
@@ -308,7 +313,7 @@ __device__ __forceinline__ void stamp_end(unsigned long long* p, unsigned long l
 }
 
 struct LdsAct {
-    int8_t* q;     // Q8 [col][in]  (bm_col >= 0: global block-major, column bm_col)
+    int8_t* q;     // Q8 [col][in]  (bm_col >= 0: global block-major of stride in, column bm_col)
     float* d;      // Q8 [col][in/32]
     uint16_t* h;   // F16 [col][in]
     float* f;      // F32 [col][in]
@@ -499,8 +504,8 @@ __device__ __forceinline__ void prologue(const GemvArgs& a, const LdsAct& x, dou
                                 | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.z * id) << 16
                                 | (uint32_t)(uint8_t)(int8_t)__builtin_roundf(t.w * id) << 24;
             if (f < nf && x.bm_col >= 0) {
-                *(uint32_t*)(x.q + bm_off(x.bm_col, 4 * f)) = word;
-                if ((lane & 7) == 0) x.d[(size_t)(f / 8) * 16 + x.bm_col] = h2f(f2h(d));
+                *(uint32_t*)(x.q + bm_off(x.bm_col, 4 * f, in)) = word;
+                if ((lane & 7) == 0) x.d[bm_doff(x.bm_col, 4 * f, in)] = h2f(f2h(d));
             } else if (f < nf) {
                 *(uint32_t*)(x.q + (size_t)n * in + 4 * f) = word;
                 if ((lane & 7) == 0) x.d[(size_t)n * nb + f / 8] = h2f(f2h(d));
@@ -711,8 +716,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
                 float dv;
                 quant_q8_lane(g, lane, &qv, &dv);
                 if (lane < 32 && d.bm) {
-                    d.q[bm_off(n, o)] = qv;
-                    if (lane == 0) d.d[(size_t)(o / 32) * 16 + n] = dv;
+                    d.q[bm_off(n, o, d.stride)] = qv;
+                    if (lane == 0) d.d[bm_doff(n, o, d.stride)] = dv;
                 } else if (lane < 32) {
                     d.q[(size_t)n * d.stride + o] = qv;
                     if (lane == 0) d.d[(size_t)n * (d.stride / 32) + o / 32] = dv;
@@ -1397,7 +1402,10 @@ template <> struct MfW<T_Q4_0> {
     }
 };
 
-template <int WT, int NB, int KW, int TILES, int EPI>
+__device__ __forceinline__ void mf_opaque(uint2& v) { asm volatile("" : "+v"(v.x), "+v"(v.y)); }
+__device__ __forceinline__ void mf_opaque(uint32_t& v) { asm volatile("" : "+v"(v)); }
+
+template <int WT, int NB, int KW, int TILES, int EPI, bool WIDE>
 __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     constexpr int M = 64 / KW;                        // leaves (partials) per wave
     constexpr int LB = ilog2<M>();
@@ -1407,19 +1415,40 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     static_assert(NB % KW == 0 && (NB < 64 || NB % 64 == 0), "unsupported width");
     static_assert(EPI != EPI_GELU_ACT || ROWS == 32, "GELU blocks quantize whole 32-row blocks");
     __shared__ float red[KW][ROWS][17];
+    __shared__ float yg[WIDE ? MF_MAX_COLS / 16 : 1][ROWS][17];   // WIDE: every column group's sums
     // adapter operands: the tile's B rows, every column's A x (rank <= 64), DoRA m and norm
     constexpr int AD_MAX = (ROWS + 16) * 64 + 2 * ROWS, AD_PER = (AD_MAX + 64 * KW - 1) / (64 * KW);
     __shared__ float adsh[AD_MAX];
     const unsigned long long t0 = stamp_begin(a.stamp);
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
-    const int row0 = blockIdx.x * ROWS, ncol = a.ncol;
+    // WIDE (17 to 64 columns, no adapter): the column groups one after another against one load
+    // of the weights, every group's epilogue after the last; else one group, epilogue in place
+    const int row0 = blockIdx.x * ROWS, ncol = a.ncol, groups = WIDE ? (ncol + 15) >> 4 : 1;
     const ActBuf& x = a.src;
     const int8_t* Wm = a.w.qm;
+    // one 16-column group of the block-major source: stride * 16 quant bytes, stride / 2 scales
+    const size_t gq = (size_t)x.stride * 16, gd = (size_t)(x.stride / 32) * 16;
+    // widths up to 2048 prefetch the next group's activations during a group's reduction; wider
+    // rows hold too many weight registers for that and load them at the group's start
+    constexpr bool PREFETCH = NB < 192;
     // 1. every load of the wave, in visiting order (a leaf's weights, activations and scales
     //    together, so its products can start while later leaves are still loading)
     typename MfW<WT>::T wa[TILES][M][S];
     uint2 xb[M][S], dw[TILES][M][S];
     float xd[M][S];
+    const auto load_x = [&](int grp) {
+#pragma unroll
+        for (int j = 0; j < M; ++j) {
+            const int i = bitrev<LB>(j);
+            if (i >= NVL) continue;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const int b = w + KW * i + 64 * s;
+                xb[j][s] = *(const uint2*)(x.q + grp * gq + ((size_t)b * 64 + lane) * 8);
+                xd[j][s] = x.d[grp * gd + (size_t)b * 16 + c16];
+            }
+        }
+    };
 #pragma unroll
     for (int j = 0; j < M; ++j) {
         const int i = bitrev<LB>(j);
@@ -1440,8 +1469,8 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     // adapter operands behind the weights (used only in the epilogue)
     const int ad_nb = a.ad_ax ? ROWS * a.ad_rank : 0, ad_nx = a.ad_ax ? ad_nb + ncol * a.ad_rank : 0;
     const int ad_n = ad_nx + (a.ad_ax && a.ad_m ? 2 * ROWS : 0);
-    float adr[AD_PER];
-    if (a.ad_ax) {
+    float adr[WIDE ? 1 : AD_PER];
+    if (!WIDE && a.ad_ax) {
         // one unconditional load per slot: the address is selected, slots past the end re-read B[0]
 #pragma unroll
         for (int k = 0; k < AD_PER; ++k) {
@@ -1457,6 +1486,52 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     // keep every load above in flight together: the scheduler would otherwise sink each next
     // to its first use and pay the memory latency once per leaf
     __builtin_amdgcn_sched_barrier(0);
+    // one output (row row0 + r, column n): the adapter, then the epilogue. (The caches' bases
+    // are read once here: a per-lane choice between two argument fields would otherwise become
+    // a per-lane load of the chosen field.)
+    float* const kcache = a.k;
+    float* const vcache = a.v;
+    const auto finish = [&](int n, int r, float y) {
+        const int row = row0 + r;
+        const bool live = n < ncol;
+        if (!WIDE && a.ad_ax && live)    // (an adapter's launch has at most 16 columns)
+            y = adapt_from(a, adsh + r * a.ad_rank, adsh + ad_nb + n * a.ad_rank, a.ad_m ? adsh[ad_nx + r] : 1.0f,
+                           a.ad_m ? adsh[ad_nx + ROWS + r] : 1.0f, y);
+        if constexpr (EPI == EPI_GELU_ACT) {
+            const float ge = gelu_erf(y);
+            const ActBuf& d = a.dst;
+            if (d.kind == ACT_Q8) {
+                int8_t qv;
+                float dv;
+                quant_q8_lane(ge, lane, &qv, &dv);    // lanes 32k..32k+31: one column's 32 rows
+                if (live && d.bm) {
+                    d.q[bm_off(n, row, d.stride)] = qv;
+                    if ((lane & 31) == 0) d.d[bm_doff(n, row, d.stride)] = dv;
+                } else if (live) {
+                    d.q[(size_t)n * d.stride + row] = qv;
+                    if ((lane & 31) == 0) d.d[(size_t)n * (d.stride / 32) + row / 32] = dv;
+                }
+            } else if (live) {
+                if (d.kind == ACT_F16) d.h[(size_t)n * d.stride + row] = f2h(ge);
+                else d.f[(size_t)n * d.stride + row] = ge;
+            }
+            if (live && a.dst_f) a.dst_f[(size_t)n * d.stride + row] = ge;
+        } else if (live && (EPI == EPI_QKV || !a.gate || a.gate[a.col0 + n])) {
+            if (EPI == EPI_STORE) a.y[(size_t)n * a.y_stride + row] = y;
+            else if (EPI == EPI_RESID) a.y[(size_t)n * a.y_stride + row] = a.y[(size_t)n * a.y_stride + row] + y;
+            else {
+                const int sec = row / a.dim, wi = row - sec * a.dim, head = wi >> 6, dm = wi & 63;
+                if (sec == 0) a.y[(size_t)n * a.dim + wi] = y;
+                else (sec == 1 ? kcache : vcache)[(((size_t)kv_col(a, n) * a.heads + head) * a.cap + a.pos[(a.col0 + n) >> a.cshift]) * 64 + dm] = y;
+            }
+        }
+    };
+    // column groups one after another against the same weights (in registers)
+    for (int cg = 0;;) {
+    if (WIDE && !PREFETCH && cg > 0) {
+        load_x(cg);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     // 2. leaves in order, merged as a binary counter
     float4 lev[TILES][LB + 1];
 #pragma unroll
@@ -1498,6 +1573,9 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
             lev[t][k] = carry;
         }
     }
+    // the next group's activations, behind this group's reduction (when the registers allow)
+    if (WIDE && PREFETCH && cg + 1 < groups) load_x(cg + 1);
+    __builtin_amdgcn_sched_barrier(0);
     // 3. the KW subtree sums -> the top of the tree, one (row, column) per thread
 #pragma unroll
     for (int t = 0; t < TILES; ++t) {
@@ -1506,14 +1584,16 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
         red[w][16 * t + 4 * g + 2][c16] = lev[t][LB].z;
         red[w][16 * t + 4 * g + 3][c16] = lev[t][LB].w;
     }
+    if constexpr (!WIDE) {
 #pragma unroll
-    for (int k = 0; k < AD_PER; ++k)
-        if (tid + 64 * KW * k < ad_n) adsh[tid + 64 * KW * k] = adr[k];
+        for (int k = 0; k < AD_PER; ++k)
+            if (tid + 64 * KW * k < ad_n) adsh[tid + 64 * KW * k] = adr[k];
+    }
     __syncthreads();
     for (int idx0 = 0; idx0 < ROWS * 16; idx0 += NT) {
         const int idx = idx0 + tid;
         if (idx0 + (tid & ~63) >= ROWS * 16) break;    // whole waves past the tile
-        const int n = idx / ROWS, r = idx % ROWS, row = row0 + r;
+        const int n = idx / ROWS, r = idx % ROWS;
         float v[KW];
 #pragma unroll
         for (int q = 0; q < KW; ++q) v[q] = red[q][r][n];
@@ -1521,38 +1601,35 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
         for (int off = KW / 2; off >= 1; off >>= 1)
 #pragma unroll
             for (int q = 0; q < off; ++q) v[q] = v[q] + v[q + off];
-        float y = v[0];
-        const bool live = n < ncol;
-        if (a.ad_ax && live)
-            y = adapt_from(a, adsh + r * a.ad_rank, adsh + ad_nb + n * a.ad_rank, a.ad_m ? adsh[ad_nx + r] : 1.0f,
-                           a.ad_m ? adsh[ad_nx + ROWS + r] : 1.0f, y);
-        if constexpr (EPI == EPI_GELU_ACT) {
-            const float ge = gelu_erf(y);
-            const ActBuf& d = a.dst;
-            if (d.kind == ACT_Q8) {
-                int8_t qv;
-                float dv;
-                quant_q8_lane(ge, lane, &qv, &dv);    // lanes 32k..32k+31: one column's 32 rows
-                if (live && d.bm) {
-                    d.q[bm_off(n, row)] = qv;
-                    if ((lane & 31) == 0) d.d[(size_t)(row / 32) * 16 + n] = dv;
-                } else if (live) {
-                    d.q[(size_t)n * d.stride + row] = qv;
-                    if ((lane & 31) == 0) d.d[(size_t)n * (d.stride / 32) + row / 32] = dv;
-                }
-            } else if (live) {
-                if (d.kind == ACT_F16) d.h[(size_t)n * d.stride + row] = f2h(ge);
-                else d.f[(size_t)n * d.stride + row] = ge;
+        if constexpr (WIDE) yg[cg][r][n] = v[0];
+        else finish(n, r, v[0]);
+    }
+    if constexpr (!WIDE) break;
+    if (++cg >= groups) break;
+    __syncthreads();   // the next group rewrites red
+    // the empty asm makes the weights look new to the next group, so their conversions (fp16
+    // scales, Q4_0 nibbles) are not hoisted out of the loop into twice the registers; at the
+    // loop's end, so the first group's products still start while its later loads are in flight
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+        if (bitrev<LB>(j) >= NVL) continue;
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int t = 0; t < TILES; ++t) {
+                mf_opaque(wa[t][j][s]);
+                mf_opaque(dw[t][j][s]);
             }
-            if (live && a.dst_f) a.dst_f[(size_t)n * d.stride + row] = ge;
-        } else if (live && (EPI == EPI_QKV || !a.gate || a.gate[a.col0 + n])) {
-            if (EPI == EPI_STORE) a.y[(size_t)n * a.y_stride + row] = y;
-            else if (EPI == EPI_RESID) a.y[(size_t)n * a.y_stride + row] = a.y[(size_t)n * a.y_stride + row] + y;
-            else {
-                const int sec = row / a.dim, wi = row - sec * a.dim, head = wi >> 6, dm = wi & 63;
-                if (sec == 0) a.y[(size_t)n * a.dim + wi] = y;
-                else (sec == 1 ? a.k : a.v)[(((size_t)kv_col(a, n) * a.heads + head) * a.cap + a.pos[(a.col0 + n) >> a.cshift]) * 64 + dm] = y;
-            }
+    }
+    }
+    // 4. WIDE: every group's epilogues, once the weights' registers are free
+    if constexpr (WIDE) {
+        __syncthreads();
+        for (int idx0 = 0; idx0 < groups * ROWS * 16; idx0 += NT) {
+            const int idx = idx0 + tid;
+            if (idx0 + (tid & ~63) >= groups * ROWS * 16) break;    // whole waves past the last group
+            const int n = idx / ROWS, r = idx % ROWS;
+            finish(n, r, yg[n >> 4][r][n & 15]);
         }
     }
     stamp_end(a.stamp, t0);
@@ -1615,6 +1692,7 @@ template <int WT> static void gemv_wt(const GemvArgs& a, hipStream_t s) {
 // Columns go in groups of two (every per-column pointer advanced by the group's offset).
 // ---- matrix-core GEMV: (blocks per row, waves per 16-row tile) choices
 static int mf_kw(int nb, int tiles_out) {
+    if (nb >= 256) return 8;   // 8192-wide rows: 16 waves would need more than 128 registers
     const int base = nb >= 128 ? 8 : 4;
     const int kw = tiles_out >= 256 ? base : 16;
     return nb % kw == 0 ? kw : base;
@@ -1628,12 +1706,15 @@ bool gemv_mf_ok(const GemvArgs& a) {
     return (a.w.type == T_Q8_0 || a.w.type == T_Q4_0) && a.w.dt && a.w.qm && a.pro == PRO_ACT && a.src.kind == ACT_Q8 &&
            a.src.bm &&
            a.src.stride == a.w.in &&
-           a.ncol >= 3 && a.ncol <= 16 && a.w.in % 32 == 0 &&
+           a.ncol >= 3 && a.ncol <= MF_MAX_COLS && (a.ncol <= 16 || !a.ad_ax) && a.w.in % 32 == 0 &&
            (mf_width(a.w.in / 32) || (a.w.type == T_Q4_0 && a.w.in / 32 == 256)) && a.w.out % rows == 0 &&
            (a.epi != EPI_GELU_ACT || a.w.in <= 2048);
 }
 template <int WT, int NB, int KW, int TILES, int EPI> static void mf_go(const GemvArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((k_gemv_mf<WT, NB, KW, TILES, EPI>), dim3(a.w.out / (16 * TILES)), dim3(64 * KW), 0, s, a);
+    if (a.ncol > 16)
+        hipLaunchKernelGGL((k_gemv_mf<WT, NB, KW, TILES, EPI, true>), dim3(a.w.out / (16 * TILES)), dim3(64 * KW), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_gemv_mf<WT, NB, KW, TILES, EPI, false>), dim3(a.w.out / (16 * TILES)), dim3(64 * KW), 0, s, a);
 }
 template <int WT, int NB, int KW> static void mf_epi(const GemvArgs& a, hipStream_t s) {
     switch (a.epi) {
@@ -1644,11 +1725,11 @@ template <int WT, int NB, int KW> static void mf_epi(const GemvArgs& a, hipStrea
     }
 }
 template <int WT, int NB> static void mf_nb(const GemvArgs& a, hipStream_t s) {
-    // mf_kw gives 4 only below 128 blocks, 8 only at 128 and up, 16 only when it divides NB
+    // mf_kw gives 4 only below 128 blocks, 8 only at 128 and up, 16 only when it divides NB and NB < 256
     switch (mf_kw(NB, a.w.out / (a.epi == EPI_GELU_ACT ? 32 : 16))) {
     case 4: if constexpr (NB < 128) mf_epi<WT, NB, 4>(a, s); break;
     case 8: if constexpr (NB >= 128) mf_epi<WT, NB, 8>(a, s); break;
-    default: if constexpr (NB % 16 == 0) mf_epi<WT, NB, 16>(a, s); break;
+    default: if constexpr (NB % 16 == 0 && NB < 256) mf_epi<WT, NB, 16>(a, s); break;
     }
 }
 template <int WT> static void mf_wt(const GemvArgs& a, hipStream_t s) {

@@ -148,7 +148,7 @@ struct mgx_stream {
     // share the kv_cols caches of the stream it serves)
     size_t layer_kv() const { return (size_t)(kv_cols ? kv_cols : n_seq) * m->c.heads * kv_rows * 64; }
     void alloc_act(ActStore& a, int cols, int stride) {
-        if (n_seq >= 3) cols = std::max(cols, 16);   // block-major Q8 has 16 column slots
+        if (n_seq >= 3) cols = (std::max(cols, 16) + 15) / 16 * 16;   // block-major Q8: whole 16-column groups
         a.stride = stride;
         a.q = mem.alloc<int8_t>((size_t)cols * stride);
         a.d = mem.alloc<float>((size_t)cols * stride / 32);
@@ -212,7 +212,7 @@ void gemv_ad(mgx_stream* s, mgx::GemvArgs a, const AdapterW* ad, const float* xf
         m.pro = mgx::PRO_ACT;
         m.src = s->act_ln.view(mgx::T_Q8_0, true);
         m.src.stride = a.w.in;
-        if (s->act_ln.q && a.w.in <= s->act_ln.stride && mgx::gemv_mf_ok(m)) {
+        if (s->act_ln.q && a.w.in <= s->act_ln.stride && (a.ncol <= 16 || !ad) && mgx::gemv_mf_ok(m)) {
             mgx::GemvArgs p = ga(ad ? ad->A : mgx::DevMat{}, a.ncol);
             p.w.in = a.w.in;
             p.pro = a.pro; p.x = a.x; p.x_stride = a.x_stride; p.ln_w = a.ln_w; p.ln_b = a.ln_b; p.eps = a.eps;
@@ -490,7 +490,7 @@ std::unique_ptr<mgx_stream> make_prefill_view(mgx_stream* main, int g) {
     const mgx_lm_config& c = m->c;
     if (main->n_req != 1) throw Error(MGX_ERR_INVALID, "internal: a prefill view serves one request");
     const int cpr = main->cpr, n_seq = g * cpr;
-    if (g < 2 || n_seq > 16 || (cpr & (cpr - 1))) throw Error(MGX_ERR_INVALID, "internal: bad prefill view shape");
+    if (g < 2 || n_seq > mgx::MF_MAX_COLS || (cpr & (cpr - 1))) throw Error(MGX_ERR_INVALID, "internal: bad prefill view shape");
     auto s = std::make_unique<mgx_stream>();
     s->m = main->m;
     s->m->live.fetch_add(1);
@@ -517,15 +517,21 @@ std::unique_ptr<mgx_stream> make_prefill_view(mgx_stream* main, int g) {
     return s;
 }
 
+// Positions per prefill group: 64 columns (the matrix-core GEMV's widest launch), 16 when the
+// model carries adapters (their epilogue holds one 16-column group).
+int prefill_positions(const mgx_stream* s) {
+    return (s->m->ad_rank_max > 0 ? 16 : mgx::MF_MAX_COLS) / s->cpr;
+}
+
 // Runs positions first .. first + count - 1 of single-request stream s without heads (the
-// positions of a prefill before its last), 16 / cpr at a time through s's prefill view: each
+// positions of a prefill before its last), prefill_positions at a time through s's prefill view: each
 // column at its own position, causal by key count, all of a group's K / V appended by the same
 // launch before any column attends. Leaves s's device position at first + count. Returns false,
 // running nothing, when a view cannot serve s: several requests, or a stream count that is not
 // 1, 2, 4 or 8 (a view's column n is at position n >> log2(streams)).
 bool run_prefill(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int first, int count) {
     if (s->n_req != 1 || s->cpr > 8 || (s->cpr & (s->cpr - 1)) || count < 2) return false;
-    if (!s->pf) s->pf = make_prefill_view(s, 16 / s->cpr);
+    if (!s->pf) s->pf = make_prefill_view(s, prefill_positions(s));
     mgx_stream* pf = s->pf.get();
     const int G = pf->n_req;
     for (int p0 = 0; p0 < count; p0 += G) {
@@ -890,7 +896,7 @@ void session_create(mgx_model* m, const mgx_batch_request* reqs, int R, int32_t 
     make_stream(m, S, R * (ss->guided ? 2 : 1), R, t5s.data(), n_ctx, ss->guided ? 1 : 0, &raw);
     ss->s.reset(raw);
     mgx_stream* st = ss->s.get();
-    if (R == 1 && start - 1 >= 2) st->pf = make_prefill_view(st, 16 / st->cpr);
+    if (R == 1 && start - 1 >= 2) st->pf = make_prefill_view(st, prefill_positions(st));
     ss->dseq = ss->mem.alloc<int32_t>(ss->seq.size());
     uint8_t* dmask = ss->mem.alloc<uint8_t>(mask.size());
     mgx::ReqParams* dpar = ss->mem.alloc<mgx::ReqParams>(par.size());
