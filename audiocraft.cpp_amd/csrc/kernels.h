@@ -185,6 +185,8 @@ void launch_sample(const SampleArgs& a, hipStream_t s);
 void launch_advance(int* pos, int* live, const ReqParams* par, int n_req, hipStream_t s);
 // pos[r] = p0 + r for r < n (n <= 64): the positions of a multi-position prefill group.
 void launch_set_positions(int* pos, int n, int p0, hipStream_t s);
+// p[r] = v for r < n (n <= 64).
+void launch_fill_i32(int* p, int n, int v, hipStream_t s);
 // Opens request r of a slotted batch: position 0, live, its parameters and conditioning length.
 void launch_slot_open(int* pos, int* live, ReqParams* par, int* nc, int r, const ReqParams& p, int n_ctx,
                       hipStream_t s);

@@ -1344,6 +1344,13 @@ __global__ __launch_bounds__(64) void k_set_positions(int* pos, int n, int p0) {
 void launch_set_positions(int* pos, int n, int p0, hipStream_t s) {
     hipLaunchKernelGGL(k_set_positions, dim3(1), dim3(64), 0, s, pos, n, p0);
 }
+__global__ __launch_bounds__(64) void k_fill_i32(int* p, int n, int v) {
+    const int r = threadIdx.x;
+    if (r < n) p[r] = v;
+}
+void launch_fill_i32(int* p, int n, int v, hipStream_t s) {
+    hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(64), 0, s, p, n, v);
+}
 void launch_slot_open(int* pos, int* live, ReqParams* par, int* nc, int r, const ReqParams& p, int n_ctx,
                       hipStream_t s) {
     hipLaunchKernelGGL(k_slot_open, dim3(1), dim3(64), 0, s, pos, live, par, nc, r, p, n_ctx);

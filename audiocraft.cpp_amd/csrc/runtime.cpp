@@ -125,9 +125,10 @@ struct mgx_stream {
     unsigned long long* stamps = nullptr;
     double clock_khz = 0.0;
     // A prefill view (make_prefill_view) borrows the caches, the memory, the sinusoid table and
-    // the HIP stream of the stream it serves: columns map to caches modulo kv_cols and every
-    // request reads memory 0.
-    int kv_cols = 0;
+    // the HIP stream of the stream it serves, aimed at one of its requests (aim_view): columns
+    // map to that request's caches modulo kv_cols, layers step over the served stream's kv_layer
+    // cache columns, and every column reads that request's memory.
+    int kv_cols = 0, kv_layer = 0;
     bool shared_mem = false, owns_hs = true;
     int mem_reqs = 0;                        // requests the cross K / V hold (n_req unless a view)
     std::unique_ptr<mgx_stream> pf;          // this stream's prefill view, once a prefill used one
@@ -144,9 +145,9 @@ struct mgx_stream {
         marks.push_back({(int)marks.size(), kind, bytes});
         return stamps + 2 * 64 * (size_t)marks.back().slot;
     }
-    // one layer's K (or V) cache: every cache column's heads x rows (a prefill view's columns
-    // share the kv_cols caches of the stream it serves)
-    size_t layer_kv() const { return (size_t)(kv_cols ? kv_cols : n_seq) * m->c.heads * kv_rows * 64; }
+    // one layer's K (or V) cache: every cache column's heads x rows (a prefill view steps over
+    // the kv_layer columns of the stream it serves)
+    size_t layer_kv() const { return (size_t)(kv_layer ? kv_layer : n_seq) * m->c.heads * kv_rows * 64; }
     void alloc_act(ActStore& a, int cols, int stride) {
         if (n_seq >= 3) cols = (std::max(cols, 16) + 15) / 16 * 16;   // block-major Q8: whole 16-column groups
         a.stride = stride;
@@ -488,7 +489,7 @@ namespace {
 std::unique_ptr<mgx_stream> make_prefill_view(mgx_stream* main, int g) {
     const mgx_model* m = main->m;
     const mgx_lm_config& c = m->c;
-    if (main->n_req != 1) throw Error(MGX_ERR_INVALID, "internal: a prefill view serves one request");
+    if (main->n_req != 1 && !main->dlive) throw Error(MGX_ERR_INVALID, "internal: a prefill view serves one request or slots");
     const int cpr = main->cpr, n_seq = g * cpr;
     if (g < 2 || n_seq > mgx::MF_MAX_COLS || (cpr & (cpr - 1))) throw Error(MGX_ERR_INVALID, "internal: bad prefill view shape");
     auto s = std::make_unique<mgx_stream>();
@@ -501,8 +502,9 @@ std::unique_ptr<mgx_stream> make_prefill_view(mgx_stream* main, int g) {
     s->max_chunks = main->max_chunks; s->kv_rows = main->kv_rows;
     s->hs = main->hs; s->owns_hs = false;
     s->K = main->K; s->V = main->V; s->xk = main->xk; s->xv = main->xv; s->table = main->table;
-    s->kv_cols = cpr; s->shared_mem = true;
+    s->kv_cols = cpr; s->kv_layer = main->n_seq; s->shared_mem = true;
     s->dpos = s->mem.alloc<int>((size_t)g);
+    if (main->dnc) s->dnc = s->mem.alloc<int>((size_t)g);   // the aimed request's conditioning length, per position
     s->cmax = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * mgx::ATT_SUBS);
     s->x = s->mem.alloc<float>((size_t)n_seq * c.dim);
     s->qb = s->mem.alloc<float>((size_t)n_seq * c.dim);
@@ -515,6 +517,17 @@ std::unique_ptr<mgx_stream> make_prefill_view(mgx_stream* main, int g) {
     s->alloc_act(s->act_ln, n_seq, c.dim);
     if (m->ad_rank_max > 0) s->ax = s->mem.alloc<float>((size_t)n_seq * m->ad_rank_max);
     return s;
+}
+
+// Aims view pf of stream main at main's request r: its caches (columns r * cpr ..), its memory.
+void aim_view(mgx_stream* pf, const mgx_stream* main, int r) {
+    const mgx_lm_config& c = main->m->c;
+    const size_t col = (size_t)r * main->cpr * c.heads * main->kv_rows * 64;
+    pf->K = main->K + col;
+    pf->V = main->V + col;
+    const size_t mem = (size_t)r * c.heads * main->n_ctx * 64;
+    pf->xk = main->xk ? main->xk + mem : nullptr;
+    pf->xv = main->xv ? main->xv + mem : nullptr;
 }
 
 // Positions per prefill group: 64 columns (the matrix-core GEMV's widest launch), 16 when the
@@ -533,6 +546,7 @@ bool run_prefill(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base
     if (s->n_req != 1 || s->cpr > 8 || (s->cpr & (s->cpr - 1)) || count < 2) return false;
     if (!s->pf) s->pf = make_prefill_view(s, prefill_positions(s));
     mgx_stream* pf = s->pf.get();
+    aim_view(pf, s, 0);
     const int G = pf->n_req;
     for (int p0 = 0; p0 < count; p0 += G) {
         const int g = std::min(G, count - p0);
@@ -1145,9 +1159,11 @@ int mgx_generate(mgx_model* m, const float* t5_hidden, int32_t n_ctx, int32_t de
 // ------------------------------------------------------------------------------------
 // `n` slots of `cpr` streams (2: guided or not, 1: unguided only) share one stream of n * cpr
 // columns. A request is opened into a free slot between steps: its delay-pattern sequence,
-// mask and uniforms go to the slot's rows, its conditioning to the slot's cross K / V, and its
-// position to 0. Every step then processes each live slot's next position -- its prompt
-// positions first (no sampling), then its loop offsets start..S-1 (sampling) -- and the device
+// mask and uniforms go to the slot's rows, its conditioning to the slot's cross K / V, its
+// prompt before the last position runs through the prefill view aimed at the slot (slot_prefill)
+// and its position goes to start - 1 (0 for a prompt too short for a group). Every step then
+// processes each live slot's next position -- any prompt positions left (no sampling), then
+// its loop offsets start..S-1 (sampling) -- and the device
 // retires a slot after its last offset (k_advance). Each request computes exactly what it
 // computes alone: every column's arithmetic depends only on that column's inputs.
 struct mgx_slots {
@@ -1246,6 +1262,29 @@ void slot_check(const mgx_slots* sl, const mgx_batch_request& q, int n_ctx, int 
     if (guided && !q.t5_hidden) throw Error(MGX_ERR_INVALID, "the conditioning has no tokens");
 }
 
+// Runs positions 0 .. count - 1 of slot r (its prompt before the last position) through the
+// slots stream's prefill view aimed at the slot, prefill_positions at a time, and moves the
+// slot's device position to count. The same columns as batch steps would compute (each at its
+// own position, causal by key count), so the slot's caches hold the same values. Returns false,
+// running nothing, when the prompt is too short for a group or the view cannot serve the slots.
+bool slot_prefill(mgx_slots* sl, int r, int count, int nc) {
+    mgx_stream* st = sl->s.get();
+    if (count < 2 || st->cpr > 8 || (st->cpr & (st->cpr - 1))) return false;
+    if (!st->pf) st->pf = make_prefill_view(st, prefill_positions(st));
+    mgx_stream* pf = st->pf.get();
+    aim_view(pf, st, r);
+    const int G = pf->n_req;
+    if (pf->dnc) mgx::launch_fill_i32(pf->dnc, G, nc, st->hs);
+    const int32_t* ids = sl->dseq + (size_t)r * sl->K * sl->seq_len;
+    for (int p0 = 0; p0 < count; p0 += G) {
+        const int g = std::min(G, count - p0);
+        mgx::launch_set_positions(pf->dpos, g, p0, st->hs);
+        step(pf, ids, sl->seq_len, 0, 0, false, nullptr, p0 + g - 1, g * pf->cpr);
+    }
+    mgx::launch_set_positions(st->dpos + r, 1, count, st->hs);
+    return true;
+}
+
 void slot_open(mgx_slots* sl, int r, const mgx_batch_request& q, int n_ctx, int prompt_len) {
     slot_check(sl, q, n_ctx, prompt_len);
     if (r < 0 || r >= sl->n) throw Error(MGX_ERR_INVALID, "slot index out of range");
@@ -1287,8 +1326,10 @@ void slot_open(mgx_slots* sl, int r, const mgx_batch_request& q, int n_ctx, int 
     }
     mgx::launch_slot_open(st->dpos, st->dlive, st->dpar, st->dnc, r, req_params(p, guided, start, S),
                           guided ? n_ctx : 0, st->hs);
+    // the prompt before its last position in groups (no sampling happens there)
+    const int pre = slot_prefill(sl, r, start - 1, guided ? n_ctx : 0) ? start - 1 : 0;
     HIP_OK(hipGetLastError());
-    h.live = true; h.unread = true; h.pos = 0; h.start = start; h.S = S; h.T = T;
+    h.live = true; h.unread = true; h.pos = pre; h.start = start; h.S = S; h.T = T;
 }
 
 hipGraphExec_t slots_capture(mgx_slots* sl, int position) {
