@@ -489,7 +489,6 @@ namespace {
 std::unique_ptr<mgx_stream> make_prefill_view(mgx_stream* main, int g) {
     const mgx_model* m = main->m;
     const mgx_lm_config& c = m->c;
-    if (main->n_req != 1 && !main->dlive) throw Error(MGX_ERR_INVALID, "internal: a prefill view serves one request or slots");
     const int cpr = main->cpr, n_seq = g * cpr;
     if (g < 2 || n_seq > mgx::MF_MAX_COLS || (cpr & (cpr - 1))) throw Error(MGX_ERR_INVALID, "internal: bad prefill view shape");
     auto s = std::make_unique<mgx_stream>();
@@ -536,24 +535,38 @@ int prefill_positions(const mgx_stream* s) {
     return (s->m->ad_rank_max > 0 ? 16 : mgx::MF_MAX_COLS) / s->cpr;
 }
 
-// Runs positions first .. first + count - 1 of single-request stream s without heads (the
-// positions of a prefill before its last), prefill_positions at a time through s's prefill view: each
-// column at its own position, causal by key count, all of a group's K / V appended by the same
-// launch before any column attends. Leaves s's device position at first + count. Returns false,
-// running nothing, when a view cannot serve s: several requests, or a stream count that is not
-// 1, 2, 4 or 8 (a view's column n is at position n >> log2(streams)).
-bool run_prefill(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int first, int count) {
-    if (s->n_req != 1 || s->cpr > 8 || (s->cpr & (s->cpr - 1)) || count < 2) return false;
+// Whether stream s prefills through a view: a view's column n is at position n >> log2(streams)
+// (1, 2, 4 or 8 streams per request), and a lockstep batch takes one request at a time only
+// when a view's group is wider than the batch's own steps (with adapters both are 16 columns,
+// and the batch's captured steps then win).
+bool prefill_by_view(const mgx_stream* s) {
+    if (s->cpr > 8 || (s->cpr & (s->cpr - 1))) return false;
+    return s->n_req == 1 || prefill_positions(s) * s->cpr > s->n_seq;
+}
+
+// Runs positions first .. first + count - 1 of stream s without heads (the positions of a
+// prefill before its last), request by request, prefill_positions at a time through s's
+// prefill view aimed at the request: each column at its own position, causal by key count, all
+// of a group's K / V appended by the same launch before any column attends. Request r's id of
+// codebook q at position p is ids[r * ids_req_stride + q * ids_stride + p - ids_base]. Leaves
+// every request's device position at first + count. Returns false, running nothing, when the
+// stream does not prefill by view (prefill_by_view) or count < 2.
+bool run_prefill(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int ids_req_stride, int first,
+                 int count) {
+    if (!prefill_by_view(s) || count < 2) return false;
     if (!s->pf) s->pf = make_prefill_view(s, prefill_positions(s));
     mgx_stream* pf = s->pf.get();
-    aim_view(pf, s, 0);
     const int G = pf->n_req;
-    for (int p0 = 0; p0 < count; p0 += G) {
-        const int g = std::min(G, count - p0);
-        mgx::launch_set_positions(pf->dpos, g, first + p0, s->hs);
-        step(pf, ids, ids_stride, ids_base, 0, false, nullptr, first + p0 + g - 1, g * pf->cpr);
+    for (int r = 0; r < s->n_req; ++r) {
+        aim_view(pf, s, r);
+        const int32_t* idr = ids + (size_t)r * ids_req_stride;
+        for (int p0 = 0; p0 < count; p0 += G) {
+            const int g = std::min(G, count - p0);
+            mgx::launch_set_positions(pf->dpos, g, first + p0, s->hs);
+            step(pf, idr, ids_stride, ids_base, 0, false, nullptr, first + p0 + g - 1, g * pf->cpr);
+        }
     }
-    mgx::launch_set_positions(s->dpos, 1, first + count, s->hs);
+    mgx::launch_fill_i32(s->dpos, s->n_req, first + count, s->hs);
     return true;
 }
 
@@ -766,7 +779,7 @@ int mgx_forward(mgx_stream* s, const int32_t* ids, int32_t n_tokens, float* logi
         // A prefill is the same per-position arithmetic as single steps (its causal mask only
         // adds exact zeros): the positions before the last run in groups of columns, the last
         // (the only one whose logits are read) as a single step.
-        if (run_prefill(s, s->ids, n_tokens, used, used, n_tokens - 1))
+        if (run_prefill(s, s->ids, n_tokens, used, 0, used, n_tokens - 1))
             step(s, s->ids, n_tokens, used, 0, true, nullptr, used + n_tokens - 1);
         else
             for (int t = 0; t < n_tokens; ++t) step(s, s->ids, n_tokens, used, 0, t == n_tokens - 1, nullptr, used + t);
@@ -910,7 +923,7 @@ void session_create(mgx_model* m, const mgx_batch_request* reqs, int R, int32_t 
     make_stream(m, S, R * (ss->guided ? 2 : 1), R, t5s.data(), n_ctx, ss->guided ? 1 : 0, &raw);
     ss->s.reset(raw);
     mgx_stream* st = ss->s.get();
-    if (R == 1 && start - 1 >= 2) st->pf = make_prefill_view(st, prefill_positions(st));
+    if (start - 1 >= 2 && prefill_by_view(st)) st->pf = make_prefill_view(st, prefill_positions(st));
     ss->dseq = ss->mem.alloc<int32_t>(ss->seq.size());
     uint8_t* dmask = ss->mem.alloc<uint8_t>(mask.size());
     mgx::ReqParams* dpar = ss->mem.alloc<mgx::ReqParams>(par.size());
@@ -973,8 +986,8 @@ int session_step(mgx_session* ss, int n) {
         const bool profiled = ss->prof_every > 0 && (offset - ss->start) % ss->prof_every == 0;
         if (offset == ss->start) {
             // prompt positions in groups, then the loop's first forward (one position at a time
-            // through the captured body steps where a group cannot serve: batches of requests)
-            if (!run_prefill(s, ss->dseq, ss->S, 0, 0, ss->start - 1))
+            // through the captured body steps where a group cannot serve)
+            if (!run_prefill(s, ss->dseq, ss->S, 0, ss->K * ss->S, 0, ss->start - 1))
                 for (int pos = 0; pos < ss->start - 1; ++pos) run_position(ss, false, false, pos);
             run_position(ss, true, false, ss->start - 1);
             HIP_OK(hipGetLastError());
