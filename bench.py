@@ -287,7 +287,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} requested). "
-              "The decode step shards by request; see DESIGN.md.", file=sys.stderr)
+              "The decode step would shard by request, one process per GPU.", file=sys.stderr)
         sys.exit(2)
     import mgx
     if args.workload == "server-medium-q8":

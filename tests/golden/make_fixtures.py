@@ -27,7 +27,9 @@ from oracle import cpu_ref as R  # noqa: E402
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 
-# BASELINE configurations 1-4 (5, the batched DoRA one, is checked against the oracle live).
+# The four single-request workloads at full length: small Q8_0 p250+c500, small F16 p500+c1500,
+# medium Q8_0 p500+c1500, large Q4_0 p1500+c1500 (the batched DoRA workload is checked against
+# the oracle live).
 CASES = {
     "c1_small_q8": dict(shape="small", wtype=8, prompt=250, gen=500, seed=0, sampling=True, top_k=250),
     "c1_small_q8_greedy": dict(shape="small", wtype=8, prompt=250, gen=500, seed=0, sampling=False, top_k=250),

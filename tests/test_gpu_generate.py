@@ -1,8 +1,9 @@
 """mg_generate on the GPU (mgx_generate / sessions) against the oracle's restatement.
 
 Live cases run the oracle beside the GPU on small shapes and compare every step's mixed
-logits bit for bit; fixture cases replay BASELINE configurations 1-4 at full length against
-codes the oracle produced ahead of time (tests/golden/make_fixtures.py)."""
+logits bit for bit; fixture cases replay the four single-request workloads (small Q8_0 and F16,
+medium Q8_0, large Q4_0) at full length against codes the oracle produced ahead of time
+(tests/golden/make_fixtures.py)."""
 import os
 import zlib
 
