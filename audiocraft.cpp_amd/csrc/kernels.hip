@@ -926,6 +926,94 @@ __global__ __launch_bounds__(64 * WAVES) void k_attn_pv(AttnArgs a) {
     }
 }
 
+// Wide launches (prefill groups): the softmax once per (head, column) instead of once per
+// chunk block. The same values in the same order as k_attn_pv builds them: global max from the
+// score-block maxima, e = expf(s - max) (0 past the position) written over the scores, each
+// 256-key chunk's sum in double by the butterfly, chunks added in order, and (float)(1 / total)
+// into the head's first score-block maximum slot.
+template <int NCH>
+__global__ __launch_bounds__(256) void k_attn_soft(AttnArgs a) {
+    const int h = blockIdx.x, n = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const size_t head = (size_t)n * a.heads + h;
+    float* S = a.scores + head * a.cap;
+    float* cmh = a.cmax + head * a.max_chunks * ATT_SUBS;
+    const int u = a.pos[n >> a.cshift] + 1;
+    __shared__ float el[NCH * ATT_CHUNK];
+    __shared__ double cs[NCH];
+    float M = cmh[0];
+#pragma unroll
+    for (int i = 1; i < NCH * ATT_SUBS; ++i) M = M > cmh[i] ? M : cmh[i];
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        const int j = tid + ATT_CHUNK * i;
+        const float e = j < u ? dexpf(S[j] - M) : 0.0f;
+        el[j] = e;
+        S[j] = e;
+    }
+    lds_barrier();
+    for (int cc = wave; cc < NCH; cc += 4) {
+        const float* e = el + cc * ATT_CHUNK;
+        const double r = fold64d_b(((double)e[lane] + (double)e[lane + 128]) + ((double)e[lane + 64] + (double)e[lane + 192]));
+        if (lane == 0) cs[cc] = r;
+    }
+    lds_barrier();
+    if (tid == 0) {
+        double total = 0.0;
+        for (int cc = 0; cc < NCH; ++cc) total = total + cs[cc];
+        cmh[0] = (float)(1.0 / total);
+    }
+}
+
+// Softmax.V of one chunk after k_attn_soft: p = e * inv from the rewritten scores; V as in
+// k_attn_pv (partial g = key mod 16, keys in increasing order, the 16 partials folded).
+__global__ __launch_bounds__(256) void k_attn_pv_e(AttnArgs a) {
+    const int c = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const size_t head = (size_t)n * a.heads + h;
+    const float* S = a.scores + head * a.cap;
+    const float inv = a.cmax[head * a.max_chunks * ATT_SUBS];
+    __shared__ float el[ATT_CHUNK];
+    __shared__ float4 vred[16][16];
+    const int g = wave * 4 + (lane >> 4), dq = lane & 15;
+    const float* V = a.v + ((size_t)(a.kv_cols ? n % a.kv_cols : n) * a.heads + h) * a.cap * 64;
+    const int u = a.pos[n >> a.cshift] + 1;
+    float4 vv[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+        const int j = c * ATT_CHUNK + g + 16 * m, jl = j < u ? j : u - 1;
+        vv[m] = ((const float4*)(V + (size_t)jl * 64))[dq];
+    }
+    el[tid] = S[c * ATT_CHUNK + tid];
+    lds_barrier();
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const int u_c = u - c * ATT_CHUNK;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+        const int jj = g + 16 * m;
+        if (jj < u_c) {
+            const float pm = el[jj] * inv;
+            acc.x = __builtin_fmaf(pm, vv[m].x, acc.x);
+            acc.y = __builtin_fmaf(pm, vv[m].y, acc.y);
+            acc.z = __builtin_fmaf(pm, vv[m].z, acc.z);
+            acc.w = __builtin_fmaf(pm, vv[m].w, acc.w);
+        }
+    }
+    vred[g][dq] = acc;
+    lds_barrier();
+    if (wave < 2) {
+        const float4 o = vred[g + 8][dq];
+        vred[g][dq] = make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
+    }
+    lds_barrier();
+    if (wave == 0) {
+        const float4 sv4 = vred[g][dq], o = vred[g + 4][dq];
+        float4 r = make_float4(sv4.x + o.x, sv4.y + o.y, sv4.z + o.z, sv4.w + o.w);
+        r.x = r.x + take_up<32>(r.x); r.y = r.y + take_up<32>(r.y); r.z = r.z + take_up<32>(r.z); r.w = r.w + take_up<32>(r.w);
+        r.x = r.x + take_up<16>(r.x); r.y = r.y + take_up<16>(r.y); r.z = r.z + take_up<16>(r.z); r.w = r.w + take_up<16>(r.w);
+        if (lane < 16) ((float4*)(a.opart + (head * a.max_chunks + c) * 64))[dq] = r;
+    }
+}
+
 // Chunk results added in order; the head's 64 outputs go to the out-projection activation.
 __global__ __launch_bounds__(64) void k_attn_reduce(AttnArgs a) {
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
@@ -1795,8 +1883,35 @@ void launch_gemv(const GemvArgs& a0, hipStream_t s) {
 template <int NCH> static void attn_pv(const AttnArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((k_attn_pv<NCH, PV_WAVES>), dim3(NCH, a.heads, a.ncol), dim3(64 * PV_WAVES), 0, s, a);
 }
+template <int NCH> static void attn_soft(const AttnArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((k_attn_soft<NCH>), dim3(a.heads, a.ncol), dim3(256), 0, s, a);
+}
 void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
     hipLaunchKernelGGL(k_attn_scores, dim3(nch * ATT_SUBS, a.heads, a.ncol), dim3(256), 0, s, a);
+    if (a.ncol > 16) {
+        // wide launches: the softmax once per (head, column), then every chunk's V
+        switch (nch) {
+        case 1: attn_soft<1>(a, s); break;
+        case 2: attn_soft<2>(a, s); break;
+        case 3: attn_soft<3>(a, s); break;
+        case 4: attn_soft<4>(a, s); break;
+        case 5: attn_soft<5>(a, s); break;
+        case 6: attn_soft<6>(a, s); break;
+        case 7: attn_soft<7>(a, s); break;
+        case 8: attn_soft<8>(a, s); break;
+        case 9: attn_soft<9>(a, s); break;
+        case 10: attn_soft<10>(a, s); break;
+        case 11: attn_soft<11>(a, s); break;
+        case 12: attn_soft<12>(a, s); break;
+        case 13: attn_soft<13>(a, s); break;
+        case 14: attn_soft<14>(a, s); break;
+        case 15: attn_soft<15>(a, s); break;
+        default: attn_soft<16>(a, s); break;
+        }
+        hipLaunchKernelGGL(k_attn_pv_e, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_attn_reduce, dim3(a.heads, a.ncol), dim3(64), 0, s, a);
+        return;
+    }
     switch (nch) {
     case 1: attn_pv<1>(a, s); break;
     case 2: attn_pv<2>(a, s); break;
