@@ -1511,13 +1511,14 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     static_assert(EPI != EPI_GELU_ACT || ROWS == 32, "GELU blocks quantize whole 32-row blocks");
     __shared__ float red[KW][ROWS][17];
     __shared__ float yg[WIDE ? MF_MAX_COLS / 16 : 1][ROWS][17];   // WIDE: every column group's sums
-    // adapter operands: the tile's B rows, every column's A x (rank <= 64), DoRA m and norm
+    // adapter operands: the tile's B rows, one column group's A x (rank <= 64), DoRA m and norm
     constexpr int AD_MAX = (ROWS + 16) * 64 + 2 * ROWS, AD_PER = (AD_MAX + 64 * KW - 1) / (64 * KW);
     __shared__ float adsh[AD_MAX];
     const unsigned long long t0 = stamp_begin(a.stamp);
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
-    // WIDE (17 to 64 columns, no adapter): the column groups one after another against one load
-    // of the weights, every group's epilogue after the last; else one group, epilogue in place
+    // WIDE (17 to 64 columns): the column groups one after another against one load of the
+    // weights, every group's epilogue after the last (an adapter's operands staged group by
+    // group); else one group, epilogue in place
     const int row0 = blockIdx.x * ROWS, ncol = a.ncol, groups = WIDE ? (ncol + 15) >> 4 : 1;
     const ActBuf& x = a.src;
     const int8_t* Wm = a.w.qm;
@@ -1562,7 +1563,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
         }
     }
     // adapter operands behind the weights (used only in the epilogue)
-    const int ad_nb = a.ad_ax ? ROWS * a.ad_rank : 0, ad_nx = a.ad_ax ? ad_nb + ncol * a.ad_rank : 0;
+    const int ad_nb = a.ad_ax ? ROWS * a.ad_rank : 0, ad_nx = a.ad_ax ? ad_nb + (WIDE ? 16 : ncol) * a.ad_rank : 0;
     const int ad_n = ad_nx + (a.ad_ax && a.ad_m ? 2 * ROWS : 0);
     float adr[WIDE ? 1 : AD_PER];
     if (!WIDE && a.ad_ax) {
@@ -1589,8 +1590,8 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     const auto finish = [&](int n, int r, float y) {
         const int row = row0 + r;
         const bool live = n < ncol;
-        if (!WIDE && a.ad_ax && live)    // (an adapter's launch has at most 16 columns)
-            y = adapt_from(a, adsh + r * a.ad_rank, adsh + ad_nb + n * a.ad_rank, a.ad_m ? adsh[ad_nx + r] : 1.0f,
+        if (a.ad_ax && live)    // the staged A x holds column n's group (n < 16 when not WIDE)
+            y = adapt_from(a, adsh + r * a.ad_rank, adsh + ad_nb + (n & 15) * a.ad_rank, a.ad_m ? adsh[ad_nx + r] : 1.0f,
                            a.ad_m ? adsh[ad_nx + ROWS + r] : 1.0f, y);
         if constexpr (EPI == EPI_GELU_ACT) {
             const float ge = gelu_erf(y);
@@ -1720,11 +1721,32 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     // 4. WIDE: every group's epilogues, once the weights' registers are free
     if constexpr (WIDE) {
         __syncthreads();
-        for (int idx0 = 0; idx0 < groups * ROWS * 16; idx0 += NT) {
-            const int idx = idx0 + tid;
-            if (idx0 + (tid & ~63) >= groups * ROWS * 16) break;    // whole waves past the last group
-            const int n = idx / ROWS, r = idx % ROWS;
-            finish(n, r, yg[n >> 4][r][n & 15]);
+        if (!a.ad_ax) {
+            for (int idx0 = 0; idx0 < groups * ROWS * 16; idx0 += NT) {
+                const int idx = idx0 + tid;
+                if (idx0 + (tid & ~63) >= groups * ROWS * 16) break;    // whole waves past the last group
+                const int n = idx / ROWS, r = idx % ROWS;
+                finish(n, r, yg[n >> 4][r][n & 15]);
+            }
+        } else {
+            for (int g2 = 0; g2 < groups; ++g2) {
+                // the group's adapter operands: the tile's B rows, its 16 columns' A x (0 past the
+                // launch's columns), DoRA m and norm -- the layout the non-WIDE staging builds
+                const int ax0 = g2 * 16 * a.ad_rank, axn = ncol * a.ad_rank;
+                for (int e = tid; e < ad_n; e += NT)
+                    adsh[e] = e < ad_nb ? a.ad_B[(size_t)row0 * a.ad_rank + e]
+                            : e < ad_nx ? (ax0 + e - ad_nb < axn ? a.ad_ax[ax0 + e - ad_nb] : 0.0f)
+                            : e < ad_nx + ROWS ? a.ad_m[row0 + (e - ad_nx)]
+                            : a.ad_norm[row0 + (e - ad_nx - ROWS)];
+                __syncthreads();
+                for (int idx0 = 0; idx0 < ROWS * 16; idx0 += NT) {
+                    const int idx = idx0 + tid;
+                    if (idx0 + (tid & ~63) >= ROWS * 16) break;    // whole waves past the group
+                    const int nl = idx / ROWS, r = idx % ROWS;
+                    finish(g2 * 16 + nl, r, yg[g2][r][nl]);
+                }
+                __syncthreads();   // the next group rewrites the staged operands
+            }
         }
     }
     stamp_end(a.stamp, t0);
@@ -1801,7 +1823,7 @@ bool gemv_mf_ok(const GemvArgs& a) {
     return (a.w.type == T_Q8_0 || a.w.type == T_Q4_0) && a.w.dt && a.w.qm && a.pro == PRO_ACT && a.src.kind == ACT_Q8 &&
            a.src.bm &&
            a.src.stride == a.w.in &&
-           a.ncol >= 3 && a.ncol <= MF_MAX_COLS && (a.ncol <= 16 || !a.ad_ax) && a.w.in % 32 == 0 &&
+           a.ncol >= 3 && a.ncol <= MF_MAX_COLS && a.w.in % 32 == 0 &&
            (mf_width(a.w.in / 32) || (a.w.type == T_Q4_0 && a.w.in / 32 == 256)) && a.w.out % rows == 0 &&
            (a.epi != EPI_GELU_ACT || a.w.in <= 2048);
 }

@@ -213,7 +213,7 @@ void gemv_ad(mgx_stream* s, mgx::GemvArgs a, const AdapterW* ad, const float* xf
         m.pro = mgx::PRO_ACT;
         m.src = s->act_ln.view(mgx::T_Q8_0, true);
         m.src.stride = a.w.in;
-        if (s->act_ln.q && a.w.in <= s->act_ln.stride && (a.ncol <= 16 || !ad) && mgx::gemv_mf_ok(m)) {
+        if (s->act_ln.q && a.w.in <= s->act_ln.stride && mgx::gemv_mf_ok(m)) {
             mgx::GemvArgs p = ga(ad ? ad->A : mgx::DevMat{}, a.ncol);
             p.w.in = a.w.in;
             p.pro = a.pro; p.x = a.x; p.x_stride = a.x_stride; p.ln_w = a.ln_w; p.ln_b = a.ln_b; p.eps = a.eps;
@@ -529,16 +529,14 @@ void aim_view(mgx_stream* pf, const mgx_stream* main, int r) {
     pf->xv = main->xv ? main->xv + mem : nullptr;
 }
 
-// Positions per prefill group: 64 columns (the matrix-core GEMV's widest launch), 16 when the
-// model carries adapters (their epilogue holds one 16-column group).
+// Positions per prefill group: 64 columns (the matrix-core GEMV's widest launch).
 int prefill_positions(const mgx_stream* s) {
-    return (s->m->ad_rank_max > 0 ? 16 : mgx::MF_MAX_COLS) / s->cpr;
+    return mgx::MF_MAX_COLS / s->cpr;
 }
 
 // Whether stream s prefills through a view: a view's column n is at position n >> log2(streams)
 // (1, 2, 4 or 8 streams per request), and a lockstep batch takes one request at a time only
-// when a view's group is wider than the batch's own steps (with adapters both are 16 columns,
-// and the batch's captured steps then win).
+// when a view's group is wider than the batch's own steps.
 bool prefill_by_view(const mgx_stream* s) {
     if (s->cpr > 8 || (s->cpr & (s->cpr - 1))) return false;
     return s->n_req == 1 || prefill_positions(s) * s->cpr > s->n_seq;

@@ -67,6 +67,20 @@ def test_adapter_ranks_at_real_widths(M, shape, wtype, rank):
         assert np.array_equal(got, want), f"position {t}: max {np.abs(got - want).max()}"
 
 
+@pytest.mark.parametrize("shape,wtype,rank", [("mini1536", 8, 16), ("mini2048", 2, 64)])
+@pytest.mark.parametrize("dora", [False, True])
+def test_adapter_wide_prefill_matches_oracle(M, shape, wtype, rank, dora):
+    """A 40-token prefill with every projection adapted runs its first 39 positions through the
+    prefill view: one full 64-column group (32 positions x 2 streams, four 16-column groups
+    against one load of the weights, the adapter's A x staged group by group) and a ragged
+    group of 7 positions; then single steps."""
+    print(f"adapter wide prefill {shape} wtype={wtype} rank={rank} dora={dora}", flush=True)
+    c = H.model(shape, wtype, 5).config
+    ads = synth.synth_adapters(c, rank=rank, targets=ALL, dora=dora, seed=rank + 1)
+    for t, got, want in forward_both(M, shape, wtype, 5, ads, prefill=40, steps=2):
+        assert np.array_equal(got, want), f"position {t}: max {np.abs(got - want).max()}"
+
+
 @pytest.mark.parametrize("dora", [False, True])
 def test_zero_strength_adapter_is_identity(M, dora):
     """lora.h:62 / mg_train_parity_probe.cpp:97-102: strength 0 gives the base model bit for bit."""
