@@ -970,6 +970,45 @@ REF_API void ref_softmax_into(const float* logits, int n, float temperature, flo
     const float inv = (float)(1.0 / total);
     for (int i = 0; i < n; ++i) probs[i] *= inv;
 }
+/* softmax_into with the GPU sampler's exp routine (ref_exp, the same Cody-Waite + Taylor
+   steps as the kernel's) in place of libm's exp: the tests count the rows where the two
+   give different float probabilities. */
+REF_API void ref_softmax_into_devexp(const float* logits, int n, float temperature, float* probs) {
+    float peak = logits[0];
+    for (int i = 1; i < n; ++i) peak = peak < logits[i] ? logits[i] : peak;
+    double total = 0.0;
+    for (int i = 0; i < n; ++i) {
+        const double e = ref_exp(((double)logits[i] - peak) / temperature);
+        probs[i] = (float)e;
+        total += e;
+    }
+    const float inv = (float)(1.0 / total);
+    for (int i = 0; i < n; ++i) probs[i] *= inv;
+}
+/* Rows [rows][n]: how many rows' probabilities differ between libm's exp and ref_exp, and how
+   many of the exp values differ at all (in double). */
+REF_API void ref_softmax_exp_compare(const float* logits, int n, int rows, float temperature, long long* row_diff,
+                                     long long* exp_diff) {
+    long long rd = 0, ed = 0;
+    #pragma omp parallel for reduction(+:rd, ed) schedule(static)
+    for (int r = 0; r < rows; ++r) {
+        const float* x = logits + (size_t)r * n;
+        float* a = (float*)malloc(sizeof(float) * (size_t)n);
+        float* b = (float*)malloc(sizeof(float) * (size_t)n);
+        ref_softmax_into(x, n, temperature, a);
+        ref_softmax_into_devexp(x, n, temperature, b);
+        if (memcmp(a, b, sizeof(float) * (size_t)n) != 0) ++rd;
+        float peak = x[0];
+        for (int i = 1; i < n; ++i) peak = peak < x[i] ? x[i] : peak;
+        for (int i = 0; i < n; ++i) {
+            const double t = ((double)x[i] - peak) / temperature;
+            if (exp(t) != ref_exp(t)) ++ed;
+        }
+        free(a); free(b);
+    }
+    *row_diff = rd;
+    *exp_diff = ed;
+}
 static int cmp_desc(const void* a, const void* b) {
     const float x = *(const float*)a, y = *(const float*)b;
     return x < y ? 1 : (x > y ? -1 : 0);

@@ -92,6 +92,9 @@ def lib():
         L.ref_rng_uniform.argtypes = [P]
         L.ref_argmax.argtypes = [P, C.c_int]
         L.ref_softmax_into.argtypes = [P, C.c_int, C.c_float, P]
+        L.ref_softmax_into_devexp.argtypes = [P, C.c_int, C.c_float, P]
+        L.ref_softmax_exp_compare.argtypes = [P, C.c_int, C.c_int, C.c_float, C.POINTER(C.c_longlong),
+                                              C.POINTER(C.c_longlong)]
         L.ref_top_k_filter.argtypes = [P, C.c_int, C.c_int]
         L.ref_categorical.argtypes = [P, C.c_int, C.c_double, P]
         L.ref_sample_top_k.argtypes = [P, C.c_int, C.c_int, C.c_float, P, P]
