@@ -117,10 +117,11 @@ struct mgx_stream {
     int32_t* ids = nullptr;                  // [n_q][cap] staged ids for mgx_forward
     // Launch timing: when `prof_on`, every GEMV and attention launch gets a slot in `stamps`
     // (device [slot][2]: earliest block start, latest wave end on the GPU wall clock).
-    struct Mark { int slot, kind; double bytes; };
+    struct Mark { int slot, kind, tag; double bytes; };
     static constexpr int STAMP_SLOTS = 16384;   // launches; 64 sub-slots of 16 B each
     bool prof_on = false;
     int prof_pos = 0;                        // host view of the position, for profiling
+    int prof_tag = -1;                       // the projection (MGX_PROF_*) the next launches belong to
     std::vector<Mark> marks;
     unsigned long long* stamps = nullptr;
     double clock_khz = 0.0;
@@ -142,7 +143,7 @@ struct mgx_stream {
     // the next timing slot, or null when profiling is off or the slots are used up
     unsigned long long* stamp_slot(int kind, double bytes) {
         if (!prof_on || !stamps || (int)marks.size() >= STAMP_SLOTS) return nullptr;
-        marks.push_back({(int)marks.size(), kind, bytes});
+        marks.push_back({(int)marks.size(), kind, prof_tag, bytes});
         return stamps + 2 * 64 * (size_t)marks.back().slot;
     }
     // one layer's K (or V) cache: every cache column's heads x rows (a prefill view steps over
@@ -189,7 +190,7 @@ double bytes_per_weight(int type) {
     return 4.0;
 }
 
-enum { PROF_GEMV = 0, PROF_ATTN = 1 };
+enum { PROF_GEMV = MGX_PROF_GEMV, PROF_ATTN = MGX_PROF_ATTN };
 
 // One projection. Algorithmic bytes of a launch = the weights at their stored precision.
 void gemv(mgx_stream* s, mgx::GemvArgs a) {
@@ -279,6 +280,7 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
         float* Vl = s->V + (size_t)l * s->layer_kv();
         // self-attention: LN1 + qkv with the K/V append, scores, softmax + V (+ chunk reduce)
         {
+            s->prof_tag = MGX_PROF_QKV;
             mgx::GemvArgs a = ga(L.w[P_QKV], N);
             pro_ln(a, s->x, D, L.n1w, L.n1b, c.norm_eps);
             a.epi = mgx::EPI_QKV; a.y = s->qb; a.k = Kl; a.v = Vl; a.dim = D; a.heads = c.heads; a.cap = s->kv_rows;
@@ -286,6 +288,7 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
             gemv_ad(s, a, L.ad[P_QKV]);
         }
         {
+            s->prof_tag = MGX_PROF_ATTN;
             mgx::AttnArgs at{};
             at.q = s->qb; at.k = Kl; at.v = Vl; at.scores = s->scores; at.opart = s->opart; at.cmax = s->cmax;
             at.dim = D; at.heads = c.heads; at.cap = s->kv_rows; at.max_chunks = s->max_chunks; at.ncol = N;
@@ -296,6 +299,7 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
             mgx::launch_attention(at, att_chunks(position), s->hs);
         }
         {
+            s->prof_tag = MGX_PROF_OUT;
             mgx::GemvArgs a = ga(L.w[P_OUT], N);
             pro_act(a, s->act_o.view(L.w[P_OUT].type, bo));
             epi_store(a, s->x, D, true);
@@ -305,6 +309,7 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
         // contribution is exactly 0): column r * cpr of x
         if (s->cross) {
             const size_t xl = (size_t)l * s->mem_reqs * c.heads * s->n_ctx * 64;
+            s->prof_tag = MGX_PROF_CROSS_Q;
             mgx::GemvArgs a = ga(L.w[P_CQ], R);
             pro_ln(a, s->x, s->cpr * D, L.ncw, L.ncb, c.norm_eps);
             epi_store(a, s->qc, D);
@@ -316,6 +321,7 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
             xa.out = s->act_c.view(L.w[P_COUT].type, bc);
             xa.out_f = L.ad[P_COUT] ? s->act_c.f : nullptr;
             mgx::launch_xattn(xa, c.heads, R, s->hs);
+            s->prof_tag = MGX_PROF_CROSS_OUT;
             mgx::GemvArgs b = ga(L.w[P_COUT], R);
             pro_act(b, s->act_c.view(L.w[P_COUT].type, bc));
             epi_store(b, s->x, s->cpr * D, true);
@@ -324,11 +330,13 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
         }
         // feed-forward: LN2 + ff.0 + GELU (quantized in the epilogue), ff.2 + residual
         {
+            s->prof_tag = MGX_PROF_FF0;
             mgx::GemvArgs a = ga(L.w[P_FF0], N);
             pro_ln(a, s->x, D, L.n2w, L.n2b, c.norm_eps);
             a.epi = mgx::EPI_GELU_ACT; a.dst = s->act_f.view(L.w[P_FF2].type, bf);
             a.dst_f = L.ad[P_FF2] ? s->act_f.f : nullptr;
             gemv_ad(s, a, L.ad[P_FF0]);
+            s->prof_tag = MGX_PROF_FF2;
             mgx::GemvArgs b = ga(L.w[P_FF2], N);
             pro_act(b, s->act_f.view(L.w[P_FF2].type, bf));
             epi_store(b, s->x, D, true);
@@ -336,11 +344,13 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
         }
     }
     if (heads) {
+        s->prof_tag = MGX_PROF_HEADS;
         mgx::GemvArgs a = ga(m->heads, N);
         pro_ln(a, s->x, D, m->out_w, m->out_b, c.norm_eps);
         epi_store(a, s->logits, c.n_q * c.card);
         gemv_ad(s, a, nullptr);
     }
+    s->prof_tag = -1;
     if (sample) mgx::launch_sample(*sample, s->hs);
     mgx::launch_advance(s->dpos, s->dlive, s->dpar, R, s->hs);
 }
@@ -1129,7 +1139,7 @@ int mgx_session_profile_read(mgx_session* ss, int32_t kind, double* ms_total, do
             std::vector<unsigned long long> st(2 * 64 * s->marks.size());
             HIP_OK(hipMemcpy(st.data(), s->stamps, st.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost));
             for (const auto& mk : s->marks) {
-                if (mk.kind != kind) continue;
+                if (mk.kind != kind && mk.tag != kind) continue;
                 unsigned long long b = ~0ull, e = 0ull;
                 for (int k = 0; k < 64; ++k) {
                     b = std::min(b, st[2 * (64 * (size_t)mk.slot + k)]);

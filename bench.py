@@ -7,17 +7,22 @@ reference's mg_generate (src/mg/pipeline.cpp:255-302). The workload is MusicGen-
 (48 layers, dim 1536, 24 heads, FFN 6144, 4 x 2048 codebooks) with random N(0, 0.02) weights
 quantized to Q8_0, CFG 3 over two streams, a 24 x 768 N(0,1) memory, a 500-frame random-code
 prompt (prefilled, untimed) and a 1500-frame continuation sampled with top-k 250, temperature 1,
-seed 1. W warmup decode steps run untimed, then exactly K decode steps are timed; if the
+seed 1. W warmup decode steps run untimed, then exactly K decode steps are timed; a run of fewer
+steps than the continuation holds is centred on the continuation's middle (the steps before it
+run untimed), so the keys it attends average those of the whole 30 s continuation; if the
 continuation runs out, a fresh session is prefilled outside the timed segments.
 
-Prints one JSON line. `value` is decode frames/s; `roofline` is the weight-GEMV kernel's
-achieved HBM bandwidth: weight bytes at their stored precision (34/32 B per Q8_0 weight) over
-the GPU-side duration of every GEMV launch of every 64th timed step (earliest block start to
-latest wave end, stamped by the kernels on the GPU wall clock of the session's stream);
-`traffic` is the HBM bytes per GEMV launch that rocprofv3's FETCH_SIZE + WRITE_SIZE counters
-read, scaled by the same counters on a copy of known size (profiles/gemv_traffic_medium_q8.txt,
-when present); `cpu_baseline` times the oracle's CPU restatement of the reference decode step
-on the host for a bounded sample of the same workload.
+Prints one JSON line. `value` is decode frames/s over the timed steps (graph replays, nothing
+else in the timed region). After them, untimed, the launches of a few decode steps at the timed
+segment's middle stamp their spans on the GPU wall clock (earliest block start to latest wave
+end, on the session's own stream): `roofline` is the dominant kernel's achieved HBM bandwidth
+(algorithmic bytes per launch -- weights at their stored precision, 34/32 B per Q8_0 weight; for
+attention the f32 K and V of the keys attended -- over its average launch span), `kernels` the
+same for every projection and the attention; `traffic` is the HBM bytes per launch of that
+kernel that rocprofv3's FETCH_SIZE + WRITE_SIZE counters read, scaled by the same counters on a
+copy of known size (profiles/traffic_<workload>.txt, when present); `cpu_baseline` times the
+oracle's CPU restatement of the reference decode step on the host for a bounded sample of the
+same workload.
 """
 import argparse
 import ctypes
@@ -71,13 +76,13 @@ def step_bytes(c, wbpw, n_seq, n_ctx, u, requests=1, adapter_bytes=0.0):
     return w + adapter_bytes + kv_read + kv_write + xkv + Q * C * n_seq * 4
 
 
-def gemv_traffic(workload):
-    """HBM bytes per GEMV launch from the committed counter summary, or None."""
-    path = os.path.join(ROOT, "profiles", f"gemv_traffic_{workload.replace('-', '_')}.txt")
+def gemv_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` from the committed counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload.replace('-', '_')}.txt")
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(f"traffic_bytes_per_launch {kernel}:"):
                     return float(line.split(":", 1)[1])
     except OSError:
         return None
@@ -277,7 +282,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="medium-q8",
                     choices=sorted(WORKLOADS) + ["server-medium-q8", "t5-base", "encodec-decode"])
-    ap.add_argument("--profile-every", type=int, default=64)
+    ap.add_argument("--profile-steps", type=int, default=8,
+                    help="decode steps whose launches are timed on the GPU clock after the timed run (untimed)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prompt", type=int, default=None,
@@ -325,54 +331,101 @@ def main():
           f"{time.time() - t_build:.1f} s", file=sys.stderr, flush=True)
     S = T + c.n_q
     start = w["prompt"] + 1
+    D = S - start - 1                                      # decode steps of one continuation
+
+    def new_session():
+        ss = mgx.Batch(gm, reqs, w["prompt"]) if R > 1 else mgx.Session(gm, t5, prompt, w["prompt"], reqs[0]["params"])
+        hip_sync()
+        tp = time.perf_counter()
+        ss.step(1)                                         # prefill, outside the timed steps
+        prefill_s.append(time.perf_counter() - tp)
+        print(f"[bench] session prefilled ({start} tokens x {R} requests) in {prefill_s[-1]:.3f} s",
+              file=sys.stderr, flush=True)
+        return ss
+
+    def keys_now(ss):
+        return S - ss.remaining()                          # keys the next decode step attends
 
     timed = 0.0
     timed_steps = 0
     bytes_total = 0.0
-    gemv = [0.0, 0.0, 0]
-    attn = [0.0, 0.0, 0]
-    warm_left = args.warmup
-    sess = None
     prefill_s = []
+    segments = []
+    # One continuation holds D decode steps whose attended keys grow from start + 1 to S - 1. A
+    # run of fewer steps is centred on the continuation's middle, so its keys average what the
+    # whole continuation's do: the steps before it run untimed (the last `warmup` of them just
+    # before the timed ones).
+    sess = new_session()
+    lead = max(0, (D - args.steps) // 2 - args.warmup) if args.steps < D else 0
+    while lead > 0:
+        lead -= sess.step(min(lead, 256))
+    warm_left = args.warmup
     while timed_steps < args.steps:
-        if sess is None or sess.remaining() == 0:
-            if sess is not None:
-                for k, acc in ((0, gemv), (1, attn)):
-                    ms, by, n = sess.profile_read(k)
-                    acc[0] += ms; acc[1] += by; acc[2] += n
-                sess.close()
-            sess = mgx.Batch(gm, reqs, w["prompt"]) if R > 1 else mgx.Session(gm, t5, prompt, w["prompt"],
-                                                                               reqs[0]["params"])
-            hip_sync()
-            tp = time.perf_counter()
-            sess.step(1)                                   # prefill, outside the timed steps
-            prefill_s.append(time.perf_counter() - tp)
-            print(f"[bench] session prefilled ({start} tokens x {R} requests) in {prefill_s[-1]:.3f} s",
-                  file=sys.stderr, flush=True)
+        if sess.remaining() == 0:
+            sess.close()
+            sess = new_session()
         if warm_left > 0:
             warm_left -= sess.step(min(warm_left, sess.remaining()))
             continue
         n = min(args.steps - timed_steps, sess.remaining())
-        pos0 = S - sess.remaining() - 1                    # cache position of the first step
-        sess.profile(args.profile_every)
+        u0 = keys_now(sess)
         hip_sync()
         t0 = time.perf_counter()
         done = sess.step(n)
         hip_sync()
         timed += time.perf_counter() - t0
-        sess.profile(0)
         for i in range(done):
-            bytes_total += step_bytes(c, BPW[w["wtype"]], 2 * R, w["n_ctx"], pos0 + i + 1, R, adapter_bytes)
+            bytes_total += step_bytes(c, BPW[w["wtype"]], 2 * R, w["n_ctx"], u0 + i, R, adapter_bytes)
+        segments.append([u0, u0 + done - 1])
         timed_steps += done
         print(f"[bench] timed {timed_steps}/{args.steps} steps, {timed:.2f} s", file=sys.stderr, flush=True)
-    for k, acc in ((0, gemv), (1, attn)):
-        ms, by, nn = sess.profile_read(k)
-        acc[0] += ms; acc[1] += by; acc[2] += nn
+
+    # Launch timing after the timed segment, untimed and outside the captured graphs: every
+    # launch of `profile_steps` steps at the timed segment's middle keys (or right after it)
+    # stamps its span on the GPU clock.
+    kinds = {"gemv": 0, "attention": 1, "qkv": 2, "self.out": 3, "cross.q": 4, "cross.out": 5, "ff.0": 6,
+             "ff.2": 7, "heads": 8}
+    prof = {k: [0.0, 0.0, 0] for k in kinds}
+    P = max(0, args.profile_steps)
+    if P:
+        mid = (segments[0][0] + segments[-1][1]) // 2
+        if sess.remaining() < P:
+            sess.close()
+            sess = new_session()
+            skip = max(0, mid - P // 2 - keys_now(sess))
+            while skip > 0 and sess.remaining() > P:
+                skip -= sess.step(min(skip, 256, sess.remaining() - P))
+        prof_keys = keys_now(sess)
+        sess.profile(1)
+        sess.step(P)
+        sess.profile(0)
+        for k, kind in kinds.items():
+            ms, by, nn = sess.profile_read(kind)
+            prof[k] = [ms, by, nn]
     sess.close()
 
+    def rate(k):
+        ms, by, nn = prof[k]
+        if nn == 0 or ms <= 0:
+            return None
+        return dict(achieved=round(by / (ms * 1e-3) / 1e9, 1), launches_timed=nn,
+                    avg_launch_us=round(1000.0 * ms / nn, 3), bytes_per_launch=round(by / nn),
+                    frac=round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+
+    per_kernel = {k: rate(k) for k in kinds if k not in ("gemv",)}
+    timed_units = {k: v for k, v in per_kernel.items() if v is not None}
+    # the dominant kernel: the largest share of a profiled step's GPU time
+    dom = max(timed_units, key=lambda k: prof[k][0]) if timed_units else None
+    wname = {8: "Q8_0", 2: "Q4_0", 1: "F16", 0: "F32"}[w["wtype"]]
+    labels = {"qkv": f"k_gemv / k_gemv_mf self.qkv ({wname} weights, LayerNorm prologue, K/V append)",
+              "self.out": f"self.out GEMV ({wname}, residual)", "cross.q": f"cross.q GEMV ({wname}, LayerNorm)",
+              "cross.out": f"cross.out GEMV ({wname}, residual)",
+              "ff.0": f"ff.0 GEMV ({wname} weights, LayerNorm prologue, GELU epilogue)",
+              "ff.2": f"ff.2 GEMV ({wname}, residual)", "heads": f"output heads GEMV ({wname}, out_norm)",
+              "attention": "self-attention (f32 K/V of the keys attended, every stream)"}
     fps = R * timed_steps / timed                          # frames of every request
-    gemv_gbs = gemv[1] / (gemv[0] * 1e-3) / 1e9 if gemv[0] > 0 else 0.0
-    attn_gbs = attn[1] / (attn[0] * 1e-3) / 1e9 if attn[0] > 0 else 0.0
+    gemv_rate = rate("gemv")
+    keys_mean = sum((a + b) * (b - a + 1) / 2 for a, b in segments) / max(timed_steps, 1)
     out = {
         "metric": "LM frames/sec & HBM GB/s, MusicGen-medium Q8_0 CFG=2, 30 s continuation"
         if args.workload == "medium-q8" else f"LM frames/sec & HBM GB/s, {args.workload}",
@@ -388,18 +441,21 @@ def main():
         "dtype": {8: "int8xq8_0+f32", 2: "int8xq4_0+f32", 1: "f16+f32", 0: "f32"}[w["wtype"]],
         "data": "synthetic (seeded random N(0,0.02) weights, N(0,1) memory, uniform prompt codes)",
         "config": {"workload": w["desc"], "requests": R, "layers": c.layers, "dim": c.dim, "heads": c.heads,
-                   "ff_dim": c.ff_dim,
-                   "weights": {8: "Q8_0", 2: "Q4_0", 1: "F16", 0: "F32"}[w["wtype"]], "n_ctx": w["n_ctx"],
+                   "ff_dim": c.ff_dim, "weights": wname, "n_ctx": w["n_ctx"],
                    "prompt_frames": w["prompt"], "continuation_frames": w["gen"], "cfg_coef": 3.0, "top_k": 250,
                    "temperature": 1.0, "seed": w["seed"], "parallelism": "single GPU"},
+        "timed_keys": {"segments": segments, "mean": round(keys_mean, 1),
+                       "continuation_mean": round((start + 1 + S - 1) / 2, 1)},
         "hbm_gbs_step": round(bytes_total / timed / 1e9, 1),
         "roofline_frac_step": round(bytes_total / timed / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": gemv_traffic(args.workload),
-                     "kernel": "k_gemv (Q8_0 weight GEMV, all projections)", "launches_timed": gemv[2],
-                     "avg_launch_us": round(1000.0 * gemv[0] / max(gemv[2], 1), 3)},
-        "attention": {"achieved": round(attn_gbs, 1), "unit": "GB/s", "launches_timed": attn[2],
-                      "avg_launch_us": round(1000.0 * attn[0] / max(attn[2], 1), 3)},
+        "roofline": None if dom is None else {
+            "bound": "hbm", "achieved": timed_units[dom]["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": timed_units[dom]["frac"], "traffic": gemv_traffic(args.workload, dom),
+            "kernel": labels[dom], "launches_timed": timed_units[dom]["launches_timed"],
+            "avg_launch_us": timed_units[dom]["avg_launch_us"],
+            "bytes_per_launch": timed_units[dom]["bytes_per_launch"], "profiled_keys": prof_keys},
+        "gemv_family": gemv_rate,
+        "kernels": per_kernel,
         # the prompt's prefill (the loop's first forward, start tokens), outside `value`
         "prefill_ms": round(1000.0 * min(prefill_s), 2) if prefill_s else None,
     }

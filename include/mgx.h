@@ -229,7 +229,13 @@ void mgx_server_destroy(mgx_server* server);
    of every `every`-th loop iteration records its span on the GPU's constant-rate wall clock
    (earliest block start to latest wave end -- a kernel tracer's duration; for attention, the
    scores kernel's start to the reduce kernel's end). profile_read sums those milliseconds, the algorithmic bytes (weights at their stored
-   precision; f32 K and V of the keys attended) and the launch count. */
+   precision; f32 K and V of the keys attended) and the launch count, for one kind of launch:
+   MGX_PROF_GEMV every weight GEMV, MGX_PROF_ATTN the self-attention, or the GEMV of one
+   projection (its adapter's A x launch, if any, is not included). */
+enum {
+    MGX_PROF_GEMV = 0, MGX_PROF_ATTN = 1, MGX_PROF_QKV = 2, MGX_PROF_OUT = 3, MGX_PROF_CROSS_Q = 4,
+    MGX_PROF_CROSS_OUT = 5, MGX_PROF_FF0 = 6, MGX_PROF_FF2 = 7, MGX_PROF_HEADS = 8
+};
 int mgx_session_profile(mgx_session* session, int32_t every);
 int mgx_session_profile_read(mgx_session* session, int32_t kind, double* ms_total, double* bytes_total,
                              int32_t* launches);
