@@ -206,8 +206,9 @@ void launch_repack(int type, const uint8_t* raw, int64_t rows, int in, void* q, 
 void launch_rows(const DevMat& m, const int32_t* ids, int n, float* out, hipStream_t s);
 // RMS norm of ncol columns of n elements (stride apart): (x * (1 / sqrtf(mean(x^2) + eps))) * w
 void launch_rms(const float* x, int n, int ncol, int stride, const float* w, float eps, float* y, hipStream_t s);
-// bias[(h * seq + q) * seq + k] = table row buckets[q * seq + k], element h, + 0
-void launch_t5_bias(const DevMat& table, const int32_t* buckets, int seq, int heads, float* bias, hipStream_t s);
+// bias[(h * seq + q) * seq + k] = table row rel[k - q + zero], element h, + 0 (rel: the bucket
+// of each relative position key - query, position 0 at index zero)
+void launch_t5_bias(const DevMat& table, const int32_t* rel, int zero, int seq, int heads, float* bias, hipStream_t s);
 // ReLU of ncol columns of n f32 values into the activation form of the consumer's weights
 void launch_relu_act(const float* x, int n, int ncol, const ActBuf& dst, hipStream_t s);
 

@@ -2299,15 +2299,17 @@ void launch_rms(const float* x, int n, int ncol, int stride, const float* w, flo
     hipLaunchKernelGGL(k_rms, dim3(ncol), dim3(256), 0, s, x, n, stride, w, eps, y);
 }
 
-__global__ __launch_bounds__(256) void k_t5_bias(DevMat table, const int32_t* buckets, int seq, int heads,
+// bias[h][query][key] = table[bucket(key - query)][h]; rel[r] holds the bucket of relative
+// position r - zero.
+__global__ __launch_bounds__(256) void k_t5_bias(DevMat table, const int32_t* rel, int zero, int seq, int heads,
                                                  float* bias) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= seq * seq * heads) return;
-    const int h = i / (seq * seq), qk = i - h * seq * seq;
-    bias[i] = mat_elem(table, buckets[qk], h) + 0.0f;
+    const int h = i / (seq * seq), qk = i - h * seq * seq, qi = qk / seq, ki = qk - qi * seq;
+    bias[i] = mat_elem(table, rel[ki - qi + zero], h) + 0.0f;
 }
-void launch_t5_bias(const DevMat& table, const int32_t* buckets, int seq, int heads, float* bias, hipStream_t s) {
-    hipLaunchKernelGGL(k_t5_bias, dim3((seq * seq * heads + 255) / 256), dim3(256), 0, s, table, buckets, seq, heads,
+void launch_t5_bias(const DevMat& table, const int32_t* rel, int zero, int seq, int heads, float* bias, hipStream_t s) {
+    hipLaunchKernelGGL(k_t5_bias, dim3((seq * seq * heads + 255) / 256), dim3(256), 0, s, table, rel, zero, seq, heads,
                        bias);
 }
 

@@ -103,7 +103,7 @@ EXPORTS = ["mgx_model_create", "mgx_model_set_adapters", "mgx_model_destroy", "m
            "mgx_gguf_find_tensor", "mgx_gguf_u32", "mgx_gguf_f32", "mgx_gguf_string", "mgx_gguf_lm_config",
            "mgx_model_create_from_gguf", "mgx_model_set_adapters_from_gguf", "mgx_server_create",
            "mgx_server_generate", "mgx_server_stats", "mgx_server_destroy", "mgx_t5_create", "mgx_gguf_t5_config",
-           "mgx_t5_create_from_gguf", "mgx_t5_encode", "mgx_t5_destroy", "mgx_t5_relative_bucket", "mgx_codec_create",
+           "mgx_t5_create_from_gguf", "mgx_t5_encode", "mgx_t5_encode_static", "mgx_t5_destroy", "mgx_t5_relative_bucket", "mgx_codec_create",
            "mgx_gguf_codec_config", "mgx_codec_create_from_gguf", "mgx_codec_decode", "mgx_codec_decode_latent",
            "mgx_codec_destroy", "mgx_last_error"]
 

@@ -290,6 +290,16 @@ int mgx_t5_create(const mgx_t5_config* config, const mgx_tensor* tensors, int32_
 int mgx_gguf_t5_config(const mgx_gguf* file, mgx_t5_config* out);
 int mgx_t5_create_from_gguf(const mgx_gguf* file, mgx_t5** out);
 int mgx_t5_encode(mgx_t5* t5, const int32_t* ids, int32_t n_tokens, float* hidden_out);
+/* mgx_t5_encode without any allocation: every working buffer of the encode (ids, relative
+   buckets, hidden states, q / k / v, attention bias, activation forms) lives in one file-scope
+   device array of 32 MiB that each device running the call holds until the process ends. No
+   counterpart in the reference: it is for callers that cannot allocate device memory while
+   they run (tight serving loops, code around HIP graph capture). Same arguments and results as
+   mgx_t5_encode (bit for bit); MGX_ERR_INVALID when the encode needs more than 32 MiB
+   (about n_tokens * (2 dim + 6 heads*64 + 2 intermediate) * 4 + heads * n_tokens^2 * 4 bytes:
+   15 MiB for T5-base at 256 tokens). Calls share the array: calls that overlap on one device
+   race (the encoder's own lock serializes calls on one mgx_t5). */
+int mgx_t5_encode_static(mgx_t5* t5, const int32_t* ids, int32_t n_tokens, float* hidden_out);
 void mgx_t5_destroy(mgx_t5* t5);
 /* t5_relative_position_bucket (t5.h:46-61): relative_position = key - query. */
 int32_t mgx_t5_relative_bucket(int32_t relative_position, int32_t num_buckets, int32_t max_distance);
