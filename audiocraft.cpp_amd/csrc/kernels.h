@@ -13,10 +13,11 @@ enum { PRO_LN = 0, PRO_F32 = 1, PRO_ACT = 2 };
 // GEMV epilogues: store, residual add, q + KV-cache append, GELU then activation form.
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GELU_ACT = 3 };
 
-constexpr int ATT_CHUNK = 256;   // keys per attention chunk (fixes the reduction order)
-constexpr int ATT_MAX_CHUNKS = 16;  // capacity up to 4096 positions
-constexpr int ATT_SUB = 64;         // keys per score block
-constexpr int ATT_SUBS = ATT_CHUNK / ATT_SUB;
+constexpr int ATT_CHUNK = 64;       // keys per attention chunk (fixes the reduction order)
+constexpr int ATT_SPAN = 256;       // a step's attention grid covers whole 256-key spans (4 chunks),
+                                    // so one captured step graph serves 256 positions
+constexpr int ATT_MAX_SPANS = 16;   // capacity up to 4096 positions
+constexpr int ATT_MAX_CHUNKS = ATT_MAX_SPANS * ATT_SPAN / ATT_CHUNK;
 constexpr int MAX_CARD = 2048;   // sampler's LDS rows
 constexpr int MF_MAX_COLS = 64;  // matrix-core GEMV columns per launch (16-column groups; 16 with an adapter)
 
@@ -96,9 +97,9 @@ struct AttnArgs {
     const float* q;       // [col][dim]
     const float* k;       // [col][heads][cap][64]
     const float* v;       // [col][heads][cap][64]
-    float* scores;        // [col][heads][cap]
-    float* opart;         // [col][heads][max_chunks][64]
-    float* cmax;          // [col][heads][max_chunks * ATT_SUBS] score-block maxima
+    float* opart;         // [col][heads][max_chunks][64] each chunk's V.e
+    float* cmax;          // [col][heads][max_chunks] each chunk's score max
+    double* csum;         // [col][heads][max_chunks] each chunk's sum of e
     int dim, heads, cap, max_chunks, ncol;
     float scale;
     const int* pos;       // [request] device positions: column n attends keys [0, pos[n >> cshift]]
@@ -106,7 +107,7 @@ struct AttnArgs {
     int kv_cols;          // 0, or the cache column count when columns share caches (column n -> n % kv_cols)
     ActBuf out;           // the out-projection's activation
     float* out_f;         // optional f32 copy [col][dim] (an adapted out-projection's A x reads it)
-    unsigned long long* stamp;   // optional [64][2]: scores' earliest starts, reduce's latest ends
+    unsigned long long* stamp;   // optional [64][2]: the chunk kernel's earliest starts, the combine's latest ends
 };
 
 // One block per (head, request r): q + r*dim, k / v + r*heads*n_ctx*64, output column r.
@@ -172,7 +173,10 @@ void launch_scales_t(const DevMat& w, uint16_t* dt, hipStream_t s);
 void launch_weights_mf(const DevMat& w, int8_t* qm, hipStream_t s);
 // the Q4_0 operand-order copy (one word of 8 nibbles per lane and block) for a Q4_0 matrix
 void launch_weights_mf4(const DevMat& w, uint32_t* qm, hipStream_t s);
-// nch: the 256-key chunks of the position the launch runs at (the grid covers exactly these)
+// Self-attention in two launches: one block per (64-key chunk, head, column) for the chunk's
+// max, sum and V.e, then one wave per (head, column) combining the chunks. nch: the chunks the
+// grid covers (at least those of the largest position in the launch; a block past its column's
+// position exits at once).
 void launch_attention(const AttnArgs& a, int nch, hipStream_t s);
 void launch_xattn(const XAttnArgs& a, int heads, int n_req, hipStream_t s);
 void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s);

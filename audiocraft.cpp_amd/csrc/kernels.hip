@@ -10,11 +10,13 @@
 //   * F16 / F32 GEMV: the same with 8-element chunks and fmaf;
 //   * LayerNorm: 256 double partials (partial i sums float4 groups i, i+256, ... in element
 //     order), butterfly, (x-mean)*(1/sqrtf(var+eps))*w+b;
-//   * attention: keys in chunks of 256; q.k as 16 four-dim fmaf partials + butterfly;
-//     softmax sum in double per chunk (butterfly), chunks added in order; V as 16 key-strided
-//     partials per chunk + butterfly, chunk results added in order;
-//   * exp / erf: this file's own double routines (Cody-Waite + Taylor; Taylor / continued
-//     fraction), rounded to f32 once.
+//   * attention: keys in chunks of 256; q.k as 16 four-dim fmaf partials + butterfly; per
+//     chunk its max m, e = expf(s - m), the sum of e in double (butterfly) and V.e as 16
+//     key-strided partials + butterfly; the chunks combined in order by their weights
+//     exp(m - max) in double: total = sum(sum * weight), output = sum fmaf(V.e, (float)(weight
+//     / total), .);
+//   * exp / erf: this file's own double routines (Cody-Waite + Taylor; two Chebyshev
+//     interpolants), rounded to f32 once.
 //
 // The reference computes the same steps through ggml (src/mg/lm.h:152-259, src/nn.h:186-191,
 // src/ac/transformer.h:28-38, src/mg/sampling.h:32-105).
@@ -58,36 +60,38 @@ __device__ double dexp(double x) {
 }
 __device__ __forceinline__ float dexpf(float x) { return (float)dexp((double)x); }
 
-__device__ __constant__ double ERF_TAYLOR[30] = {
-    1.0, -0.3333333333333333, 0.1, -0.023809523809523808,
-    0.004629629629629629, -0.0007575757575757576, 0.00010683760683760684, -1.3227513227513228e-05,
-    1.4589169000933706e-06, -1.4503852223150468e-07, 1.3122532963802806e-08, -1.0892221037148573e-09,
-    8.35070279514724e-11, -5.9477940136376354e-12, 3.9554295164585257e-13, -2.466827010264457e-14,
-    1.4483264643598138e-15, -8.032735012415773e-17, 4.221407288807088e-18, -2.107855191442136e-19,
-    1.0025164934907719e-20, -4.5518467589282e-22, 1.977064753877905e-23, -8.230149299214221e-25,
-    3.289260349175752e-26, -1.2641078988989164e-27, 4.6784835155184856e-29, -1.669761793417372e-30,
-    5.754191643982172e-32, -1.9169428621097826e-33};
+// erf: two Chebyshev interpolants in monomial form (erf_coeffs.py derives them from 40-digit
+// values): |x| < 1: x * P(2x^2 - 1), P of degree 11; 1 <= |x| < 4: 1 - Q(|x| * 2/3 - 5/3), Q
+// (erfc on [1, 4]) of degree 20; +-1 beyond. Absolute error below 1.5e-15 and 1.3e-12.
+__device__ __constant__ double ERF_P[12] = {
+    0x1.ee51eb23cb7ebp-1, -0x1.1fd162921520ep-3, 0x1.454368017b319p-6,
+    -0x1.2b902b7b26e28p-9, 0x1.c82aa24968f47p-13, -0x1.263991d3aca15p-16,
+    0x1.4866394fa4c3ep-20, -0x1.429e4c163b13bp-24, 0x1.1ad503d95b599p-28,
+    -0x1.c02cc0da54c52p-33, 0x1.4424c09b26e7bp-37, -0x1.2d4c29f5686cbp-42};
+__device__ __constant__ double ERF_Q[21] = {
+    0x1.aab859b20b140p-12, -0x1.ac44a2cdb3c80p-9, 0x1.9180586b55ae8p-7,
+    -0x1.cdb9fd59ee319p-6, 0x1.65964ef5668ffp-5, -0x1.7c8c5ebf7f0ccp-5,
+    0x1.0521f53919ddep-5, -0x1.2faaceec90308p-7, -0x1.b5d2183e391e9p-8,
+    0x1.3b371adacbf70p-7, -0x1.29d400459d61ep-8, -0x1.ca1cf08ac8d5dp-12,
+    0x1.df3c4bd10ee4ep-10, -0x1.e7099cc2c7d56p-11, -0x1.d14ddd0a26b51p-15,
+    0x1.3dc0c2909a110p-12, -0x1.e193532b72642p-14, -0x1.3af7b90db0f1ap-15,
+    0x1.17a5709f8fe8ap-15, 0x1.048f70bb1e4f4p-20, -0x1.e180cb94805c1p-19};
 
-// erf: Taylor series below |x| = 2, the Laplace continued fraction for erfc (forward
-// three-term recurrence, 50 terms) up to 6, +-1 beyond.
 __device__ double derf(double x) {
     const double ax = __builtin_fabs(x);
-    if (ax < 2.0) {
-        const double t = x * x;
-        double p = ERF_TAYLOR[29];
-        for (int n = 28; n >= 0; --n) p = __builtin_fma(p, t, ERF_TAYLOR[n]);
-        return (x * p) * 1.1283791670955126;
+    if (ax < 1.0) {
+        const double t = __builtin_fma(2.0 * x, x, -1.0);
+        double p = ERF_P[11];
+#pragma unroll
+        for (int n = 10; n >= 0; --n) p = __builtin_fma(p, t, ERF_P[n]);
+        return x * p;
     }
-    if (ax >= 6.0) return x > 0 ? 1.0 : -1.0;
-    double am2 = 1.0, am1 = 0.0, bm2 = 0.0, bm1 = 1.0;
-    for (int n = 1; n <= 50; ++n) {
-        const double a = (n == 1) ? 1.0 : 0.5 * (double)(n - 1);
-        const double A = __builtin_fma(ax, am1, a * am2);
-        const double B = __builtin_fma(ax, bm1, a * bm2);
-        am2 = am1; am1 = A; bm2 = bm1; bm1 = B;
-    }
-    const double erfc = (dexp(-(ax * ax)) * 0.5641895835477563) * (am1 / bm1);
-    const double r = 1.0 - erfc;
+    if (ax >= 4.0) return x > 0 ? 1.0 : -1.0;
+    const double t = __builtin_fma(ax, 0x1.5555555555555p-1, -0x1.aaaaaaaaaaaabp+0);
+    double p = ERF_Q[20];
+#pragma unroll
+    for (int n = 19; n >= 0; --n) p = __builtin_fma(p, t, ERF_Q[n]);
+    const double r = 1.0 - p;
     return x > 0 ? r : -r;
 }
 
@@ -791,242 +795,138 @@ __device__ __forceinline__ float halving4(const float (&p)[4], int t) {
     return b + shfl_xor(b, 1);
 }
 
-// Scores of one 64-key block (16 lanes per key, four dims each; 16 keys per pass) and the
-// block's max (-inf when it holds no key yet), into cmax[head][block].
-__global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
+// The 16 key-strided partials of a chunk's V.e, lane l of a wave holding partials (l >> 4) + 4k
+// for k = 0..3 (P[k]) and dimensions 4 (l & 15) .. + 3: the butterfly off 8 and 4 in registers,
+// 2 and 1 across lanes 32 and 16 apart; lanes 0-15 end with the chunk's 64 outputs.
+__device__ __forceinline__ float4 fold_partials16(const float4 (&P)[4]) {
+    float4 a0 = make_float4(P[0].x + P[2].x, P[0].y + P[2].y, P[0].z + P[2].z, P[0].w + P[2].w);
+    const float4 a1 = make_float4(P[1].x + P[3].x, P[1].y + P[3].y, P[1].z + P[3].z, P[1].w + P[3].w);
+    a0 = make_float4(a0.x + a1.x, a0.y + a1.y, a0.z + a1.z, a0.w + a1.w);
+    a0.x = a0.x + take_up<32>(a0.x); a0.y = a0.y + take_up<32>(a0.y);
+    a0.z = a0.z + take_up<32>(a0.z); a0.w = a0.w + take_up<32>(a0.w);
+    a0.x = a0.x + take_up<16>(a0.x); a0.y = a0.y + take_up<16>(a0.y);
+    a0.z = a0.z + take_up<16>(a0.z); a0.w = a0.w + take_up<16>(a0.w);
+    return a0;
+}
+
+// One 64-key chunk of one (head, column): 256 threads. Every load is issued up front (keys past
+// the position re-read the last key: a cache hit, never a stale row): K as 16 lanes per key
+// (four dims each), key 16*it + 4*wave + g for it = 0..3; V as 16 key-strided partials p =
+// tid / 16 (keys p, p + 16, p + 32, p + 48) by 16 dimension quads. Scores: 16 four-dim fmaf
+// partials folded by the butterfly, times the scale. The chunk's max m; e = expf(s - m) (0 past
+// the position) in LDS; the chunk's sum of e in double by the 64-wide butterfly; o = sum e v as
+// the 16 key-strided fmaf partials folded by the butterfly. Writes o [64], m and the sum; a
+// chunk wholly past the column's position writes nothing (the combine reads only chunks that
+// exist).
+__global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     const unsigned long long t0 = stamp_begin(a.stamp);
-    const int b = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
-    const int u = a.pos[n >> a.cshift] + 1;
+    const int c = blockIdx.x, h = blockIdx.y, n = blockIdx.z, j0 = c * ATT_CHUNK;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, t = lane & 15;
     const size_t head = (size_t)n * a.heads + h;
-    const float* K = a.k + ((size_t)(a.kv_cols ? n % a.kv_cols : n) * a.heads + h) * a.cap * 64;
-    float* S = a.scores + head * a.cap;
+    const size_t kvh = ((size_t)(a.kv_cols ? n % a.kv_cols : n) * a.heads + h) * a.cap * 64 + (size_t)j0 * 64;
+    const float* K = a.k + kvh;
+    const float* V = a.v + kvh;
     __shared__ float red_f[4];
+    __shared__ float el[ATT_CHUNK];
+    __shared__ float4 vred[16][16];
+    // The chunk's 64 rows are loaded before the position is known (they lie inside the cache's
+    // rows, which cover whole 256-key spans); rows past the position only ever enter masked
+    // lanes, so their contents never reach a result.
     const float4 q = ((const float4*)(a.q + (size_t)n * a.dim + h * 64))[t];
     float4 kv[4];
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        // keys past the position re-read the last key (a cache hit, not HBM traffic)
-        const int j = b * ATT_SUB + it * 16 + wave * 4 + g, jl = j < u ? j : u - 1;
-        kv[it] = ((const float4*)(K + (size_t)jl * 64))[t];
+    for (int it = 0; it < 4; ++it) kv[it] = ((const float4*)(K + (size_t)(it * 16 + wave * 4 + g) * 64))[t];
+    const int pv = tid >> 4, dq = tid & 15;
+    float4 vv[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) vv[m] = ((const float4*)(V + (size_t)(pv + 16 * m) * 64))[dq];
+    const int u = a.pos[n >> a.cshift] + 1;
+    if (j0 >= u) {
+        if (a.stamp && threadIdx.x == 0) atomicMin(stamp_sub(a.stamp), t0);
+        return;
     }
-    float p[4];
+    const int uc = u - j0 < ATT_CHUNK ? u - j0 : ATT_CHUNK;
+    float pr[4];
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         float v = __builtin_fmaf(q.x, kv[it].x, 0.0f);
         v = __builtin_fmaf(q.y, kv[it].y, v);
         v = __builtin_fmaf(q.z, kv[it].z, v);
-        p[it] = __builtin_fmaf(q.w, kv[it].w, v);
+        pr[it] = __builtin_fmaf(q.w, kv[it].w, v);
     }
-    const int jt = b * ATT_SUB + (2 * ((t >> 3) & 1) + ((t >> 2) & 1)) * 16 + wave * 4 + g;
-    const float sc = halving4(p, t) * a.scale;
-    float mx = -__builtin_inff();
-    if (jt < u) {
-        if ((t & 3) == 0) S[jt] = sc;
-        mx = sc;
-    }
+    // lanes t .. t ^ 3 hold key 16 * (2*((t>>3)&1) + ((t>>2)&1)) + 4 * wave + g
+    const int jt = (2 * ((t >> 3) & 1) + ((t >> 2) & 1)) * 16 + wave * 4 + g;
+    const float sc = halving4(pr, t) * a.scale;
+    float mx = jt < uc ? sc : -__builtin_inff();
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(mx, off); mx = mx > o ? mx : o; }
     if (lane == 0) red_f[wave] = mx;
     lds_barrier();
-    if (tid == 0) {
-        float m = red_f[0];
-        for (int w = 1; w < 4; ++w) m = m > red_f[w] ? m : red_f[w];
-        a.cmax[head * a.max_chunks * ATT_SUBS + b] = m;
+    float m = red_f[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) m = m > red_f[w] ? m : red_f[w];
+    if ((t & 3) == 0) el[jt] = jt < uc ? dexpf(sc - m) : 0.0f;
+    lds_barrier();
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+        const int j = pv + 16 * mm;
+        if (j < uc) {
+            const float e = el[j];
+            acc.x = __builtin_fmaf(e, vv[mm].x, acc.x);
+            acc.y = __builtin_fmaf(e, vv[mm].y, acc.y);
+            acc.z = __builtin_fmaf(e, vv[mm].z, acc.z);
+            acc.w = __builtin_fmaf(e, vv[mm].w, acc.w);
+        }
+    }
+    vred[pv][dq] = acc;
+    const double sum = wave == 0 ? fold64d_b((double)el[lane]) : 0.0;
+    lds_barrier();
+    if (wave == 0) {
+        float4 P[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) P[k] = vred[g + 4 * k][t];
+        const float4 o = fold_partials16(P);
+        if (lane < 16) ((float4*)(a.opart + (head * a.max_chunks + c) * 64))[lane] = o;
+        if (lane == 0) {
+            a.cmax[head * a.max_chunks + c] = m;
+            a.csum[head * a.max_chunks + c] = sum;
+        }
     }
     if (a.stamp && threadIdx.x == 0) atomicMin(stamp_sub(a.stamp), t0);
 }
 
-// Softmax + this chunk's share of V^T p, one block of 64*WAVES threads per (chunk, head,
-// stream); NCH = the position's chunk count. Every block rebuilds the head's normalizer:
-// global max from the score-block maxima, e = expf(s - max) for every key (spread over all
-// the block's threads), per-chunk double sums in the 256-key butterfly, chunks added in
-// order, p = e * (float)(1/sum). V (waves 0-3): partial g = key mod 16 (g = 4*wave +
-// lane/16), lane%16 -> dims 4*(lane%16)..+3, keys in increasing order, then the 16 partials
-// folded. Every load is issued before the first use (cache rows exist up to the chunk end).
-template <int NCH, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void k_attn_pv(AttnArgs a) {
-    constexpr int NT = 64 * WAVES, PER = (NCH * ATT_CHUNK + NT - 1) / NT;
-    const int c = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const size_t head = (size_t)n * a.heads + h;
-    const float* S = a.scores + head * a.cap;
-    __shared__ float el[NCH * ATT_CHUNK];
-    __shared__ float4 vred[16][16];
-    float sv[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int j = tid + NT * i;
-        sv[i] = S[j < NCH * ATT_CHUNK ? j : 0];
-    }
-    float cm[NCH * ATT_SUBS];
-#pragma unroll
-    for (int i = 0; i < NCH * ATT_SUBS; ++i) cm[i] = a.cmax[head * a.max_chunks * ATT_SUBS + i];
-    const int g = (wave & 3) * 4 + (lane >> 4), dq = lane & 15;
-    const float* V = a.v + ((size_t)(a.kv_cols ? n % a.kv_cols : n) * a.heads + h) * a.cap * 64;
-    float4 vv[16];
-    const int u = a.pos[n >> a.cshift] + 1;
-    if (wave < 4) {
-        // keys past the position re-read the last key (a cache hit, not HBM traffic)
-#pragma unroll
-        for (int m = 0; m < 16; ++m) {
-            const int j = c * ATT_CHUNK + g + 16 * m, jl = j < u ? j : u - 1;
-            vv[m] = ((const float4*)(V + (size_t)jl * 64))[dq];
-        }
-    }
-    float M = cm[0];
-#pragma unroll
-    for (int i = 1; i < NCH * ATT_SUBS; ++i) M = M > cm[i] ? M : cm[i];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int j = tid + NT * i;
-        if (j < NCH * ATT_CHUNK) el[j] = j < u ? dexpf(sv[i] - M) : 0.0f;
-    }
-    lds_barrier();
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (wave < 4) {
-        // every V wave folds every chunk (off 128, 64 from LDS, 32..1 in-wave), chunks added in order
-        double cs[NCH];
-#pragma unroll
-        for (int cc = 0; cc < NCH; ++cc) {
-            const float* e = el + cc * ATT_CHUNK;
-            cs[cc] = fold64d_b(((double)e[lane] + (double)e[lane + 128]) + ((double)e[lane + 64] + (double)e[lane + 192]));
-        }
-        double total = 0.0;
-#pragma unroll
-        for (int cc = 0; cc < NCH; ++cc) total = total + cs[cc];
-        const float inv = (float)(1.0 / total);
-        const int u_c = u - c * ATT_CHUNK;   // keys of this chunk that exist
-#pragma unroll
-        for (int m = 0; m < 16; ++m) {
-            const int jj = g + 16 * m;
-            if (jj < u_c) {
-                const float pm = el[c * ATT_CHUNK + jj] * inv;
-                acc.x = __builtin_fmaf(pm, vv[m].x, acc.x);
-                acc.y = __builtin_fmaf(pm, vv[m].y, acc.y);
-                acc.z = __builtin_fmaf(pm, vv[m].z, acc.z);
-                acc.w = __builtin_fmaf(pm, vv[m].w, acc.w);
-            }
-        }
-        vred[g][dq] = acc;
-    }
-    lds_barrier();
-    if (wave < 2) {
-        const float4 o = vred[g + 8][dq];
-        vred[g][dq] = make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
-    }
-    lds_barrier();
-    if (wave == 0) {
-        // g = lane/16 here: level 4 from LDS, levels 2 and 1 are lanes 32 and 16 apart
-        const float4 sv4 = vred[g][dq], o = vred[g + 4][dq];
-        float4 r = make_float4(sv4.x + o.x, sv4.y + o.y, sv4.z + o.z, sv4.w + o.w);
-        r.x = r.x + take_up<32>(r.x); r.y = r.y + take_up<32>(r.y); r.z = r.z + take_up<32>(r.z); r.w = r.w + take_up<32>(r.w);
-        r.x = r.x + take_up<16>(r.x); r.y = r.y + take_up<16>(r.y); r.z = r.z + take_up<16>(r.z); r.w = r.w + take_up<16>(r.w);
-        if (lane < 16) ((float4*)(a.opart + (head * a.max_chunks + c) * 64))[dq] = r;
-    }
-}
-
-// Wide launches (prefill groups): the softmax once per (head, column) instead of once per
-// chunk block. The same values in the same order as k_attn_pv builds them: global max from the
-// score-block maxima, e = expf(s - max) (0 past the position) written over the scores, each
-// 256-key chunk's sum in double by the butterfly, chunks added in order, and (float)(1 / total)
-// into the head's first score-block maximum slot.
-template <int NCH>
-__global__ __launch_bounds__(256) void k_attn_soft(AttnArgs a) {
-    const int h = blockIdx.x, n = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const size_t head = (size_t)n * a.heads + h;
-    float* S = a.scores + head * a.cap;
-    float* cmh = a.cmax + head * a.max_chunks * ATT_SUBS;
-    const int u = a.pos[n >> a.cshift] + 1;
-    __shared__ float el[NCH * ATT_CHUNK];
-    __shared__ double cs[NCH];
-    float M = cmh[0];
-#pragma unroll
-    for (int i = 1; i < NCH * ATT_SUBS; ++i) M = M > cmh[i] ? M : cmh[i];
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-        const int j = tid + ATT_CHUNK * i;
-        const float e = j < u ? dexpf(S[j] - M) : 0.0f;
-        el[j] = e;
-        S[j] = e;
-    }
-    lds_barrier();
-    for (int cc = wave; cc < NCH; cc += 4) {
-        const float* e = el + cc * ATT_CHUNK;
-        const double r = fold64d_b(((double)e[lane] + (double)e[lane + 128]) + ((double)e[lane + 64] + (double)e[lane + 192]));
-        if (lane == 0) cs[cc] = r;
-    }
-    lds_barrier();
-    if (tid == 0) {
-        double total = 0.0;
-        for (int cc = 0; cc < NCH; ++cc) total = total + cs[cc];
-        cmh[0] = (float)(1.0 / total);
-    }
-}
-
-// Softmax.V of one chunk after k_attn_soft: p = e * inv from the rewritten scores; V as in
-// k_attn_pv (partial g = key mod 16, keys in increasing order, the 16 partials folded).
-__global__ __launch_bounds__(256) void k_attn_pv_e(AttnArgs a) {
-    const int c = blockIdx.x, h = blockIdx.y, n = blockIdx.z;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const size_t head = (size_t)n * a.heads + h;
-    const float* S = a.scores + head * a.cap;
-    const float inv = a.cmax[head * a.max_chunks * ATT_SUBS];
-    __shared__ float el[ATT_CHUNK];
-    __shared__ float4 vred[16][16];
-    const int g = wave * 4 + (lane >> 4), dq = lane & 15;
-    const float* V = a.v + ((size_t)(a.kv_cols ? n % a.kv_cols : n) * a.heads + h) * a.cap * 64;
-    const int u = a.pos[n >> a.cshift] + 1;
-    float4 vv[16];
-#pragma unroll
-    for (int m = 0; m < 16; ++m) {
-        const int j = c * ATT_CHUNK + g + 16 * m, jl = j < u ? j : u - 1;
-        vv[m] = ((const float4*)(V + (size_t)jl * 64))[dq];
-    }
-    el[tid] = S[c * ATT_CHUNK + tid];
-    lds_barrier();
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    const int u_c = u - c * ATT_CHUNK;
-#pragma unroll
-    for (int m = 0; m < 16; ++m) {
-        const int jj = g + 16 * m;
-        if (jj < u_c) {
-            const float pm = el[jj] * inv;
-            acc.x = __builtin_fmaf(pm, vv[m].x, acc.x);
-            acc.y = __builtin_fmaf(pm, vv[m].y, acc.y);
-            acc.z = __builtin_fmaf(pm, vv[m].z, acc.z);
-            acc.w = __builtin_fmaf(pm, vv[m].w, acc.w);
-        }
-    }
-    vred[g][dq] = acc;
-    lds_barrier();
-    if (wave < 2) {
-        const float4 o = vred[g + 8][dq];
-        vred[g][dq] = make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
-    }
-    lds_barrier();
-    if (wave == 0) {
-        const float4 sv4 = vred[g][dq], o = vred[g + 4][dq];
-        float4 r = make_float4(sv4.x + o.x, sv4.y + o.y, sv4.z + o.z, sv4.w + o.w);
-        r.x = r.x + take_up<32>(r.x); r.y = r.y + take_up<32>(r.y); r.z = r.z + take_up<32>(r.z); r.w = r.w + take_up<32>(r.w);
-        r.x = r.x + take_up<16>(r.x); r.y = r.y + take_up<16>(r.y); r.z = r.z + take_up<16>(r.z); r.w = r.w + take_up<16>(r.w);
-        if (lane < 16) ((float4*)(a.opart + (head * a.max_chunks + c) * 64))[dq] = r;
-    }
-}
-
-// Chunk results added in order; the head's 64 outputs go to the out-projection activation.
-__global__ __launch_bounds__(64) void k_attn_reduce(AttnArgs a) {
+// The chunks of one (head, column) combined: lane c holds chunk c; M = max m_c, w_c =
+// exp((double)m_c - M), total = the 64-wide butterfly of S_c * w_c (zeros past the column's
+// chunks), f_c = (float)(w_c / total); lane d then sums fmaf(o_c[d], f_c, .) over the chunks in
+// order. The head's 64 outputs go to the out-projection's activation.
+__global__ __launch_bounds__(64) void k_attn_combine(AttnArgs a) {
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
-    const int u = a.pos[n >> a.cshift] + 1, nch = (u + ATT_CHUNK - 1) / ATT_CHUNK;
-    const size_t head = (size_t)n * a.heads + h;
-    float part[ATT_MAX_CHUNKS];
+    const size_t head = (size_t)n * a.heads + h, hc = head * a.max_chunks;
+    // every chunk slot of the head is loaded before the position is known; slots past the
+    // column's chunks are never used
+    const int cl = lane < a.max_chunks ? lane : a.max_chunks - 1;
+    const float mc0 = a.cmax[hc + cl];
+    const double sc0 = a.csum[hc + cl];
+    const float* op = a.opart + hc * 64 + lane;
+    float o[ATT_MAX_CHUNKS];
 #pragma unroll
-    for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc)
-        part[cc] = cc < nch ? a.opart[(head * a.max_chunks + cc) * 64 + lane] : 0.0f;
+    for (int k = 0; k < ATT_MAX_CHUNKS; ++k) o[k] = op[(size_t)(k < a.max_chunks ? k : a.max_chunks - 1) * 64];
+    const int u = a.pos[n >> a.cshift] + 1, nch = (u + ATT_CHUNK - 1) / ATT_CHUNK;
+    const bool live = lane < nch;
+    const float mc = live ? mc0 : -__builtin_inff();
+    float M = mc;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) { const float x = shfl_xor(M, off); M = M > x ? M : x; }
+    const double w = live ? dexp((double)mc - (double)M) : 0.0;
+    const double total = fold64d_b(live ? sc0 * w : 0.0);
+    const float f = live ? (float)(w / total) : 0.0f;
     float r = 0.0f;
 #pragma unroll
-    for (int cc = 0; cc < ATT_MAX_CHUNKS; ++cc)
-        if (cc < nch) r = r + part[cc];
+    for (int k = 0; k < ATT_MAX_CHUNKS; ++k) {
+        const float fk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), k));
+        r = k < nch ? __builtin_fmaf(o[k], fk, r) : r;
+    }
     put_act(a.out, n, h * 64 + lane, r, lane);
     if (a.out_f) a.out_f[(size_t)n * a.dim + h * 64 + lane] = r;
     if (a.stamp && lane == 0) atomicMax(stamp_sub(a.stamp) + 1, (unsigned long long)wall_clock64());
@@ -1036,90 +936,96 @@ __global__ __launch_bounds__(64) void k_attn_reduce(AttnArgs a) {
 // cross-attention of the conditional stream over the projected memory (lm.h:181-199).
 // The null stream's memory is zero, so its block output is exactly zero and is skipped.
 // ------------------------------------------------------------------------------------
-// One head's cross-attention by a 256-thread group (threads 0..255 of the block): n_ctx <= 16
-// * KEYQ keys of one 256-key chunk. Scores: 16 lanes per key (four dims each), 16 keys per pass;
-// after the halving reduce thread (wave, g, t) holds key 16t + 4*wave + g. V: partial g16 = key
-// mod 16, lane%16 -> dims 4*(lane%16)..+3. q: the head's 64 values (global memory or LDS).
-// Output column r, elements h*64..h*64+63 of `out` (and of out_f when set). Every thread of
-// the block must call it (it holds block barriers); threads >= 256 only take part in those.
-template <int KEYQ>
+// One head's attention over nc <= 256 keys (the projected memory, or a T5 prompt) by 256
+// threads: wave w takes the 64-key chunk w. Scores: 16 lanes per key (four dims each), key 64w +
+// 4*it + g for it = 0..15, folded by the butterfly (after the halving reduce lane t holds it =
+// t), times the scale, plus the bias row when given. Per chunk: its max m, e = expf(s - m), the
+// sum of e in double by the 64-wide butterfly, V.e as 16 key-strided partials (lane l holds
+// partials (l >> 4) + 4k, dims 4 (l & 15)..+3) folded by the butterfly. Wave 0 combines the
+// chunks as the self-attention combine does. q: the head's 64 values. Output column r, elements
+// h*64..h*64+63 of `out` (and of out_f when set); nc == 0 writes zeros.
 __device__ __forceinline__ void xattn_head(const float* qh, const float* K, const float* V, int nc, float scale,
                                            const float* bias, const ActBuf& out, float* out_f, int dim, int h,
                                            int r) {
+    __shared__ float cm[4];
+    __shared__ double cs[4];
+    __shared__ float4 co[4][16];
     __shared__ float el[256];
-    __shared__ float red_f[4];
-    __shared__ float4 vred[16][16];
-    __shared__ float ol[64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, t = lane & 15;
-    const bool act = tid < 256;
-    const int g16 = (wave & 3) * 4 + g, dq = lane & 15;
-    float4 kv[KEYQ], vv[KEYQ];
-#pragma unroll
-    for (int it = 0; it < KEYQ; ++it) {
-        const int j = it * 16 + (wave & 3) * 4 + g;
-        kv[it] = act && j < nc ? ((const float4*)(K + (size_t)j * 64))[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
-#pragma unroll
-    for (int m = 0; m < KEYQ; ++m) {
-        const int j = g16 + 16 * m;
-        vv[m] = act && j < nc ? ((const float4*)(V + (size_t)j * 64))[dq] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
+    const int j0 = wave * 64, uc = nc - j0 < 64 ? nc - j0 : 64;   // this wave's chunk holds uc keys
+    const bool has = uc > 0;
+    float4 kv[16], vv[16];
     const float4 q = ((const float4*)qh)[t];
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+        const int j = it * 4 + g, jl = j < uc ? j : uc - 1;
+        kv[it] = has ? ((const float4*)(K + (size_t)(j0 + jl) * 64))[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+            const int j = g + 4 * k + 16 * mm, jl = j < uc ? j : uc - 1;
+            vv[4 * k + mm] = has ? ((const float4*)(V + (size_t)(j0 + jl) * 64))[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
     float p[16];
 #pragma unroll
     for (int it = 0; it < 16; ++it) {
-        if (it < KEYQ) {
-            float v = __builtin_fmaf(q.x, kv[it].x, 0.0f);
-            v = __builtin_fmaf(q.y, kv[it].y, v);
-            v = __builtin_fmaf(q.z, kv[it].z, v);
-            p[it] = __builtin_fmaf(q.w, kv[it].w, v);
-        } else {
-            p[it] = 0.0f;
-        }
+        float v = __builtin_fmaf(q.x, kv[it].x, 0.0f);
+        v = __builtin_fmaf(q.y, kv[it].y, v);
+        v = __builtin_fmaf(q.z, kv[it].z, v);
+        p[it] = __builtin_fmaf(q.w, kv[it].w, v);
     }
-    const int jt = t * 16 + (wave & 3) * 4 + g;
+    const int jt = 4 * t + g;   // this lane's key after the halving reduce
     float sc = halving16(p, t) * scale;
-    if (bias && jt < nc) sc = sc + bias[jt];
-    float mx = jt < nc ? sc : -__builtin_inff();
+    if (bias && jt < uc) sc = sc + bias[j0 + jt];
+    float m = jt < uc ? sc : -__builtin_inff();
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(mx, off); mx = mx > o ? mx : o; }
-    if (act && lane == 0) red_f[wave] = mx;
+    for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(m, off); m = m > o ? m : o; }
+    el[j0 + jt] = jt < uc ? dexpf(sc - m) : 0.0f;
     lds_barrier();
-    float M = red_f[0];
-    for (int w = 1; w < 4; ++w) M = M > red_f[w] ? M : red_f[w];
-    if (act) el[jt] = jt < nc ? dexpf(sc - M) : 0.0f;
-    lds_barrier();
-    // the 256-key sum in double (butterfly), every wave; p = e * (float)(1/sum)
-    const double es = ((double)el[lane] + (double)el[lane + 128]) + ((double)el[lane + 64] + (double)el[lane + 192]);
-    const float inv = (float)(1.0 / (0.0 + fold64d_b(es)));
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const double sum = fold64d_b((double)el[j0 + lane]);
+    float4 P[4];
 #pragma unroll
-    for (int m = 0; m < KEYQ; ++m) {
-        const int j = g16 + 16 * m;
-        if (j < nc) {
-            const float pm = el[j] * inv;
-            acc.x = __builtin_fmaf(pm, vv[m].x, acc.x);
-            acc.y = __builtin_fmaf(pm, vv[m].y, acc.y);
-            acc.z = __builtin_fmaf(pm, vv[m].z, acc.z);
-            acc.w = __builtin_fmaf(pm, vv[m].w, acc.w);
+    for (int k = 0; k < 4; ++k) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+            const int j = g + 4 * k + 16 * mm;
+            if (j < uc) {
+                const float e = el[j0 + j];
+                acc.x = __builtin_fmaf(e, vv[4 * k + mm].x, acc.x);
+                acc.y = __builtin_fmaf(e, vv[4 * k + mm].y, acc.y);
+                acc.z = __builtin_fmaf(e, vv[4 * k + mm].z, acc.z);
+                acc.w = __builtin_fmaf(e, vv[4 * k + mm].w, acc.w);
+            }
         }
+        P[k] = acc;
     }
-    if (act) vred[g16][dq] = acc;
-    lds_barrier();
-    if (act && g16 < 8) {
-        const float4 o = vred[g16 + 8][dq];
-        vred[g16][dq] = make_float4(acc.x + o.x, acc.y + o.y, acc.z + o.z, acc.w + o.w);
-    }
+    const float4 o = fold_partials16(P);
+    if (lane < 16) co[wave][lane] = o;
+    if (lane == 0) { cm[wave] = m; cs[wave] = sum; }
     lds_barrier();
     if (wave == 0) {
-        // g16 = lane/16 here: levels 4 (LDS), 2 and 1 (lanes 32 and 16 apart)
-        const float4 sv = vred[g16][dq], o = vred[g16 + 4][dq];
-        float4 rr = make_float4(sv.x + o.x, sv.y + o.y, sv.z + o.z, sv.w + o.w);
-        rr.x = rr.x + take_up<32>(rr.x); rr.y = rr.y + take_up<32>(rr.y); rr.z = rr.z + take_up<32>(rr.z); rr.w = rr.w + take_up<32>(rr.w);
-        rr.x = rr.x + take_up<16>(rr.x); rr.y = rr.y + take_up<16>(rr.y); rr.z = rr.z + take_up<16>(rr.z); rr.w = rr.w + take_up<16>(rr.w);
-        if (lane < 16) ((float4*)ol)[dq] = make_float4(0.0f + rr.x, 0.0f + rr.y, 0.0f + rr.z, 0.0f + rr.w);
-        put_act(out, r, h * 64 + lane, ol[lane], lane);
-        if (out_f) out_f[(size_t)r * dim + h * 64 + lane] = ol[lane];
+        const int nch = (nc + 63) / 64;
+        const bool live = lane < nch;
+        const float mcv = live ? cm[lane] : -__builtin_inff();
+        float M = mcv;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) { const float x = shfl_xor(M, off); M = M > x ? M : x; }
+        const double w = live ? dexp((double)mcv - (double)M) : 0.0;
+        const double total = fold64d_b(live ? cs[lane] * w : 0.0);
+        const float f = live ? (float)(w / total) : 0.0f;
+        const float* cof = (const float*)co;
+        float res = 0.0f;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            if (cc >= nch) break;
+            res = __builtin_fmaf(cof[cc * 64 + lane], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), cc)), res);
+        }
+        const float v = nc > 0 ? res : 0.0f;
+        put_act(out, r, h * 64 + lane, v, lane);
+        if (out_f) out_f[(size_t)r * dim + h * 64 + lane] = v;
     }
 }
 
@@ -1129,7 +1035,7 @@ __global__ __launch_bounds__(256) void k_xattn(XAttnArgs a) {
     const int nc = a.nc ? a.nc[r] : a.n_ctx;
     const size_t kr = a.shared_kv ? 0 : (size_t)r;
     const float* bias = a.bias ? a.bias + ((size_t)h * gridDim.y + r) * a.bias_stride : nullptr;
-    xattn_head<16>(a.q + (size_t)r * a.dim + h * 64, a.k + (kr * H + h) * a.n_ctx * 64,
+    xattn_head(a.q + (size_t)r * a.dim + h * 64, a.k + (kr * H + h) * a.n_ctx * 64,
                    a.v + (kr * H + h) * a.n_ctx * 64, nc, a.scale, bias, a.out, a.out_f, a.dim, h, r);
 }
 
@@ -1752,7 +1658,6 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     stamp_end(a.stamp, t0);
 }
 
-constexpr int PV_WAVES = 8;   // softmax + V block: 8 waves share the exps, 4 do V
 
 // ---- GEMV launch: kernel choice by weight type, prologue / epilogue kind and unit count
 template <int WT, int NC, int G, int U, int PRO, int EPI, int W>
@@ -1902,64 +1807,17 @@ void launch_gemv(const GemvArgs& a0, hipStream_t s) {
         }
     }
 }
-template <int NCH> static void attn_pv(const AttnArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((k_attn_pv<NCH, PV_WAVES>), dim3(NCH, a.heads, a.ncol), dim3(64 * PV_WAVES), 0, s, a);
-}
-template <int NCH> static void attn_soft(const AttnArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((k_attn_soft<NCH>), dim3(a.heads, a.ncol), dim3(256), 0, s, a);
-}
 void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
-    hipLaunchKernelGGL(k_attn_scores, dim3(nch * ATT_SUBS, a.heads, a.ncol), dim3(256), 0, s, a);
-    if (a.ncol > 16) {
-        // wide launches: the softmax once per (head, column), then every chunk's V
-        switch (nch) {
-        case 1: attn_soft<1>(a, s); break;
-        case 2: attn_soft<2>(a, s); break;
-        case 3: attn_soft<3>(a, s); break;
-        case 4: attn_soft<4>(a, s); break;
-        case 5: attn_soft<5>(a, s); break;
-        case 6: attn_soft<6>(a, s); break;
-        case 7: attn_soft<7>(a, s); break;
-        case 8: attn_soft<8>(a, s); break;
-        case 9: attn_soft<9>(a, s); break;
-        case 10: attn_soft<10>(a, s); break;
-        case 11: attn_soft<11>(a, s); break;
-        case 12: attn_soft<12>(a, s); break;
-        case 13: attn_soft<13>(a, s); break;
-        case 14: attn_soft<14>(a, s); break;
-        case 15: attn_soft<15>(a, s); break;
-        default: attn_soft<16>(a, s); break;
-        }
-        hipLaunchKernelGGL(k_attn_pv_e, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
-        hipLaunchKernelGGL(k_attn_reduce, dim3(a.heads, a.ncol), dim3(64), 0, s, a);
-        return;
-    }
-    switch (nch) {
-    case 1: attn_pv<1>(a, s); break;
-    case 2: attn_pv<2>(a, s); break;
-    case 3: attn_pv<3>(a, s); break;
-    case 4: attn_pv<4>(a, s); break;
-    case 5: attn_pv<5>(a, s); break;
-    case 6: attn_pv<6>(a, s); break;
-    case 7: attn_pv<7>(a, s); break;
-    case 8: attn_pv<8>(a, s); break;
-    case 9: attn_pv<9>(a, s); break;
-    case 10: attn_pv<10>(a, s); break;
-    case 11: attn_pv<11>(a, s); break;
-    case 12: attn_pv<12>(a, s); break;
-    case 13: attn_pv<13>(a, s); break;
-    case 14: attn_pv<14>(a, s); break;
-    case 15: attn_pv<15>(a, s); break;
-    default: attn_pv<16>(a, s); break;
-    }
-    hipLaunchKernelGGL(k_attn_reduce, dim3(a.heads, a.ncol), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(k_attn_chunk, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.heads, a.ncol), dim3(64), 0, s, a);
 }
 // The same cross-attention for n_ctx <= 64 with one wave per (head, request) and no block
 // barrier on the critical path. Equal orders: a key's 16 four-dim partials (lanes t of a
 // 16-lane group) fold by the butterfly (lane t adds lane t+off, off 8..1: lane 0 ends with the
-// butterfly's value); the 256-key double sum is the 64-wide butterfly of the first 64 keys (the
-// others are exact zeros: (e + 0) + (0 + 0) = e); lane d sums dimension d's 16 key-strided
-// partials (key mod 16, fmaf in key order) and folds them by the butterfly in registers.
+// butterfly's value); the chunk's double sum is the 64-wide butterfly of its keys; lane d sums
+// dimension d's 16 key-strided partials of e v (key mod 16, fmaf in key order), folds them by
+// the butterfly in registers and scales by (float)(1/sum) with one fmaf -- the one-chunk case of
+// the self-attention combine.
 __global__ __launch_bounds__(64) void k_xattn_w(XAttnArgs a) {
     const int h = blockIdx.x, r = blockIdx.y, H = gridDim.x, lane = threadIdx.x, g = lane >> 4, t = lane & 15;
     const int nc = a.nc ? a.nc[r] : a.n_ctx;
@@ -2008,9 +1866,9 @@ __global__ __launch_bounds__(64) void k_xattn_w(XAttnArgs a) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(M, off); M = M > o ? M : o; }
     const float e = lane < nc ? dexpf(sc - M) : 0.0f;
-    const float inv = (float)(1.0 / (0.0 + fold64d_b((double)e)));
+    const float f = (float)(1.0 / fold64d_b((double)e));
     __syncthreads();
-    pj[lane] = e * inv;
+    pj[lane] = e;
     __syncthreads();
     float acc[16];
 #pragma unroll
@@ -2022,7 +1880,7 @@ __global__ __launch_bounds__(64) void k_xattn_w(XAttnArgs a) {
     for (int off = 8; off >= 1; off >>= 1)
 #pragma unroll
         for (int gg = 0; gg < off; ++gg) acc[gg] = acc[gg] + acc[gg + off];
-    const float o = 0.0f + acc[0];
+    const float o = __builtin_fmaf(acc[0], f, 0.0f);
     put_act(a.out, r, h * 64 + lane, o, lane);
     if (a.out_f) a.out_f[(size_t)r * a.dim + h * 64 + lane] = o;
 }

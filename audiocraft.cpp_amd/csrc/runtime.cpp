@@ -94,7 +94,7 @@ struct mgx_stream {
     int cap = 0, n_seq = 0, cross = 0, n_ctx = 0, used = 0, forwards = 0, max_chunks = 0;
     int n_req = 1, cpr = 1;                  // requests, and columns (streams) per request
     int cshift = 0;                          // column n belongs to request n >> cshift
-    int kv_rows = 0;                         // cache rows per head: cap rounded up to whole 256-key chunks
+    int kv_rows = 0;                         // cache rows per head: cap rounded up to whole 256-key spans
     hipStream_t hs = nullptr;
     DevArena mem;
     float *K = nullptr, *V = nullptr;        // per layer [n_seq][H][kv_rows][64]
@@ -109,8 +109,9 @@ struct mgx_stream {
     mgx::ReqParams* dpar = nullptr;
     int* dnc = nullptr;
     float *t5d = nullptr, *ctx = nullptr, *kvp = nullptr;   // memory projection scratch (n_ctx rows)
-    float* cmax = nullptr;                   // [n_seq][H][max_chunks * ATT_SUBS] attention score-block maxima
-    float *x = nullptr, *qb = nullptr, *scores = nullptr, *opart = nullptr, *logits = nullptr;
+    float* cmax = nullptr;                   // [n_seq][H][max_chunks] attention chunk maxima
+    double* csum = nullptr;                  // [n_seq][H][max_chunks] attention chunk sums
+    float *x = nullptr, *qb = nullptr, *opart = nullptr, *logits = nullptr;
     float* qc = nullptr;                     // cross q [n_req][dim]
     ActStore act_o, act_c, act_f;            // attention out, cross-attention out, GELU out
     ActStore act_ln;                         // LayerNorm'd columns in Q8 form (matrix-core GEMVs)
@@ -258,7 +259,7 @@ bool mf_src(const mgx::DevMat& w, int ncol, int epi) {
 // - ids_base]. With `heads`, the step's logits land in s->logits. `position` is the host's view
 // of the largest position: it sizes the attention grids (the kernels read each column's exact
 // key count on the device). Ends by advancing the device positions.
-int att_chunks(int position) { return position / mgx::ATT_CHUNK + 1; }
+int att_spans(int position) { return position / mgx::ATT_SPAN + 1; }
 
 void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int ids_req_stride, bool heads,
           const mgx::SampleArgs* sample, int position, int ncol = 0) {
@@ -278,7 +279,8 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
         const bool bf = mf_src(L.w[P_FF2], N, mgx::EPI_RESID);
         float* Kl = s->K + (size_t)l * s->layer_kv();
         float* Vl = s->V + (size_t)l * s->layer_kv();
-        // self-attention: LN1 + qkv with the K/V append, scores, softmax + V (+ chunk reduce)
+        // self-attention: LN1 + qkv with the K/V append, then per 64-key chunk the scores,
+        // softmax terms and V, then the chunks combined
         {
             s->prof_tag = MGX_PROF_QKV;
             mgx::GemvArgs a = ga(L.w[P_QKV], N);
@@ -290,13 +292,13 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
         {
             s->prof_tag = MGX_PROF_ATTN;
             mgx::AttnArgs at{};
-            at.q = s->qb; at.k = Kl; at.v = Vl; at.scores = s->scores; at.opart = s->opart; at.cmax = s->cmax;
+            at.q = s->qb; at.k = Kl; at.v = Vl; at.opart = s->opart; at.cmax = s->cmax; at.csum = s->csum;
             at.dim = D; at.heads = c.heads; at.cap = s->kv_rows; at.max_chunks = s->max_chunks; at.ncol = N;
             at.scale = scale; at.pos = s->dpos; at.cshift = s->cshift; at.kv_cols = s->kv_cols; at.out = s->act_o.view(L.w[P_OUT].type, bo);
             at.out_f = L.ad[P_OUT] ? s->act_o.f : nullptr;
             // f32 K and V of every key attended, every stream
             at.stamp = s->stamp_slot(PROF_ATTN, 2.0 * N * c.heads * (position + 1) * 64 * 4);
-            mgx::launch_attention(at, att_chunks(position), s->hs);
+            mgx::launch_attention(at, att_spans(position) * (mgx::ATT_SPAN / mgx::ATT_CHUNK), s->hs);
         }
         {
             s->prof_tag = MGX_PROF_OUT;
@@ -447,9 +449,10 @@ void make_stream(mgx_model* m, int capacity, int n_seq, int n_req, const float* 
     // one request: every column (at most 16) maps to 0; batches have 1 or 2 columns a request
     if (n_req > 1 && s->cpr > 2) throw Error(MGX_ERR_INVALID, "at most 2 streams per request");
     s->cshift = n_req == 1 ? 4 : s->cpr - 1;
-    s->max_chunks = (capacity + mgx::ATT_CHUNK - 1) / mgx::ATT_CHUNK;
-    s->kv_rows = s->max_chunks * mgx::ATT_CHUNK;
-    if (s->max_chunks > mgx::ATT_MAX_CHUNKS) throw Error(MGX_ERR_INVALID, "capacity above 4096 positions");
+    const int spans = (capacity + mgx::ATT_SPAN - 1) / mgx::ATT_SPAN;
+    if (spans > mgx::ATT_MAX_SPANS) throw Error(MGX_ERR_INVALID, "capacity above 4096 positions");
+    s->kv_rows = spans * mgx::ATT_SPAN;
+    s->max_chunks = s->kv_rows / mgx::ATT_CHUNK;
     HIP_OK(hipStreamCreateWithFlags(&s->hs, hipStreamNonBlocking));
     const size_t kv = s->layer_kv() * c.layers;
     s->K = s->mem.alloc<float>(kv);
@@ -461,10 +464,10 @@ void make_stream(mgx_model* m, int capacity, int n_seq, int n_req, const float* 
     HIP_OK(hipMemcpyAsync(s->table, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice, s->hs));
     s->dpos = s->mem.alloc<int>((size_t)n_req);
     HIP_OK(hipMemsetAsync(s->dpos, 0, sizeof(int) * (size_t)n_req, s->hs));
-    s->cmax = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * mgx::ATT_SUBS);
+    s->cmax = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks);
+    s->csum = s->mem.alloc<double>((size_t)n_seq * c.heads * s->max_chunks);
     s->x = s->mem.alloc<float>((size_t)n_seq * c.dim);
     s->qb = s->mem.alloc<float>((size_t)n_seq * c.dim);
-    s->scores = s->mem.alloc<float>((size_t)n_seq * c.heads * s->kv_rows);
     s->opart = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * 64);
     s->logits = s->mem.alloc<float>((size_t)n_seq * c.n_q * c.card);
     s->qc = s->mem.alloc<float>((size_t)n_req * c.dim);
@@ -514,10 +517,10 @@ std::unique_ptr<mgx_stream> make_prefill_view(mgx_stream* main, int g) {
     s->kv_cols = cpr; s->kv_layer = main->n_seq; s->shared_mem = true;
     s->dpos = s->mem.alloc<int>((size_t)g);
     if (main->dnc) s->dnc = s->mem.alloc<int>((size_t)g);   // the aimed request's conditioning length, per position
-    s->cmax = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * mgx::ATT_SUBS);
+    s->cmax = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks);
+    s->csum = s->mem.alloc<double>((size_t)n_seq * c.heads * s->max_chunks);
     s->x = s->mem.alloc<float>((size_t)n_seq * c.dim);
     s->qb = s->mem.alloc<float>((size_t)n_seq * c.dim);
-    s->scores = s->mem.alloc<float>((size_t)n_seq * c.heads * s->kv_rows);
     s->opart = s->mem.alloc<float>((size_t)n_seq * c.heads * s->max_chunks * 64);
     s->qc = s->mem.alloc<float>((size_t)g * c.dim);
     s->alloc_act(s->act_o, n_seq, c.dim);
@@ -835,15 +838,15 @@ struct mgx_session {
     double prefill_seconds = 0.0, decode_seconds = 0.0;
     int prof_every = 0;
     // Captured prefill positions (no heads) and decode steps (heads, CFG mix, sampling,
-    // position advance), one pair per attention chunk count: every kernel reads the position
-    // from the device, so a graph replays for every position with that many 256-key chunks.
-    hipGraphExec_t g_body[mgx::ATT_MAX_CHUNKS] = {}, g_step[mgx::ATT_MAX_CHUNKS] = {};
+    // position advance), one pair per attention span count: every kernel reads the position
+    // from the device, so a graph replays for every position with that many 256-key spans.
+    hipGraphExec_t g_body[mgx::ATT_MAX_SPANS] = {}, g_step[mgx::ATT_MAX_SPANS] = {};
     // MGX_GRAPHS=0 launches the same kernels one by one (for tools that do not follow
     // stream capture, such as kernel tracers).
     bool use_graphs = true;
     ~mgx_session() {
         if (s && s->hs) (void)hipStreamSynchronize(s->hs);
-        for (int i = 0; i < mgx::ATT_MAX_CHUNKS; ++i) {
+        for (int i = 0; i < mgx::ATT_MAX_SPANS; ++i) {
             if (g_body[i]) (void)hipGraphExecDestroy(g_body[i]);
             if (g_step[i]) (void)hipGraphExecDestroy(g_step[i]);
         }
@@ -977,7 +980,7 @@ void run_position(mgx_session* ss, bool full, bool profiled, int position) {
         step(s, ss->dseq, ss->S, 0, ss->K * ss->S, full, full ? &ss->sa : nullptr, position);
         return;
     }
-    hipGraphExec_t& g = (full ? ss->g_step : ss->g_body)[att_chunks(position) - 1];
+    hipGraphExec_t& g = (full ? ss->g_step : ss->g_body)[att_spans(position) - 1];
     if (!g) g = capture(ss, full, position);
     HIP_OK(hipGraphLaunch(g, s->hs));
 }
@@ -1202,7 +1205,7 @@ struct mgx_slots {
     uint8_t* hmask = nullptr;
     float *huni = nullptr, *ht5 = nullptr;
     mgx::SampleArgs sa{};
-    hipGraphExec_t g[mgx::ATT_MAX_CHUNKS] = {};
+    hipGraphExec_t g[mgx::ATT_MAX_SPANS] = {};
     bool use_graphs = true;
     struct Slot { bool live = false, unread = false; int pos = 0, start = 0, S = 0, T = 0; };
     std::vector<Slot> slot;
@@ -1378,7 +1381,7 @@ void slots_run(mgx_slots* sl, int steps) {
         if (!sl->use_graphs) {
             step(s, sl->dseq, sl->seq_len, 0, sl->K * sl->seq_len, true, &sl->sa, top);
         } else {
-            hipGraphExec_t& g = sl->g[att_chunks(top) - 1];
+            hipGraphExec_t& g = sl->g[att_spans(top) - 1];
             if (!g) g = slots_capture(sl, top);
             HIP_OK(hipGraphLaunch(g, s->hs));
         }

@@ -42,17 +42,19 @@
  *   norm: mean and variance as double sums, element i -> partial (i/4) mod 256 accumulated
  *     in increasing i, folded by a 256-wide butterfly (off = 128,..,1); result (x - mean) *
  *     (1.0f / sqrtf(var + eps)), then * w, then + b, each rounded in f32.
- *   soft_max_ext: x*scale (+mask); max; e = expf(x - max); sum of e in double over chunks
- *     of 256 keys (butterfly inside a chunk, chunks added in order); p = e * (float)(1/sum).
- *   attention matmuls (f32 x f32): q.k as 16 partials (dim i -> partial (i/4) mod 16,
- *     fmaf in order) + butterfly; V^T.p per 256-key chunk as 16 partials (key j ->
- *     partial j mod 16, fmaf in increasing j) + butterfly, chunk results added in order.
+ *   soft_max_ext + the V^T mul_mat, per 64-key chunk: x*scale (+mask); the chunk's max;
+ *     e = expf(x - chunk max); the chunk's sum of e in double (64-wide butterfly); V^T.e as
+ *     16 partials (key j -> partial j mod 16, fmaf in increasing j) + butterfly. The chunks
+ *     are then combined with their weights exp(chunk max - max) in double: the total is the
+ *     64-wide butterfly of the chunks' (sum * weight), and each chunk's V^T.e enters the
+ *     output, in chunk order, through an fmaf by (float)(weight / total). q.k: 16 partials
+ *     (dim i -> partial (i/4) mod 16, fmaf in order) + butterfly.
  *   gelu_erf: 0.5f*x*(1.0f+erff(x*0.70710678f)).
  *   expf / erff: (float) of this file's own double exp (Cody-Waite reduction by ln2 split
- *     hi/lo, degree-13 Taylor, ldexp) and double erf (Taylor series below |x| = 2, the
- *     Laplace continued fraction for erfc by forward recurrence up to 6, +-1 beyond).
- *     Both stay within ~1 ulp double of the true functions, so the f32 results are the
- *     correctly rounded expf/erff except in ~1e-8 of cases.
+ *     hi/lo, degree-13 Taylor, ldexp) and double erf (two Chebyshev interpolants, below
+ *     |x| = 1 and on [1, 4), +-1 beyond; absolute error under 1.3e-12). The f32 results are
+ *     within one ulp of the true functions (the correctly rounded value but for ~1e-8 of
+ *     expf and ~1e-4 of erff arguments).
  *
  * Every floating-point step is written out (the file is compiled with -ffp-contract=off),
  * so the HIP kernels can reproduce it bit for bit.
@@ -150,37 +152,38 @@ REF_API double ref_exp(double x) {
 }
 REF_API float ref_expf(float x) { return (float)ref_exp((double)x); }
 
-/* erf(x) = 2/sqrt(pi) * sum_n (-1)^n x^(2n+1) / (n! (2n+1)) */
-static const double ERF_TAYLOR[30] = {
-    1.0, -0.3333333333333333, 0.1, -0.023809523809523808,
-    0.004629629629629629, -0.0007575757575757576, 0.00010683760683760684, -1.3227513227513228e-05,
-    1.4589169000933706e-06, -1.4503852223150468e-07, 1.3122532963802806e-08, -1.0892221037148573e-09,
-    8.35070279514724e-11, -5.9477940136376354e-12, 3.9554295164585257e-13, -2.466827010264457e-14,
-    1.4483264643598138e-15, -8.032735012415773e-17, 4.221407288807088e-18, -2.107855191442136e-19,
-    1.0025164934907719e-20, -4.5518467589282e-22, 1.977064753877905e-23, -8.230149299214221e-25,
-    3.289260349175752e-26, -1.2641078988989164e-27, 4.6784835155184856e-29, -1.669761793417372e-30,
-    5.754191643982172e-32, -1.9169428621097826e-33};
+/* erf: two Chebyshev interpolants in monomial form (audiocraft.cpp_amd/csrc/erf_coeffs.py derives
+   them from 40-digit erf values): |x| < 1: x * P(2x^2 - 1), P of degree 11; 1 <= |x| < 4:
+   1 - Q(t), t = |x| * 2/3 - 5/3, Q (erfc on [1, 4]) of degree 20; +-1 beyond. Absolute error
+   below 1.5e-15 and 1.3e-12 (measured against mpmath). The GPU kernels evaluate the same
+   steps with the same constants. */
+static const double ERF_P[12] = {
+    0x1.ee51eb23cb7ebp-1, -0x1.1fd162921520ep-3, 0x1.454368017b319p-6,
+    -0x1.2b902b7b26e28p-9, 0x1.c82aa24968f47p-13, -0x1.263991d3aca15p-16,
+    0x1.4866394fa4c3ep-20, -0x1.429e4c163b13bp-24, 0x1.1ad503d95b599p-28,
+    -0x1.c02cc0da54c52p-33, 0x1.4424c09b26e7bp-37, -0x1.2d4c29f5686cbp-42};
+static const double ERF_Q[21] = {
+    0x1.aab859b20b140p-12, -0x1.ac44a2cdb3c80p-9, 0x1.9180586b55ae8p-7,
+    -0x1.cdb9fd59ee319p-6, 0x1.65964ef5668ffp-5, -0x1.7c8c5ebf7f0ccp-5,
+    0x1.0521f53919ddep-5, -0x1.2faaceec90308p-7, -0x1.b5d2183e391e9p-8,
+    0x1.3b371adacbf70p-7, -0x1.29d400459d61ep-8, -0x1.ca1cf08ac8d5dp-12,
+    0x1.df3c4bd10ee4ep-10, -0x1.e7099cc2c7d56p-11, -0x1.d14ddd0a26b51p-15,
+    0x1.3dc0c2909a110p-12, -0x1.e193532b72642p-14, -0x1.3af7b90db0f1ap-15,
+    0x1.17a5709f8fe8ap-15, 0x1.048f70bb1e4f4p-20, -0x1.e180cb94805c1p-19};
 
 REF_API double ref_erf(double x) {
     const double ax = fabs(x);
-    if (ax < 2.0) {
-        const double t = x * x;
-        double p = ERF_TAYLOR[29];
-        for (int n = 28; n >= 0; --n) p = fma(p, t, ERF_TAYLOR[n]);
-        return (x * p) * 1.1283791670955126;
+    if (ax < 1.0) {
+        const double t = fma(2.0 * x, x, -1.0);
+        double p = ERF_P[11];
+        for (int n = 10; n >= 0; --n) p = fma(p, t, ERF_P[n]);
+        return x * p;
     }
-    if (ax >= 6.0) return x > 0 ? 1.0 : -1.0;
-    /* erfc(z) = exp(-z^2)/sqrt(pi) * 1/(z + (1/2)/(z + 1/(z + (3/2)/(z + ...)))),
-       evaluated as A_N/B_N by the forward three-term recurrence, N = 50. */
-    double am2 = 1.0, am1 = 0.0, bm2 = 0.0, bm1 = 1.0;
-    for (int n = 1; n <= 50; ++n) {
-        const double a = (n == 1) ? 1.0 : 0.5 * (double)(n - 1);
-        const double A = fma(ax, am1, a * am2);
-        const double B = fma(ax, bm1, a * bm2);
-        am2 = am1; am1 = A; bm2 = bm1; bm1 = B;
-    }
-    const double erfc = (ref_exp(-(ax * ax)) * 0.5641895835477563) * (am1 / bm1);
-    const double r = 1.0 - erfc;
+    if (ax >= 4.0) return x > 0 ? 1.0 : -1.0;
+    const double t = fma(ax, 0x1.5555555555555p-1, -0x1.aaaaaaaaaaaabp+0);
+    double p = ERF_Q[20];
+    for (int n = 19; n >= 0; --n) p = fma(p, t, ERF_Q[n]);
+    const double r = 1.0 - p;
     return x > 0 ? r : -r;
 }
 REF_API float ref_erff(float x) { return (float)ref_erf((double)x); }
@@ -473,7 +476,8 @@ REF_API void ref_sin_positions(int first, int n, int dim, int pos_denominator, f
 /* ------------------------------------------------------------------------------------ */
 /* attention: one query against keys [0,u) (nn.h:186-191)                               */
 /* ------------------------------------------------------------------------------------ */
-#define ATT_CHUNK 256
+#define ATT_CHUNK 64    /* keys per attention chunk */
+#define ATT_SLOTS 64    /* chunks of one attention (4096 keys) */
 
 static inline float dot_qk(const float* q, const float* k, int hd) {
     float part[16];
@@ -483,42 +487,73 @@ static inline float dot_qk(const float* q, const float* k, int hd) {
 }
 
 /* K: key j's row at K + j*k_stride (hd floats); V^T: dim d's row at VT + d*vt_stride, key j
-   at + j. mask_row: additive, [u], or NULL. s, e: scratch [u]. */
+   at + j. mask_row: additive, [u], or NULL. s: scratch [u]. u <= ATT_CHUNK * ATT_SLOTS.
+   Keys in chunks of ATT_CHUNK (64). Per chunk c: its max m_c over the chunk's unmasked scores
+   (a chunk whose keys are all masked is skipped), e_j = expf(s_j - m_c), the chunk sum S_c of
+   the e_j in double (64-wide butterfly over the chunk's keys, zeros past its end), and o_c =
+   sum_j e_j v_j per dim as 16 key-strided fmaf partials (key j -> partial j mod 16, increasing
+   j) + butterfly. Then M = max m_c, w_c = exp((double)m_c - M) in double, total = the 64-wide
+   butterfly of slots S_c * w_c (slot c, zeros for absent chunks), and out = sum over the
+   chunks in order of fmaf(o_c, (float)(w_c / total), .) -- the softmax of nn.h:186-191 with
+   its normalization applied per chunk. */
 static void attend(const float* q, int hd, int u, const float* K, size_t k_stride, const float* VT,
                    size_t vt_stride, const float* mask_row, float scale, float* out, float* s) {
+    const int nch = (u + ATT_CHUNK - 1) / ATT_CHUNK;
+    if (nch > ATT_SLOTS || hd > 64) {   /* beyond every shape this oracle serves */
+        for (int d = 0; d < hd; ++d) out[d] = NAN;
+        return;
+    }
     for (int j = 0; j < u; ++j) {
         float w = dot_qk(q, K + (size_t)j * k_stride, hd) * scale;
         if (mask_row) w = w + mask_row[j];
         s[j] = w;
     }
-    float mx = -INFINITY;
-    for (int j = 0; j < u; ++j) mx = mx > s[j] ? mx : s[j];
-    for (int j = 0; j < u; ++j) s[j] = ref_expf(s[j] - mx);
-    double total = 0.0;
-    for (int c = 0; c * ATT_CHUNK < u; ++c) {
+    float mc[ATT_SLOTS], oc[ATT_SLOTS][64];
+    double sc[ATT_SLOTS];
+    int live[ATT_SLOTS];
+    for (int c = 0; c < nch; ++c) {
+        const int j0 = c * ATT_CHUNK, j1 = j0 + ATT_CHUNK < u ? j0 + ATT_CHUNK : u;
+        float m = -INFINITY;
+        for (int j = j0; j < j1; ++j) m = m > s[j] ? m : s[j];
+        live[c] = m != -INFINITY;
+        mc[c] = m;
+        if (!live[c]) continue;
         double part[ATT_CHUNK];
         for (int l = 0; l < ATT_CHUNK; ++l) {
-            const int j = c * ATT_CHUNK + l;
-            part[l] = j < u ? (double)s[j] : 0.0;
+            const int j = j0 + l;
+            part[l] = 0.0;
+            if (j < j1) { s[j] = ref_expf(s[j] - m); part[l] = (double)s[j]; }
         }
-        total = total + fold_d(part, ATT_CHUNK);
-    }
-    const float inv = (float)(1.0 / total);
-    for (int j = 0; j < u; ++j) s[j] = s[j] * inv;
-    for (int d = 0; d < hd; ++d) {
-        const float* vrow = VT + (size_t)d * vt_stride;
-        float res = 0.0f;
-        for (int c = 0; c * ATT_CHUNK < u; ++c) {
-            float part[16];
-            for (int l = 0; l < 16; ++l) part[l] = 0.0f;
-            for (int m = 0; m < ATT_CHUNK / 16; ++m)
+        sc[c] = fold_d(part, ATT_CHUNK);
+        for (int d = 0; d < hd; ++d) {
+            const float* vrow = VT + (size_t)d * vt_stride;
+            float p16[16];
+            for (int l = 0; l < 16; ++l) p16[l] = 0.0f;
+            for (int mm = 0; mm < ATT_CHUNK / 16; ++mm)
                 for (int g = 0; g < 16; ++g) {
-                    const int j = c * ATT_CHUNK + g + 16 * m;
-                    if (j < u) part[g] = fmaf(s[j], vrow[j], part[g]);
+                    const int j = j0 + g + 16 * mm;
+                    if (j < j1) p16[g] = fmaf(s[j], vrow[j], p16[g]);
                 }
-            res = res + fold_f(part, 16);
+            oc[c][d] = fold_f(p16, 16);
         }
-        out[d] = res;
+    }
+    float M = -INFINITY;
+    for (int c = 0; c < nch; ++c) if (live[c]) M = M > mc[c] ? M : mc[c];
+    double w[ATT_SLOTS], slot[ATT_SLOTS];
+    for (int c = 0; c < ATT_SLOTS; ++c) {
+        slot[c] = 0.0;
+        if (c < nch && live[c]) {
+            w[c] = ref_exp((double)mc[c] - (double)M);
+            slot[c] = sc[c] * w[c];
+        }
+    }
+    const double total = fold_d(slot, ATT_SLOTS);
+    float f[ATT_SLOTS];
+    for (int c = 0; c < nch; ++c) if (live[c]) f[c] = (float)(w[c] / total);
+    for (int d = 0; d < hd; ++d) {
+        float r = 0.0f;
+        for (int c = 0; c < nch; ++c) if (live[c]) r = fmaf(oc[c][d], f[c], r);
+        out[d] = r;
     }
 }
 
@@ -1306,7 +1341,7 @@ done:
     return rc;
 }
 
-REF_API int ref_convention(void) { return 3; }
+REF_API int ref_convention(void) { return 4; }
 
 REF_API void ref_set_threads(int n) {
 #ifdef _OPENMP

@@ -132,3 +132,44 @@ def test_full_length_generation_matches_fixture(M, name):
     assert np.array_equal(first, f["first_logits"])
     assert gen.mean() >= 0.995
     assert bad.size == 0, f"mixed logits first differ at step {bad[0]}"
+
+
+@pytest.mark.slow
+def test_c5_batch_matches_fixture(M):
+    """The batched serving workload at full size: 8 guided medium Q8_0 requests (16 columns, 48
+    layers, rank-16 DoRA rows on qkv / ff.0 / ff.2), 500-frame prompts prefilled through the
+    64-column view (ragged last groups), then 1502 decode steps attending up to 2003 keys (eight
+    256-key chunks at 16 columns): every request's mixed logits at every step (CRC), first
+    logits and codes equal the oracle's generation of that request alone."""
+    import sys
+    sys.path.insert(0, GOLDEN)
+    from make_fixtures import CASES, adapter_digest, batch_inputs, model_digest
+    from oracle import cpu_ref as R
+    name = "c5_medium_q8_batch8_dora"
+    f = _fixture(name)
+    assert int(f["convention"]) == R.lib().ref_convention(), "fixture predates the current reduction order"
+    case = CASES[name]
+    print(f"full-length batch {name}", flush=True)
+    m, ads, reqs = batch_inputs(case)
+    assert bytes(f["model_sha256"]).hex() == model_digest(m), "the synthetic generator changed; regenerate fixtures"
+    assert bytes(f["adapter_sha256"]).hex() == adapter_digest(ads)
+    T = case["prompt"] + case["gen"]
+    requests = []
+    for r, (t5, prompt, seed) in enumerate(reqs):
+        assert zlib.crc32(t5.tobytes()) == int(f["t5_crc"][r]) and zlib.crc32(prompt.tobytes()) == int(f["prompt_crc"][r])
+        requests.append(dict(t5=t5, prompt=prompt, params=M.GenerateParams(T, 1, 1.0, case["top_k"], 3.0, seed),
+                             description_empty=False))
+    gm = M.Model(m.config, m.tensors)
+    gm.set_adapters(ads)
+    b = M.Batch(gm, requests, case["prompt"], keep_step_logits=True)
+    while b.remaining() > 0:
+        b.step(256)
+    for r in range(len(reqs)):
+        codes, first, rep, steps = b.finish(r)
+        crc = np.array([zlib.crc32(steps[i].tobytes()) for i in range(steps.shape[0])], np.uint32)
+        bad = np.nonzero(crc != f["step_crc"][r])[0]
+        print(f"  request {r}: first differing step {bad[0] if bad.size else None}", flush=True)
+        assert np.array_equal(first, f["first_logits"][r]), f"request {r}: first logits"
+        assert bad.size == 0, f"request {r}: mixed logits first differ at step {bad[0]}"
+        assert np.array_equal(codes, f["codes"][r]), f"request {r}: codes"
+    b.close()

@@ -34,19 +34,31 @@ def test_exp_within_one_ulp():
     assert L.ref_exp(-800.0) == 0.0 and math.isinf(L.ref_exp(710.0)) and math.isnan(L.ref_exp(float("nan")))
 
 
-def test_erf_within_eight_ulps_and_odd():
+def test_erf_accuracy_and_odd():
+    """The two-interpolant erf: relative error below 4e-15 for |x| < 1 (erf ~ x there), absolute
+    error below 2e-12 on [1, 4), exactly +-1 beyond, odd."""
     rs = np.random.default_rng(1)
-    xs = np.concatenate([rs.uniform(-7, 7, 4000), [0.0, 1e-8, 1.9999, 2.0, 5.9999, 6.0]])
-    worst = max(ulps(L.ref_erf(float(x)), mpmath.erf(float(x))) for x in xs if x != 0)
-    assert worst <= 8.0
+    xs = np.concatenate([rs.uniform(-7, 7, 4000), rs.uniform(-1, 1, 2000),
+                         [1e-300, 1e-8, 0.9999999, 1.0, 1.0000001, 2.5, 3.9999999, 4.0, 6.0]])
+    for x in xs:
+        got, want = L.ref_erf(float(x)), mpmath.erf(float(x))
+        if abs(x) < 1:
+            assert abs(mpmath.mpf(got) - want) <= 4e-15 * abs(want), float(x)
+        elif abs(x) < 4:
+            assert abs(mpmath.mpf(got) - want) <= 2e-12, float(x)
+        else:
+            assert got == math.copysign(1.0, x)
     for x in xs[:200]:
         assert L.ref_erf(float(-x)) == -L.ref_erf(float(x))
+    assert L.ref_erf(0.0) == 0.0
 
 
-def test_expf_erff_correctly_rounded():
-    """(float) of the double routines is the correctly rounded expf / erff on every sample
-    (checked against 200-bit mpmath); glibc's own expf / erff, which ggml's scalar path calls,
-    agree to 1 ulp."""
+def test_expf_erff_rounding():
+    """(float) of the double routines: expf is the correctly rounded value on every sample
+    (checked against 200-bit mpmath); erff is within one ulp of the true erf everywhere and the
+    correctly rounded value on all but a few in 10^4 samples (its double erf is accurate to
+    1.3e-12 absolute, so only values that close to a rounding midpoint can round the other
+    way); glibc's own expf / erff, which ggml's scalar path calls, agree to 1 ulp."""
     rs = np.random.default_rng(2)
     xs = np.concatenate([rs.uniform(-88, 88, 6000), rs.normal(0, 2, 6000)]).astype(np.float32)
     for x in xs:
@@ -54,11 +66,16 @@ def test_expf_erff_correctly_rounded():
         assert got == np.float32(float(mpmath.exp(float(x)))), float(x)
         g = np.float32(libm.expf(float(x)))
         assert abs(int(got.view(np.int32)) - int(g.view(np.int32))) <= 1
-    for y in rs.normal(0, 2, 6000).astype(np.float32):
+    off = 0
+    ys = np.concatenate([rs.normal(0, 2, 6000), rs.uniform(-4.5, 4.5, 6000)]).astype(np.float32)
+    for y in ys:
         got = np.float32(L.ref_erff(float(y)))
-        assert got == np.float32(float(mpmath.erf(float(y)))), float(y)
+        exact = np.float32(float(mpmath.erf(float(y))))
+        assert abs(int(got.view(np.int32)) - int(exact.view(np.int32))) <= 1, float(y)
+        off += got != exact
         g = np.float32(libm.erff(float(y)))
         assert abs(int(got.view(np.int32)) - int(g.view(np.int32))) <= 1
+    assert off <= 6, off
 
 
 def test_gelu_erf_closed_form():
@@ -137,12 +154,16 @@ def test_sin_positions_formula():
 
 
 def test_attention_against_dense_float64():
-    """sdpa_vt on the transposed cache = dense softmax attention (nn.h:186-191)."""
+    """sdpa_vt on the transposed cache = dense softmax attention (nn.h:186-191), with chunks
+    whose maxima differ widely (a block of keys aligned with q) so the per-chunk rescaling
+    carries real weight."""
     rs = np.random.default_rng(7)
-    for u in (1, 7, 256, 257, 1000, 3003):
+    for u in (1, 7, 64, 65, 256, 257, 1000, 3003, 4096):
         hd, cap = 64, u + 5
         q = rs.normal(0, 1, hd).astype(np.float32)
         K = rs.normal(0, 1, (u, hd)).astype(np.float32)
+        if u > 300:
+            K[260:290] += (3.0 * q / np.linalg.norm(q)).astype(np.float32)
         VT = rs.normal(0, 1, (hd, cap)).astype(np.float32)
         out = np.zeros(hd, np.float32)
         L.ref_attend(R.ptr(q), hd, u, R.ptr(K), R.ptr(VT), cap, None, 0.125, R.ptr(out))
