@@ -1083,6 +1083,17 @@ __device__ __forceinline__ double seq_sum_f(const float* x, int n) {
     return t;
 }
 
+// Double-double accumulation (h, l) += (b, bl): Knuth's two-sum of the high parts, the low
+// parts added to its error, renormalized -- the sum stays within ~2^-100 of exact for the
+// positive terms it is used on.
+__device__ __forceinline__ void dd_add(double& h, double& l, double b, double bl) {
+    const double s = h + b, bb = s - h;
+    const double err = (h - (s - bb)) + (b - bb);
+    const double t = err + (l + bl);
+    h = s + t;
+    l = t - (h - s);
+}
+
 // Block-wide inclusive scan of one int per thread (256 threads), through LDS.
 __device__ __forceinline__ int block_scan_i(int v, int* tmp) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1109,7 +1120,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
     __shared__ int itmp[8];
     __shared__ float red_f[4];
     __shared__ int red_i[4];
-    __shared__ double red_d[4];
+    __shared__ double red_d[4], dd_lo[4];
     __shared__ int tok_sh, pick_sh, exact_sh;
     __shared__ float inv_sh;
     __shared__ uint32_t prefix_sh;
@@ -1172,13 +1183,30 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
         __syncthreads();
         pk = red_f[0];
         for (int w = 1; w < 4; ++w) pk = pk < red_f[w] ? red_f[w] : pk;
+        // The reference's total is the sequential double sum of the e (sampling.h:47-51); only
+        // (float)(1 / total) is used. The sum in double-double (error ~2^-100 relative) and the
+        // sequential sum's error bound (n-1) u / (1 - (n-1) u) of it (all e >= 0) bracket the
+        // sequential total; (float)(1.0 / t) is monotone in t, so when it is the same at both
+        // ends of the bracket it is the reference's value. Otherwise (about 1e-5 of the rows)
+        // one lane runs the sequential sum.
+        double hs = 0.0, ls = 0.0;
         for (int i = tid; i < C; i += 256) {
             const double e = dexp(((double)lg[i] - (double)pk) / (double)temperature);
             ex[i] = e;
             pr[i] = (float)e;
+            dd_add(hs, ls, e, 0.0);
         }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) dd_add(hs, ls, shfl_xor(hs, off), shfl_xor(ls, off));
+        if (lane == 0) { red_d[wave] = hs; dd_lo[wave] = ls; }
         __syncthreads();
-        if (tid == 0) inv_sh = (float)(1.0 / seq_sum_d(ex, C));
+        if (tid == 0) {
+            double h = red_d[0], l = dd_lo[0];
+            for (int w = 1; w < 4; ++w) dd_add(h, l, red_d[w], dd_lo[w]);
+            const double sum = h + l, bound = (double)(C - 1) * 1.2e-16 * sum;
+            const float a0 = (float)(1.0 / (sum + bound)), a1 = (float)(1.0 / (sum - bound));
+            inv_sh = a0 == a1 ? a0 : (float)(1.0 / seq_sum_d(ex, C));
+        }
         __syncthreads();
         for (int i = tid; i < C; i += 256) pr[i] = pr[i] * inv_sh;
         __syncthreads();
@@ -1670,6 +1698,7 @@ static void gemv_go(const GemvArgs& a, hipStream_t s) {
 // Tries (G, U, W) = the listed shapes whose G * U matches the row's unit count; else the
 // runtime-loop kernel.
 #define GEMV_TRY(G_, U_, W_) if (units == (G_) * (U_)) return gemv_go<WT, NC, G_, U_, PRO, EPI, W_>(a, s)
+
 template <int WT, int NC, int PRO, int EPI> static void gemv_pick(const GemvArgs& a, hipStream_t s) {
     const int units = a.w.in / unit_elems<WT>();
     if constexpr (PRO == PRO_ACT) {
@@ -1811,79 +1840,87 @@ void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
     hipLaunchKernelGGL(k_attn_chunk, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
     hipLaunchKernelGGL(k_attn_combine, dim3(a.heads, a.ncol), dim3(64), 0, s, a);
 }
-// The same cross-attention for n_ctx <= 64 with one wave per (head, request) and no block
-// barrier on the critical path. Equal orders: a key's 16 four-dim partials (lanes t of a
-// 16-lane group) fold by the butterfly (lane t adds lane t+off, off 8..1: lane 0 ends with the
-// butterfly's value); the chunk's double sum is the 64-wide butterfly of its keys; lane d sums
-// dimension d's 16 key-strided partials of e v (key mod 16, fmaf in key order), folds them by
-// the butterfly in registers and scales by (float)(1/sum) with one fmaf -- the one-chunk case of
-// the self-attention combine.
-__global__ __launch_bounds__(64) void k_xattn_w(XAttnArgs a) {
-    const int h = blockIdx.x, r = blockIdx.y, H = gridDim.x, lane = threadIdx.x, g = lane >> 4, t = lane & 15;
-    const int nc = a.nc ? a.nc[r] : a.n_ctx;
-    if (nc <= 0) {
-        // no conditioning: zeros (the gated cross.out leaves the residual unchanged)
-        put_act(a.out, r, h * 64 + lane, 0.0f, lane);
-        if (a.out_f) a.out_f[(size_t)r * a.dim + h * 64 + lane] = 0.0f;
-        return;
-    }
+// The same cross-attention for n_ctx <= 64 (one 64-key chunk) by one wave per (head, request):
+// the chunk of xattn_head with its combine reduced to out = fmaf(o, (float)(1 / sum), 0).
+// One wave: head h of request r, of H heads and n_req requests (threads past the first 64 of a
+// block, if any, take part in its barriers only).
+__device__ __forceinline__ void xattn_wave(const XAttnArgs& a, int h, int r, int H, int n_req) {
+    const int lane = threadIdx.x & 63, g = lane >> 4, t = lane & 15;
+    const bool act = threadIdx.x < 64;
     const size_t kr = a.shared_kv ? 0 : (size_t)r;
     const float* K = a.k + (kr * H + h) * a.n_ctx * 64;
     const float* V = a.v + (kr * H + h) * a.n_ctx * 64;
-    const float* bias = a.bias ? a.bias + ((size_t)h * gridDim.y + r) * a.bias_stride : nullptr;
-    __shared__ float pj[64];
-    // every load first: q, the keys' float4s (key 4*it + g), then V column `lane` of each key
+    const float* bias = a.bias ? a.bias + ((size_t)h * n_req + r) * a.bias_stride : nullptr;
+    __shared__ float el[64];
+    __shared__ float4 ol[16];
+    const int nc = a.nc ? a.nc[r] : a.n_ctx;
+    if (nc <= 0) {
+        // no conditioning: zeros (the gated cross.out leaves the residual unchanged)
+        if (act) put_act(a.out, r, h * 64 + lane, 0.0f, lane);
+        if (act && a.out_f) a.out_f[(size_t)r * a.dim + h * 64 + lane] = 0.0f;
+        return;
+    }
+    // every load first: q, the keys 4*it + g, the V rows g + 4k + 16mm (all clamped to the keys)
     const float4 q = ((const float4*)(a.q + (size_t)r * a.dim + h * 64))[t];
-    float4 kv[16];
+    float4 kv[16], vv[16];
 #pragma unroll
     for (int it = 0; it < 16; ++it) {
-        const int j = 4 * it + g, jl = j < nc ? j : nc - 1;
+        const int j = it * 4 + g, jl = j < nc ? j : nc - 1;
         kv[it] = ((const float4*)(K + (size_t)jl * 64))[t];
     }
-    float vv[64];
 #pragma unroll
-    for (int j = 0; j < 64; ++j) vv[j] = V[(size_t)(j < nc ? j : nc - 1) * 64 + lane];
-    __builtin_amdgcn_sched_barrier(0);
-    // scores: lane (g, 0) holds key 4*it + g after the fold
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+            const int j = g + 4 * k + 16 * mm, jl = j < nc ? j : nc - 1;
+            vv[4 * k + mm] = ((const float4*)(V + (size_t)jl * 64))[t];
+        }
+    float p[16];
 #pragma unroll
     for (int it = 0; it < 16; ++it) {
-        if (4 * it >= nc) break;
         float v = __builtin_fmaf(q.x, kv[it].x, 0.0f);
         v = __builtin_fmaf(q.y, kv[it].y, v);
         v = __builtin_fmaf(q.z, kv[it].z, v);
-        v = __builtin_fmaf(q.w, kv[it].w, v);
-        v = v + take_up<8>(v);
-        v = v + take_up<4>(v);
-        v = v + take_up<2>(v);
-        v = v + take_up<1>(v);
-        float sc = v * a.scale;
-        if (bias && 4 * it + g < nc) sc = sc + bias[4 * it + g];
-        if (t == 0) pj[4 * it + g] = sc;
+        p[it] = __builtin_fmaf(q.w, kv[it].w, v);
     }
+    const int jt = 4 * t + g;
+    float sc = halving16(p, t) * a.scale;
+    if (bias && jt < nc) sc = sc + bias[jt];
+    float m = jt < nc ? sc : -__builtin_inff();
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(m, off); m = m > o ? m : o; }
+    if (act) el[jt] = jt < nc ? dexpf(sc - m) : 0.0f;
     __syncthreads();
-    const float sc = lane < nc ? pj[lane] : -__builtin_inff();
-    float M = sc;
+    const float f = (float)(1.0 / fold64d_b((double)el[lane]));
+    float4 P[4];
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(M, off); M = M > o ? M : o; }
-    const float e = lane < nc ? dexpf(sc - M) : 0.0f;
-    const float f = (float)(1.0 / fold64d_b((double)e));
+    for (int k = 0; k < 4; ++k) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+            const int j = g + 4 * k + 16 * mm;
+            if (j < nc) {
+                const float e = el[j];
+                acc.x = __builtin_fmaf(e, vv[4 * k + mm].x, acc.x);
+                acc.y = __builtin_fmaf(e, vv[4 * k + mm].y, acc.y);
+                acc.z = __builtin_fmaf(e, vv[4 * k + mm].z, acc.z);
+                acc.w = __builtin_fmaf(e, vv[4 * k + mm].w, acc.w);
+            }
+        }
+        P[k] = acc;
+    }
+    const float4 o4 = fold_partials16(P);
+    if (act && lane < 16) ol[lane] = o4;
     __syncthreads();
-    pj[lane] = e;
-    __syncthreads();
-    float acc[16];
-#pragma unroll
-    for (int gg = 0; gg < 16; ++gg) acc[gg] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 64; ++j)
-        if (j < nc) acc[j & 15] = __builtin_fmaf(pj[j], vv[j], acc[j & 15]);
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1)
-#pragma unroll
-        for (int gg = 0; gg < off; ++gg) acc[gg] = acc[gg] + acc[gg + off];
-    const float o = __builtin_fmaf(acc[0], f, 0.0f);
+    const float o = __builtin_fmaf(((const float*)ol)[lane], f, 0.0f);
+    if (!act) return;
     put_act(a.out, r, h * 64 + lane, o, lane);
     if (a.out_f) a.out_f[(size_t)r * a.dim + h * 64 + lane] = o;
 }
+__global__ __launch_bounds__(64) void k_xattn_w(XAttnArgs a) {
+    xattn_wave(a, blockIdx.x, blockIdx.y, gridDim.x, gridDim.y);
+}
+
 void launch_xattn(const XAttnArgs& a, int heads, int n_req, hipStream_t s) {
     if (a.n_ctx <= 64) hipLaunchKernelGGL(k_xattn_w, dim3(heads, n_req), dim3(64), 0, s, a);
     else hipLaunchKernelGGL(k_xattn, dim3(heads, n_req), dim3(256), 0, s, a);
