@@ -4,9 +4,12 @@
         per-kernel calls / total / average / min / max duration, GEMV instances also summed
         into one "k_gemv (all instances)" line;
     python3 -m mgx.rocprof_summary traffic <fetch counter_collection.csv> <write counter_collection.csv> <copy MiB>
-        average FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the GEMV dispatches, each scaled
-        by the same counter on the device-to-device copy of <copy MiB> that ran in the same
-        process, and the resulting HBM bytes per GEMV launch.
+                                           [<name>=<regex>[+<regex>...] [last=<n>]]
+        average FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the GEMV dispatches -- or, with a
+        unit spec, of each listed kernel's last n dispatches, summed over the kernels (one
+        "launch" of a unit such as the attention is one dispatch of each) -- each scaled by the
+        same counter on the device-to-device copy of <copy MiB> that ran in the same process,
+        and the resulting HBM bytes per launch.
 
 Used to write the text summaries under profiles/; needs only the CSV files.
 """
@@ -42,40 +45,53 @@ def stats(path):
     return "\n".join(out)
 
 
-def _counter(path, counter):
-    """Mean counter value (KiB) per dispatch for the GEMV kernels and for the copy kernel."""
-    gemv, copy = [], []
+def _counter(path, counter, pattern=None, last=0):
+    """Mean counter value (KiB) per dispatch of the kernels matching `pattern` (default: every
+    GEMV), over their last `last` dispatches when given, and the copy kernel's value."""
+    import re
+    vals, copy = [], []
+    rx = re.compile(pattern) if pattern else None
     for r in _rows(path):
         if r.get("Counter_Name") != counter:
             continue
         v = float(r["Counter_Value"])
-        if "k_gemv" in r["Kernel_Name"]:
-            gemv.append(v)
-        elif "copyBuffer" in r["Kernel_Name"]:
+        name = r["Kernel_Name"]
+        if "copyBuffer" in name:
             copy.append(v)
-    return (sum(gemv) / len(gemv) if gemv else 0.0), len(gemv), (max(copy) if copy else 0.0)
+        elif (rx.search(name) if rx else "k_gemv" in name):
+            vals.append((int(r.get("Dispatch_Id", 0) or 0), v))
+    vals.sort()
+    if last:
+        vals = vals[-last:]
+    v = [x for _, x in vals]
+    return (sum(v) / len(v) if v else 0.0), len(v), (max(copy) if copy else 0.0)
 
 
-def traffic(fetch_csv, write_csv, copy_mib):
-    f_gemv, n_f, f_copy = _counter(fetch_csv, "FETCH_SIZE")
-    w_gemv, n_w, w_copy = _counter(write_csv, "WRITE_SIZE")
+def traffic(fetch_csv, write_csv, copy_mib, unit=None, last=0):
     copy_kib = float(copy_mib) * 1024.0
-    f_scale = copy_kib / f_copy if f_copy else float("nan")
-    w_scale = copy_kib / w_copy if w_copy else float("nan")
-    per_launch = (f_gemv * f_scale + w_gemv * w_scale) * 1024.0
-    return "\n".join([
-        f"gemv dispatches: {n_f} (FETCH_SIZE run), {n_w} (WRITE_SIZE run)",
-        f"FETCH_SIZE per GEMV dispatch: {f_gemv:.1f} KiB raw; copy of {copy_mib} MiB read {f_copy:.1f} KiB -> scale {f_scale:.4f}",
-        f"WRITE_SIZE per GEMV dispatch: {w_gemv:.1f} KiB raw; copy of {copy_mib} MiB wrote {w_copy:.1f} KiB -> scale {w_scale:.4f}",
-        f"traffic_bytes_per_launch: {per_launch:.0f}",
-    ])
+    name, patterns = ("gemv", [None]) if unit is None else (unit.split("=", 1)[0], unit.split("=", 1)[1].split("+"))
+    lines, total = [], 0.0
+    for pat in patterns:
+        f_avg, n_f, f_copy = _counter(fetch_csv, "FETCH_SIZE", pat, last)
+        w_avg, n_w, w_copy = _counter(write_csv, "WRITE_SIZE", pat, last)
+        f_scale = copy_kib / f_copy if f_copy else float("nan")
+        w_scale = copy_kib / w_copy if w_copy else float("nan")
+        total += (f_avg * f_scale + w_avg * w_scale) * 1024.0
+        label = pat or "k_gemv"
+        lines += [f"{label}: {n_f} dispatches (FETCH_SIZE run), {n_w} (WRITE_SIZE run)",
+                  f"  FETCH_SIZE per dispatch {f_avg:.1f} KiB raw; copy of {copy_mib} MiB read {f_copy:.1f} KiB -> scale {f_scale:.4f}",
+                  f"  WRITE_SIZE per dispatch {w_avg:.1f} KiB raw; copy of {copy_mib} MiB wrote {w_copy:.1f} KiB -> scale {w_scale:.4f}"]
+    lines.append(f"traffic_bytes_per_launch {name}: {total:.0f}" if unit else f"traffic_bytes_per_launch: {total:.0f}")
+    return "\n".join(lines)
 
 
 def main(argv):
     if len(argv) >= 2 and argv[0] == "stats":
         print(stats(argv[1]))
     elif len(argv) >= 4 and argv[0] == "traffic":
-        print(traffic(argv[1], argv[2], argv[3]))
+        unit = argv[4] if len(argv) >= 5 else None
+        last = int(argv[5].split("=", 1)[1]) if len(argv) >= 6 else 0
+        print(traffic(argv[1], argv[2], argv[3], unit, last))
     else:
         print(__doc__, file=sys.stderr)
         return 2

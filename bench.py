@@ -96,6 +96,32 @@ def hip_sync():
         raise RuntimeError(f"hipDeviceSynchronize failed: {rc}")
 
 
+class CounterWindow:
+    """roctxProfilerResume / Pause around the parts a counter run should see (rocprofv3
+    --selected-regions collects only inside them): the calibration copy and the timed steps.
+    Outside a profiler the calls do nothing."""
+
+    def __init__(self, on):
+        self.lib = None
+        if on:
+            self.lib = ctypes.CDLL("librocprofiler-sdk-roctx.so.1")
+            self.lib.roctxProfilerPause.argtypes = [ctypes.c_uint64]
+            self.lib.roctxProfilerResume.argtypes = [ctypes.c_uint64]
+            self.lib.roctxProfilerPause(0)
+
+    def __enter__(self):
+        if self.lib:
+            hip_sync()
+            self.lib.roctxProfilerResume(0)
+        return self
+
+    def __exit__(self, *exc):
+        if self.lib:
+            hip_sync()
+            self.lib.roctxProfilerPause(0)
+        return False
+
+
 def device_copy(mib):
     """One device-to-device copy of `mib` MiB: the known-size reference a counter run scales by."""
     lib = ctypes.CDLL("libamdhip64.so.7")
@@ -110,30 +136,50 @@ def device_copy(mib):
     hip_sync()
 
 
-def cpu_baseline(w, model, t5, prompt, seconds, adapters=None):
+def cpu_baseline(w, model, t5, seconds, adapters=None):
     """The oracle (a CPU restatement of the reference's ggml-CPU decode step, including its
-    per-step cross.kv projection) on the host: prefill untimed, then decode steps for about
-    `seconds` of wall time. For a batch workload it times request 0: the reference serves
-    requests one after another, so its aggregate rate is the one-request rate."""
+    per-step cross.kv projection) on the host, for about `seconds` of wall time: decode steps
+    centred on the continuation's mean key count, as the GPU's timed steps are. The positions
+    before them are not computed: the oracle's timing mode marks them as held by the cache
+    (zero rows; a step's cost depends on how many keys it attends, not on their values), so the
+    sample does not wait minutes for a prefill it does not time. For a batch workload it times
+    one request: the reference serves requests one after another, so its aggregate rate is the
+    one-request rate."""
+    import numpy as np
     from oracle import cpu_ref as R
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
     R.set_threads(threads)
     rm = R.RefModel(model.config, model.tensors, adapters)
-    # calibrate on a few steps, then run the bounded sample
+    c = model.config
     T = w["prompt"] + w["gen"]
-    _, _, rep, _ = rm.generate(t5, prompt, w["prompt"], T, top_k=250, temperature=1.0, cfg_coef=3.0,
-                               seed=w["seed"], recompute_cross_kv=True, max_forwards=4)
-    per = max(rep.decode_seconds / 3, 1e-3)
-    n = max(4, min(w["gen"], int(seconds / per)))
-    _, _, rep, _ = rm.generate(t5, prompt, w["prompt"], T, top_k=250, temperature=1.0, cfg_coef=3.0,
-                               seed=w["seed"], recompute_cross_kv=True, max_forwards=n + 1)
+    S = T + c.n_q
+    start = w["prompt"] + 1
+    mean_keys = (start + 1 + S - 1) // 2
+
+    def run(n):
+        # the first timed step attends mean_keys - n // 2 keys: a stand-in prompt of that length
+        p = max(w["prompt"], mean_keys - n // 2 - 2)
+        codes = np.zeros((c.n_q, p), np.int32)
+        _, _, rep, _ = rm.generate(t5, codes, p, T, top_k=250, temperature=1.0, cfg_coef=3.0, seed=w["seed"],
+                                   recompute_cross_kv=True, max_forwards=n + 1)
+        return rep, p + 2
+
+    R.lib().ref_set_timing_history(1)
+    try:
+        rep, _ = run(4)                                    # calibration
+        per = max(rep.decode_seconds / 3, 1e-3)
+        n = max(4, min(w["gen"], int(seconds / per)))
+        rep, k0 = run(n)
+    finally:
+        R.lib().ref_set_timing_history(0)
     steps = rep.forwards - 1
-    which = "request 0 of the batch (requests run one after another)" if w.get("requests", 1) > 1 else "same workload"
+    which = "one request of the batch (requests run one after another)" if w.get("requests", 1) > 1 else "same workload"
     return dict(value=round(steps / rep.decode_seconds, 3), unit="frames/s", cores=R.lib().ref_get_threads(),
                 kind="port",
-                sample=f"oracle CPU restatement of the reference ggml path, {which}: {w['prompt'] + 1}-token "
-                       f"prefill untimed, then the first {steps} decode steps timed "
-                       f"({rep.decode_seconds:.1f} s, prefill {rep.prefill_seconds:.1f} s)")
+                sample=f"oracle CPU restatement of the reference ggml path, {which}: {steps} decode steps "
+                       f"attending {k0}..{k0 + steps - 1} keys (centred on the continuation's mean, {mean_keys}) "
+                       f"timed in {rep.decode_seconds:.1f} s; the positions before them held as zero cache "
+                       f"rows, not computed")
 
 
 def serve_bench(mgx):
@@ -288,6 +334,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prompt", type=int, default=None,
                     help="prompt frames override (counter runs: fewer untimed prefill dispatches)")
+    ap.add_argument("--lead", type=int, default=None,
+                    help="untimed decode steps before the warmup (default: centre the timed steps on the "
+                         "continuation's middle; counter runs with a long --prompt pass 0)")
+    ap.add_argument("--counter-window", action="store_true",
+                    help="counter runs (rocprofv3 --selected-regions): collect only over the copy and the "
+                         "timed steps")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
@@ -309,8 +361,10 @@ def main():
     if args.prompt is not None:
         w["prompt"] = args.prompt
     mgx.load()
+    window = CounterWindow(args.counter_window)
     if args.copy_mib:
-        device_copy(args.copy_mib)
+        with window:
+            device_copy(args.copy_mib)
     t_build = time.time()
     model = mgx.SyntheticModel(w["shape"], w["wtype"], seed=w["seed"])
     c = model.config
@@ -357,6 +411,8 @@ def main():
     # before the timed ones).
     sess = new_session()
     lead = max(0, (D - args.steps) // 2 - args.warmup) if args.steps < D else 0
+    if args.lead is not None:
+        lead = max(0, args.lead)
     while lead > 0:
         lead -= sess.step(min(lead, 256))
     warm_left = args.warmup
@@ -369,11 +425,12 @@ def main():
             continue
         n = min(args.steps - timed_steps, sess.remaining())
         u0 = keys_now(sess)
-        hip_sync()
-        t0 = time.perf_counter()
-        done = sess.step(n)
-        hip_sync()
-        timed += time.perf_counter() - t0
+        with window:
+            hip_sync()
+            t0 = time.perf_counter()
+            done = sess.step(n)
+            hip_sync()
+            timed += time.perf_counter() - t0
         for i in range(done):
             bytes_total += step_bytes(c, BPW[w["wtype"]], 2 * R, w["n_ctx"], u0 + i, R, adapter_bytes)
         segments.append([u0, u0 + done - 1])
@@ -461,7 +518,7 @@ def main():
     }
     if not args.no_cpu:
         try:
-            out["cpu_baseline"] = cpu_baseline(w, model, t5, prompt, args.cpu_seconds, adapters)
+            out["cpu_baseline"] = cpu_baseline(w, model, t5, args.cpu_seconds, adapters)
         except Exception as e:  # the GPU figure stands without it
             out["cpu_baseline"] = {"error": str(e)}
     print(json.dumps(out), flush=True)

@@ -225,10 +225,12 @@ int mgx_server_stats(mgx_server* server, mgx_server_counters* out);
 void mgx_server_destroy(mgx_server* server);
 
 /* Launch timing (no reference counterpart; the reference has wall clocks only,
-   pipeline.cpp:15-18): with every > 0, each GEMV (kind 0) and self-attention (kind 1) launch
-   of every `every`-th loop iteration records its span on the GPU's constant-rate wall clock
+   pipeline.cpp:15-18): with every > 0, every `every`-th loop iteration runs outside the
+   captured graph (same kernels, launched one by one) and each of its GEMV (kind 0) and
+   self-attention (kind 1) launches records its span on the GPU's constant-rate wall clock
    (earliest block start to latest wave end -- a kernel tracer's duration; for attention, the
-   scores kernel's start to the reduce kernel's end). profile_read sums those milliseconds, the algorithmic bytes (weights at their stored
+   chunk kernel's first block start to the combine kernel's last wave end, the boundary between
+   them included). profile_read sums those milliseconds, the algorithmic bytes (weights at their stored
    precision; f32 K and V of the keys attended) and the launch count, for one kind of launch:
    MGX_PROF_GEMV every weight GEMV, MGX_PROF_ATTN the self-attention, or the GEMV of one
    projection (its adapter's A x launch, if any, is not included). */

@@ -1141,6 +1141,15 @@ REF_API int ref_use_guidance(float cfg_coef, int description_empty) {
     return cfg_coef != 0.0f && !description_empty;
 }
 
+/* Timing samples of long prompts: with the flag set, ref_generate replaces the prompt's prefill
+   forward by marking the caches as holding its positions (zero rows) and samples the first
+   step from zero logits. Every decode step after it attends the same number of keys as in the
+   real run, and its cost does not depend on the values, so a CPU timing sample of late decode
+   steps no longer waits minutes for a prefill it does not time. Codes and logits are then
+   meaningless: for timing only. */
+static int g_timing_history = 0;
+REF_API void ref_set_timing_history(int on) { g_timing_history = on; }
+
 /* codes_out: [n_q][max_gen_len]; first_logits: [n_q][card]; step_logits (optional):
    [S-start][n_q][card] combined logits of every forward, for step-by-step comparison.
    max_forwards > 0 stops after that many forwards (a bounded timing sample); the codes
@@ -1181,7 +1190,11 @@ REF_API int ref_generate(const ref_model* m, const float* t5_hidden, int n_ctx, 
         if (max_forwards > 0 && done >= max_forwards) break;
         const int nt = offset - previous;
         for (int q = 0; q < K; ++q) memcpy(feed + (size_t)q * nt, seq + (size_t)q * S + previous, sizeof(int32_t) * (size_t)nt);
-        if (ref_forward(dec, feed, nt, out)) { rc = -1; break; }
+        if (g_timing_history && offset == start) {
+            dec->used = nt;
+            dec->forwards += 1;
+            memset(out, 0, sizeof(float) * (size_t)c->card * K * n_seq);
+        } else if (ref_forward(dec, feed, nt, out)) { rc = -1; break; }
         ++done;
         const float* logits = out;
         if (guided) {

@@ -170,7 +170,22 @@ def test_attention_against_dense_float64():
         s = K.astype(np.float64) @ q.astype(np.float64) * 0.125
         p = np.exp(s - s.max())
         p /= p.sum()
-        np.testing.assert_allclose(out, VT[:, :u].astype(np.float64) @ p, atol=2e-6, rtol=1e-5)
+        want = VT[:, :u].astype(np.float64) @ p
+        np.testing.assert_allclose(out, want, atol=2e-6, rtol=1e-5)
+        if u > 300:
+            # the plausible combine mistakes (chunks not rescaled by exp(m_c - M), or the
+            # total taken over the last chunk only) miss this tolerance by far
+            nch = (u + 63) // 64
+            m = np.array([s[64 * c:64 * c + 64].max() for c in range(nch)])
+            e = [np.exp(s[64 * c:64 * c + 64] - m[c]) for c in range(nch)]
+            o = np.array([VT[:, 64 * c:64 * c + len(e[c])].astype(np.float64) @ e[c] for c in range(nch)])
+            S = np.array([x.sum() for x in e])
+            unscaled = o.sum(0) / S.sum()
+            w = np.exp(m - m.max())
+            right = (o * w[:, None]).sum(0) / (S * w).sum()
+            np.testing.assert_allclose(right, want, atol=1e-12)
+            assert np.abs(unscaled - want).max() > 100 * 2e-6
+            assert np.abs((o * w[:, None]).sum(0) / S[-1] - want).max() > 100 * 2e-6
 
 
 def test_masked_attention_equals_shorter_history():
