@@ -23,6 +23,8 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
+#include <cstdio>
+#include <cstdlib>
 
 #include "kernels.h"
 
@@ -578,6 +580,13 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
     float* tile = (float*)(lds + lds_act_bytes(WT, NC, in));
     double* red = (double*)(lds + lds_act_bytes(WT, NC, in) + (size_t)NC * R * 4);
 
+    // 0. the qkv epilogue's cache row per column, read before everything else so its latency
+    //    hides behind the weights instead of following the dots
+    int qpos[NC];
+    if constexpr (EPI == EPI_QKV) {
+#pragma unroll
+        for (int n = 0; n < NC; ++n) qpos[n] = a.pos[(a.col0 + (n < ncol ? n : ncol - 1)) >> a.cshift];
+    }
     // 1. activation source (prologue: thread group pcol = tid / 256 builds column pcol)
     const int pcol = tid >> 8, ptid = tid & 255;
     float4 xr[PRO == PRO_ACT ? 1 : KG], wr[PRO == PRO_ACT ? 1 : KG], br[PRO == PRO_ACT ? 1 : KG];
@@ -744,7 +753,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
         else {
             const int sec = row / a.dim, wi = row - sec * a.dim, head = wi >> 6, dm = wi & 63;
             if (sec == 0) a.y[(size_t)n * a.dim + wi] = r;
-            else (sec == 1 ? a.k : a.v)[(((size_t)kv_col(a, n) * a.heads + head) * a.cap + a.pos[(a.col0 + n) >> a.cshift]) * 64 + dm] = r;
+            else (sec == 1 ? a.k : a.v)[(((size_t)kv_col(a, n) * a.heads + head) * a.cap + qpos[n]) * 64 + dm] = r;
         }
     }
 }
@@ -900,18 +909,21 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
 // exp((double)m_c - M), total = the 64-wide butterfly of S_c * w_c (zeros past the column's
 // chunks), f_c = (float)(w_c / total); lane d then sums fmaf(o_c[d], f_c, .) over the chunks in
 // order. The head's 64 outputs go to the out-projection's activation.
+// MC: the launch's chunk count (4 per 256-key span of the graph); chunks past the column's
+// position take no part.
+template <int MC>
 __global__ __launch_bounds__(64) void k_attn_combine(AttnArgs a) {
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
     const size_t head = (size_t)n * a.heads + h, hc = head * a.max_chunks;
-    // every chunk slot of the head is loaded before the position is known; slots past the
+    // every chunk slot of the launch is loaded before the position is known; slots past the
     // column's chunks are never used
-    const int cl = lane < a.max_chunks ? lane : a.max_chunks - 1;
+    const int cl = lane < MC ? lane : MC - 1;
     const float mc0 = a.cmax[hc + cl];
     const double sc0 = a.csum[hc + cl];
     const float* op = a.opart + hc * 64 + lane;
-    float o[ATT_MAX_CHUNKS];
+    float o[MC];
 #pragma unroll
-    for (int k = 0; k < ATT_MAX_CHUNKS; ++k) o[k] = op[(size_t)(k < a.max_chunks ? k : a.max_chunks - 1) * 64];
+    for (int k = 0; k < MC; ++k) o[k] = op[(size_t)k * 64];
     const int u = a.pos[n >> a.cshift] + 1, nch = (u + ATT_CHUNK - 1) / ATT_CHUNK;
     const bool live = lane < nch;
     const float mc = live ? mc0 : -__builtin_inff();
@@ -923,7 +935,7 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnArgs a) {
     const float f = live ? (float)(w / total) : 0.0f;
     float r = 0.0f;
 #pragma unroll
-    for (int k = 0; k < ATT_MAX_CHUNKS; ++k) {
+    for (int k = 0; k < MC; ++k) {
         const float fk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), k));
         r = k < nch ? __builtin_fmaf(o[k], fk, r) : r;
     }
@@ -1513,6 +1525,11 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
             adr[k] = *src;
         }
     }
+    // the qkv epilogue's cache row of column tid (decode groups: staged in LDS with the adapter
+    // operands; prefill groups read theirs in the epilogue)
+    __shared__ int posl[16];
+    int posr = 0;
+    if (EPI == EPI_QKV && !WIDE) posr = a.pos[(a.col0 + (tid < ncol ? (tid & 15) : ncol - 1)) >> a.cshift];
     // keep every load above in flight together: the scheduler would otherwise sink each next
     // to its first use and pay the memory latency once per leaf
     __builtin_amdgcn_sched_barrier(0);
@@ -1552,7 +1569,8 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
             else {
                 const int sec = row / a.dim, wi = row - sec * a.dim, head = wi >> 6, dm = wi & 63;
                 if (sec == 0) a.y[(size_t)n * a.dim + wi] = y;
-                else (sec == 1 ? kcache : vcache)[(((size_t)kv_col(a, n) * a.heads + head) * a.cap + a.pos[(a.col0 + n) >> a.cshift]) * 64 + dm] = y;
+                else (sec == 1 ? kcache : vcache)[(((size_t)kv_col(a, n) * a.heads + head) * a.cap +
+                                                   (WIDE ? a.pos[(a.col0 + n) >> a.cshift] : posl[n])) * 64 + dm] = y;
             }
         }
     };
@@ -1618,6 +1636,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
 #pragma unroll
         for (int k = 0; k < AD_PER; ++k)
             if (tid + 64 * KW * k < ad_n) adsh[tid + 64 * KW * k] = adr[k];
+        if (EPI == EPI_QKV && tid < 16) posl[tid] = posr;
     }
     __syncthreads();
     for (int idx0 = 0; idx0 < ROWS * 16; idx0 += NT) {
@@ -1839,9 +1858,23 @@ void launch_gemv(const GemvArgs& a0, hipStream_t s) {
         }
     }
 }
+template <int SP>
+static void launch_combine(const AttnArgs& a, int spans, hipStream_t s) {
+    if constexpr (SP <= ATT_MAX_SPANS) {
+        if (spans == SP) hipLaunchKernelGGL(k_attn_combine<4 * SP>, dim3(a.heads, a.ncol), dim3(64), 0, s, a);
+        else launch_combine<SP + 1>(a, spans, s);
+    }
+}
+// nch: the chunk grid, 4 chunks per 256-key span (the launch's key count rounded up to spans)
 void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
+    if (nch % 4 != 0 || nch < 4 || nch / 4 > ATT_MAX_SPANS || nch > a.max_chunks || a.ncol < 1 ||
+        a.ncol > MF_MAX_COLS) {
+        std::fprintf(stderr, "launch_attention: %d chunks (whole spans up to %d, at most %d slots), %d columns\n",
+                     nch, ATT_MAX_SPANS, a.max_chunks, a.ncol);
+        std::abort();
+    }
     hipLaunchKernelGGL(k_attn_chunk, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(k_attn_combine, dim3(a.heads, a.ncol), dim3(64), 0, s, a);
+    launch_combine<1>(a, nch / 4, s);
 }
 // The same cross-attention for n_ctx <= 64 (one 64-key chunk) by one wave per (head, request):
 // the chunk of xattn_head with its combine reduced to out = fmaf(o, (float)(1 / sum), 0).
@@ -1856,6 +1889,24 @@ __device__ __forceinline__ void xattn_wave(const XAttnArgs& a, int h, int r, int
     const float* bias = a.bias ? a.bias + ((size_t)h * n_req + r) * a.bias_stride : nullptr;
     __shared__ float el[64];
     __shared__ float4 ol[16];
+    // every load first: q, the keys 4*it + g, the V rows g + 4k + 16mm, clamped to the n_ctx
+    // rows the buffers hold (so no load waits for the request's own key count, read alongside;
+    // rows past that count enter masked lanes only)
+    const int rows = a.n_ctx;
+    const float4 q = ((const float4*)(a.q + (size_t)r * a.dim + h * 64))[t];
+    float4 kv[16], vv[16];
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+        const int j = it * 4 + g, jl = j < rows ? j : rows - 1;
+        kv[it] = ((const float4*)(K + (size_t)jl * 64))[t];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+            const int j = g + 4 * k + 16 * mm, jl = j < rows ? j : rows - 1;
+            vv[4 * k + mm] = ((const float4*)(V + (size_t)jl * 64))[t];
+        }
     const int nc = a.nc ? a.nc[r] : a.n_ctx;
     if (nc <= 0) {
         // no conditioning: zeros (the gated cross.out leaves the residual unchanged)
@@ -1863,21 +1914,6 @@ __device__ __forceinline__ void xattn_wave(const XAttnArgs& a, int h, int r, int
         if (act && a.out_f) a.out_f[(size_t)r * a.dim + h * 64 + lane] = 0.0f;
         return;
     }
-    // every load first: q, the keys 4*it + g, the V rows g + 4k + 16mm (all clamped to the keys)
-    const float4 q = ((const float4*)(a.q + (size_t)r * a.dim + h * 64))[t];
-    float4 kv[16], vv[16];
-#pragma unroll
-    for (int it = 0; it < 16; ++it) {
-        const int j = it * 4 + g, jl = j < nc ? j : nc - 1;
-        kv[it] = ((const float4*)(K + (size_t)jl * 64))[t];
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-        for (int mm = 0; mm < 4; ++mm) {
-            const int j = g + 4 * k + 16 * mm, jl = j < nc ? j : nc - 1;
-            vv[4 * k + mm] = ((const float4*)(V + (size_t)jl * 64))[t];
-        }
     float p[16];
 #pragma unroll
     for (int it = 0; it < 16; ++it) {

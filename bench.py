@@ -76,7 +76,7 @@ def step_bytes(c, wbpw, n_seq, n_ctx, u, requests=1, adapter_bytes=0.0):
     return w + adapter_bytes + kv_read + kv_write + xkv + Q * C * n_seq * 4
 
 
-def gemv_traffic(workload, kernel):
+def unit_traffic(workload, kernel):
     """HBM bytes per launch of `kernel` from the committed counter summary, or None."""
     path = os.path.join(ROOT, "profiles", f"traffic_{workload.replace('-', '_')}.txt")
     try:
@@ -470,6 +470,9 @@ def main():
                     frac=round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
 
     per_kernel = {k: rate(k) for k in kinds if k not in ("gemv",)}
+    for k, v in per_kernel.items():
+        if v is not None:
+            v["traffic"] = unit_traffic(args.workload, k)
     timed_units = {k: v for k, v in per_kernel.items() if v is not None}
     # the dominant kernel: the largest share of a profiled step's GPU time
     dom = max(timed_units, key=lambda k: prof[k][0]) if timed_units else None
@@ -507,7 +510,7 @@ def main():
         "roofline_frac_step": round(bytes_total / timed / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": None if dom is None else {
             "bound": "hbm", "achieved": timed_units[dom]["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": timed_units[dom]["frac"], "traffic": gemv_traffic(args.workload, dom),
+            "frac": timed_units[dom]["frac"], "traffic": unit_traffic(args.workload, dom),
             "kernel": labels[dom], "launches_timed": timed_units[dom]["launches_timed"],
             "avg_launch_us": timed_units[dom]["avg_launch_us"],
             "bytes_per_launch": timed_units[dom]["bytes_per_launch"], "profiled_keys": prof_keys},
