@@ -105,29 +105,60 @@ __device__ __forceinline__ float gelu_erf(float x) {
     return 0.5f * x * (1.0f + e);
 }
 
-template <typename T> __device__ __forceinline__ T shfl_xor(T v, int m) { return __shfl_xor(v, m, 64); }
+// Lane l gets v[l ^ OFF], every lane of the wave active: the xor exchange of __shfl_xor without
+// its LDS crossbar round trip -- quad permutes for 1 and 2, two row shifts and a select for 4
+// and 8, the gfx950 permlane swaps for 16 and 32 (swapping a register with itself leaves each
+// lane's partner in one of the two results).
+template <int OFF> __device__ __forceinline__ uint32_t xor_lane_u(uint32_t v) {
+    const int lane = (int)(threadIdx.x & 63);
+    if constexpr (OFF == 32) {
+        auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return lane < 32 ? r[1] : r[0];
+    } else if constexpr (OFF == 16) {
+        auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16) ? r[0] : r[1];
+    } else if constexpr (OFF == 1) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, true);   // quad_perm [1,0,3,2]
+    } else if constexpr (OFF == 2) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, true);   // quad_perm [2,3,0,1]
+    } else {
+        static_assert(OFF == 4 || OFF == 8, "xor offsets 1 .. 32");
+        const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x100 + OFF, 0xf, 0xf, true);
+        const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x110 + OFF, 0xf, 0xf, true);
+        return (lane & OFF) ? dn : up;
+    }
+}
+template <int OFF> __device__ __forceinline__ float xor_lane(float v) {
+    return __uint_as_float(xor_lane_u<OFF>(__float_as_uint(v)));
+}
+template <int OFF> __device__ __forceinline__ int xor_lane(int v) { return (int)xor_lane_u<OFF>((uint32_t)v); }
+template <int OFF> __device__ __forceinline__ double xor_lane(double v) {
+    const uint64_t b = __double_as_longlong(v);
+    const uint32_t lo = xor_lane_u<OFF>((uint32_t)b), hi = xor_lane_u<OFF>((uint32_t)(b >> 32));
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+// v = op(v, v[l ^ off]) for off = OFF, OFF / 2, .., 1: the xor butterfly (each pair computes
+// op on the same two operands, so for a commutative op every lane ends with the same value)
+template <int OFF, typename T, typename Op> __device__ __forceinline__ T xor_reduce(T v, Op op) {
+    v = op(v, xor_lane<OFF>(v));
+    if constexpr (OFF > 1) return xor_reduce<OFF / 2>(v, op);
+    else return v;
+}
+__device__ __forceinline__ float fmax_sel(float a, float b) { return a > b ? a : b; }
+__device__ __forceinline__ float fmin_sel(float a, float b) { return a < b ? a : b; }
 
 // Butterfly over the 64 lanes of a wave: lane l < off adds lane l+off, off = 32..1.
 __device__ __forceinline__ float fold64(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = v + shfl_xor(v, off);
-    return v;
+    return xor_reduce<32>(v, [](float a, float b) { return a + b; });
 }
 __device__ __forceinline__ double fold64d(double v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = v + shfl_xor(v, off);
-    return v;
+    return xor_reduce<32>(v, [](double a, double b) { return a + b; });
 }
 
 // Q8_0 activation quantization of one element per lane; lanes 32k..32k+31 form one block.
 // Writes q and (from the block's first lane) the fp16-rounded scale widened to f32.
 __device__ __forceinline__ void quant_q8_lane(float v, int lane, int8_t* qdst, float* ddst) {
-    float amax = __builtin_fabsf(v);
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) {
-        const float o = shfl_xor(amax, off);
-        amax = amax > o ? amax : o;
-    }
+    const float amax = xor_reduce<16>(__builtin_fabsf(v), fmax_sel);
     const float d = amax / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     *qdst = (int8_t)__builtin_roundf(v * id);
@@ -769,25 +800,25 @@ __device__ __forceinline__ float halving16(float (&p)[16], int t) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const bool lo = (t & 8) == 0;
-        const float recv = shfl_xor(lo ? p[i + 8] : p[i], 8);
+        const float recv = xor_lane<8>(lo ? p[i + 8] : p[i]);
         a[i] = (lo ? p[i] : p[i + 8]) + recv;
     }
     float b[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const bool lo = (t & 4) == 0;
-        const float recv = shfl_xor(lo ? a[i + 4] : a[i], 4);
+        const float recv = xor_lane<4>(lo ? a[i + 4] : a[i]);
         b[i] = (lo ? a[i] : a[i + 4]) + recv;
     }
     float c[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const bool lo = (t & 2) == 0;
-        const float recv = shfl_xor(lo ? b[i + 2] : b[i], 2);
+        const float recv = xor_lane<2>(lo ? b[i + 2] : b[i]);
         c[i] = (lo ? b[i] : b[i + 2]) + recv;
     }
     const bool lo = (t & 1) == 0;
-    const float recv = shfl_xor(lo ? c[1] : c[0], 1);
+    const float recv = xor_lane<1>(lo ? c[1] : c[0]);
     return (lo ? c[0] : c[1]) + recv;
 }
 
@@ -796,12 +827,12 @@ __device__ __forceinline__ float halving16(float (&p)[16], int t) {
 // additions follow the butterfly p[l] + p[l+off], off = 8, 4, 2, 1.
 __device__ __forceinline__ float halving4(const float (&p)[4], int t) {
     const bool lo8 = (t & 8) == 0;
-    const float a0 = (lo8 ? p[0] : p[2]) + shfl_xor(lo8 ? p[2] : p[0], 8);
-    const float a1 = (lo8 ? p[1] : p[3]) + shfl_xor(lo8 ? p[3] : p[1], 8);
+    const float a0 = (lo8 ? p[0] : p[2]) + xor_lane<8>(lo8 ? p[2] : p[0]);
+    const float a1 = (lo8 ? p[1] : p[3]) + xor_lane<8>(lo8 ? p[3] : p[1]);
     const bool lo4 = (t & 4) == 0;
-    float b = (lo4 ? a0 : a1) + shfl_xor(lo4 ? a1 : a0, 4);
-    b = b + shfl_xor(b, 2);
-    return b + shfl_xor(b, 1);
+    float b = (lo4 ? a0 : a1) + xor_lane<4>(lo4 ? a1 : a0);
+    b = b + xor_lane<2>(b);
+    return b + xor_lane<1>(b);
 }
 
 // The 16 key-strided partials of a chunk's V.e, lane l of a wave holding partials (l >> 4) + 4k
@@ -867,8 +898,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     const int jt = (2 * ((t >> 3) & 1) + ((t >> 2) & 1)) * 16 + wave * 4 + g;
     const float sc = halving4(pr, t) * a.scale;
     float mx = jt < uc ? sc : -__builtin_inff();
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(mx, off); mx = mx > o ? mx : o; }
+    mx = xor_reduce<32>(mx, fmax_sel);
     if (lane == 0) red_f[wave] = mx;
     lds_barrier();
     float m = red_f[0];
@@ -928,8 +958,7 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnArgs a) {
     const bool live = lane < nch;
     const float mc = live ? mc0 : -__builtin_inff();
     float M = mc;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) { const float x = shfl_xor(M, off); M = M > x ? M : x; }
+    M = xor_reduce<32>(M, fmax_sel);
     const double w = live ? dexp((double)mc - (double)M) : 0.0;
     const double total = fold64d_b(live ? sc0 * w : 0.0);
     const float f = live ? (float)(w / total) : 0.0f;
@@ -992,8 +1021,7 @@ __device__ __forceinline__ void xattn_head(const float* qh, const float* K, cons
     float sc = halving16(p, t) * scale;
     if (bias && jt < uc) sc = sc + bias[j0 + jt];
     float m = jt < uc ? sc : -__builtin_inff();
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(m, off); m = m > o ? m : o; }
+    m = xor_reduce<32>(m, fmax_sel);
     el[j0 + jt] = jt < uc ? dexpf(sc - m) : 0.0f;
     lds_barrier();
     const double sum = fold64d_b((double)el[j0 + lane]);
@@ -1023,8 +1051,7 @@ __device__ __forceinline__ void xattn_head(const float* qh, const float* K, cons
         const bool live = lane < nch;
         const float mcv = live ? cm[lane] : -__builtin_inff();
         float M = mcv;
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) { const float x = shfl_xor(M, off); M = M > x ? M : x; }
+        M = xor_reduce<32>(M, fmax_sel);
         const double w = live ? dexp((double)mcv - (double)M) : 0.0;
         const double total = fold64d_b(live ? cs[lane] * w : 0.0);
         const float f = live ? (float)(w / total) : 0.0f;
@@ -1106,6 +1133,17 @@ __device__ __forceinline__ void dd_add(double& h, double& l, double b, double bl
     l = t - (h - s);
 }
 
+// One xor level of the (largest value, lowest index) reduction, and of the double-double sum.
+template <int OFF> __device__ __forceinline__ void argmax_level(float& best, int& bi) {
+    const float ob = xor_lane<OFF>(best);
+    const int oi = xor_lane<OFF>(bi);
+    if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
+}
+template <int OFF> __device__ __forceinline__ void dd_level(double& h, double& l) {
+    const double oh = xor_lane<OFF>(h), ol = xor_lane<OFF>(l);
+    dd_add(h, l, oh, ol);
+}
+
 // Block-wide inclusive scan of one int per thread (256 threads), through LDS.
 __device__ __forceinline__ int block_scan_i(int v, int* tmp) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1169,12 +1207,12 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
         int bi = 0x7fffffff;
         for (int i = tid; i < C; i += 256)
             if (lg[i] > best || (lg[i] == best && i < bi)) { best = lg[i]; bi = i; }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float ob = shfl_xor(best, off);
-            const int oi = shfl_xor(bi, off);
-            if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
-        }
+        argmax_level<32>(best, bi);
+        argmax_level<16>(best, bi);
+        argmax_level<8>(best, bi);
+        argmax_level<4>(best, bi);
+        argmax_level<2>(best, bi);
+        argmax_level<1>(best, bi);
         if (lane == 0) { red_f[wave] = best; red_i[wave] = bi; }
         __syncthreads();
         if (tid == 0) {
@@ -1189,8 +1227,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
         // softmax_into: peak, double exps, total in index order, float scale
         float pk = -__builtin_inff();
         for (int i = tid; i < C; i += 256) pk = pk < lg[i] ? lg[i] : pk;
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(pk, off); pk = pk < o ? o : pk; }
+        pk = xor_reduce<32>(pk, [](float a, float b) { return a < b ? b : a; });
         if (lane == 0) red_f[wave] = pk;
         __syncthreads();
         pk = red_f[0];
@@ -1208,8 +1245,12 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
             pr[i] = (float)e;
             dd_add(hs, ls, e, 0.0);
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) dd_add(hs, ls, shfl_xor(hs, off), shfl_xor(ls, off));
+        dd_level<32>(hs, ls);
+        dd_level<16>(hs, ls);
+        dd_level<8>(hs, ls);
+        dd_level<4>(hs, ls);
+        dd_level<2>(hs, ls);
+        dd_level<1>(hs, ls);
         if (lane == 0) { red_d[wave] = hs; dd_lo[wave] = ls; }
         __syncthreads();
         if (tid == 0) {
@@ -1258,8 +1299,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
             // Every partial sum of these floats is exact in double when no survivor is below
             // 2^-29 (each is a multiple of 2^-52 and the sums stay below 2): any summation
             // order then gives the reference's sequential result.
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(mn, off); mn = mn < o ? mn : o; }
+            mn = xor_reduce<32>(mn, fmin_sel);
             if (lane == 0) red_f[wave] = mn;
             __syncthreads();
             if (tid == 0) {
@@ -1271,8 +1311,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
             double t = 0.0;
             if (exact_sh) {
                 for (int i = tid; i < C; i += 256) t += (double)pr[i];
-#pragma unroll
-                for (int off = 32; off >= 1; off >>= 1) t += shfl_xor(t, off);
+                t = xor_reduce<32>(t, [](double a, double b) { return a + b; });
                 if (lane == 0) red_d[wave] = t;
                 __syncthreads();
                 if (tid == 0) inv_sh = (float)(1.0 / (red_d[0] + red_d[1] + red_d[2] + red_d[3]));
@@ -1286,8 +1325,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
         // categorical(probs, 1.0): the first i whose running double sum exceeds u
         float mn = __builtin_inff();
         for (int i = tid; i < C; i += 256) if (pr[i] > 0.0f) mn = mn < pr[i] ? mn : pr[i];
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(mn, off); mn = mn < o ? mn : o; }
+        mn = xor_reduce<32>(mn, fmin_sel);
         if (lane == 0) red_f[wave] = mn;
         __syncthreads();
         if (tid == 0) {
@@ -1926,8 +1964,7 @@ __device__ __forceinline__ void xattn_wave(const XAttnArgs& a, int h, int r, int
     float sc = halving16(p, t) * a.scale;
     if (bias && jt < nc) sc = sc + bias[jt];
     float m = jt < nc ? sc : -__builtin_inff();
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) { const float o = shfl_xor(m, off); m = m > o ? m : o; }
+    m = xor_reduce<32>(m, fmax_sel);
     if (act) el[jt] = jt < nc ? dexpf(sc - m) : 0.0f;
     __syncthreads();
     const float f = (float)(1.0 / fold64d_b((double)el[lane]));
