@@ -1914,13 +1914,38 @@ void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
     hipLaunchKernelGGL(k_attn_chunk, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
     launch_combine<1>(a, nch / 4, s);
 }
-// The same cross-attention for n_ctx <= 64 (one 64-key chunk) by one wave per (head, request):
-// the chunk of xattn_head with its combine reduced to out = fmaf(o, (float)(1 / sum), 0).
-// One wave: head h of request r, of H heads and n_req requests (threads past the first 64 of a
-// block, if any, take part in its barriers only).
+// Sum over the 16 lanes of a lane group of 8 values per lane: levels 8, 4 and 2 halve the
+// values, level 1 adds in place. Lanes t and t ^ 1 end with value 4*((t>>3)&1) + 2*((t>>2)&1) +
+// ((t>>1)&1); each value's additions follow the butterfly p[l] + p[l+off], off = 8, 4, 2, 1.
+__device__ __forceinline__ float halving8(const float (&p)[8], int t) {
+    float a[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bool lo = (t & 8) == 0;
+        const float recv = xor_lane<8>(lo ? p[i + 4] : p[i]);
+        a[i] = (lo ? p[i] : p[i + 4]) + recv;
+    }
+    float b[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const bool lo = (t & 4) == 0;
+        const float recv = xor_lane<4>(lo ? a[i + 2] : a[i]);
+        b[i] = (lo ? a[i] : a[i + 2]) + recv;
+    }
+    const bool lo = (t & 2) == 0;
+    const float c = (lo ? b[0] : b[1]) + xor_lane<2>(lo ? b[1] : b[0]);
+    return c + xor_lane<1>(c);
+}
+
+// The same cross-attention for n_ctx <= NK (one 64-key chunk; NK = 32 or 64 bounds the keys the
+// wave loads and scores) by one wave per (head, request): the chunk of xattn_head with its
+// combine reduced to out = fmaf(o, (float)(1 / sum), 0). One wave: head h of request r, of H
+// heads and n_req requests.
+template <int NK>
 __device__ __forceinline__ void xattn_wave(const XAttnArgs& a, int h, int r, int H, int n_req) {
+    static_assert(NK == 32 || NK == 64, "one wave scores 32 or 64 keys");
+    constexpr int NIT = NK / 4, NMM = NK / 16;
     const int lane = threadIdx.x & 63, g = lane >> 4, t = lane & 15;
-    const bool act = threadIdx.x < 64;
     const size_t kr = a.shared_kv ? 0 : (size_t)r;
     const float* K = a.k + (kr * H + h) * a.n_ctx * 64;
     const float* V = a.v + (kr * H + h) * a.n_ctx * 64;
@@ -1932,73 +1957,82 @@ __device__ __forceinline__ void xattn_wave(const XAttnArgs& a, int h, int r, int
     // rows past that count enter masked lanes only)
     const int rows = a.n_ctx;
     const float4 q = ((const float4*)(a.q + (size_t)r * a.dim + h * 64))[t];
-    float4 kv[16], vv[16];
+    float4 kv[NIT], vv[4 * NMM];
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
+    for (int it = 0; it < NIT; ++it) {
         const int j = it * 4 + g, jl = j < rows ? j : rows - 1;
         kv[it] = ((const float4*)(K + (size_t)jl * 64))[t];
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k)
 #pragma unroll
-        for (int mm = 0; mm < 4; ++mm) {
+        for (int mm = 0; mm < NMM; ++mm) {
             const int j = g + 4 * k + 16 * mm, jl = j < rows ? j : rows - 1;
-            vv[4 * k + mm] = ((const float4*)(V + (size_t)jl * 64))[t];
+            vv[NMM * k + mm] = ((const float4*)(V + (size_t)jl * 64))[t];
         }
     const int nc = a.nc ? a.nc[r] : a.n_ctx;
     if (nc <= 0) {
         // no conditioning: zeros (the gated cross.out leaves the residual unchanged)
-        if (act) put_act(a.out, r, h * 64 + lane, 0.0f, lane);
-        if (act && a.out_f) a.out_f[(size_t)r * a.dim + h * 64 + lane] = 0.0f;
+        put_act(a.out, r, h * 64 + lane, 0.0f, lane);
+        if (a.out_f) a.out_f[(size_t)r * a.dim + h * 64 + lane] = 0.0f;
         return;
     }
-    float p[16];
+    float p[NIT];
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
+    for (int it = 0; it < NIT; ++it) {
         float v = __builtin_fmaf(q.x, kv[it].x, 0.0f);
         v = __builtin_fmaf(q.y, kv[it].y, v);
         v = __builtin_fmaf(q.z, kv[it].z, v);
         p[it] = __builtin_fmaf(q.w, kv[it].w, v);
     }
-    const int jt = 4 * t + g;
-    float sc = halving16(p, t) * a.scale;
+    // this lane's key after the halving reduce
+    int jt;
+    float sc;
+    if constexpr (NK == 64) {
+        jt = 4 * t + g;
+        sc = halving16(p, t) * a.scale;
+    } else {
+        jt = 4 * (4 * ((t >> 3) & 1) + 2 * ((t >> 2) & 1) + ((t >> 1) & 1)) + g;
+        sc = halving8(p, t) * a.scale;
+    }
     if (bias && jt < nc) sc = sc + bias[jt];
     float m = jt < nc ? sc : -__builtin_inff();
     m = xor_reduce<32>(m, fmax_sel);
-    if (act) el[jt] = jt < nc ? dexpf(sc - m) : 0.0f;
+    if (NK == 64 || (t & 1) == 0) el[jt] = jt < nc ? dexpf(sc - m) : 0.0f;
     __syncthreads();
-    const float f = (float)(1.0 / fold64d_b((double)el[lane]));
+    const float f = (float)(1.0 / fold64d_b(lane < NK ? (double)el[lane] : 0.0));
     float4 P[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int mm = 0; mm < 4; ++mm) {
+        for (int mm = 0; mm < NMM; ++mm) {
             const int j = g + 4 * k + 16 * mm;
             if (j < nc) {
                 const float e = el[j];
-                acc.x = __builtin_fmaf(e, vv[4 * k + mm].x, acc.x);
-                acc.y = __builtin_fmaf(e, vv[4 * k + mm].y, acc.y);
-                acc.z = __builtin_fmaf(e, vv[4 * k + mm].z, acc.z);
-                acc.w = __builtin_fmaf(e, vv[4 * k + mm].w, acc.w);
+                acc.x = __builtin_fmaf(e, vv[NMM * k + mm].x, acc.x);
+                acc.y = __builtin_fmaf(e, vv[NMM * k + mm].y, acc.y);
+                acc.z = __builtin_fmaf(e, vv[NMM * k + mm].z, acc.z);
+                acc.w = __builtin_fmaf(e, vv[NMM * k + mm].w, acc.w);
             }
         }
         P[k] = acc;
     }
     const float4 o4 = fold_partials16(P);
-    if (act && lane < 16) ol[lane] = o4;
+    if (lane < 16) ol[lane] = o4;
     __syncthreads();
     const float o = __builtin_fmaf(((const float*)ol)[lane], f, 0.0f);
-    if (!act) return;
     put_act(a.out, r, h * 64 + lane, o, lane);
     if (a.out_f) a.out_f[(size_t)r * a.dim + h * 64 + lane] = o;
 }
+template <int NK>
 __global__ __launch_bounds__(64) void k_xattn_w(XAttnArgs a) {
-    xattn_wave(a, blockIdx.x, blockIdx.y, gridDim.x, gridDim.y);
+    xattn_wave<NK>(a, blockIdx.x, blockIdx.y, gridDim.x, gridDim.y);
 }
 
 void launch_xattn(const XAttnArgs& a, int heads, int n_req, hipStream_t s) {
-    if (a.n_ctx <= 64) hipLaunchKernelGGL(k_xattn_w, dim3(heads, n_req), dim3(64), 0, s, a);
+    if (a.n_ctx <= 32) hipLaunchKernelGGL(k_xattn_w<32>, dim3(heads, n_req), dim3(64), 0, s, a);
+    else if (a.n_ctx <= 64) hipLaunchKernelGGL(k_xattn_w<64>, dim3(heads, n_req), dim3(64), 0, s, a);
     else hipLaunchKernelGGL(k_xattn, dim3(heads, n_req), dim3(256), 0, s, a);
 }
 void launch_xkv_split(const float* kv, int n_ctx, int rows, int dim, float* k, float* v, hipStream_t s) {
