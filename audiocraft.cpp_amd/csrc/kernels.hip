@@ -23,8 +23,8 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
-#include <cstdio>
-#include <cstdlib>
+#include <stdexcept>
+#include <string>
 
 #include "kernels.h"
 
@@ -1906,11 +1906,11 @@ static void launch_combine(const AttnArgs& a, int spans, hipStream_t s) {
 // nch: the chunk grid, 4 chunks per 256-key span (the launch's key count rounded up to spans)
 void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
     if (nch % 4 != 0 || nch < 4 || nch / 4 > ATT_MAX_SPANS || nch > a.max_chunks || a.ncol < 1 ||
-        a.ncol > MF_MAX_COLS) {
-        std::fprintf(stderr, "launch_attention: %d chunks (whole spans up to %d, at most %d slots), %d columns\n",
-                     nch, ATT_MAX_SPANS, a.max_chunks, a.ncol);
-        std::abort();
-    }
+        a.ncol > MF_MAX_COLS)
+        throw std::logic_error("internal: attention launch of " + std::to_string(nch) + " chunks over " +
+                               std::to_string(a.ncol) + " columns (whole 256-key spans up to " +
+                               std::to_string(ATT_MAX_SPANS) + ", at most " + std::to_string(a.max_chunks) +
+                               " chunk slots)");
     hipLaunchKernelGGL(k_attn_chunk, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
     launch_combine<1>(a, nch / 4, s);
 }

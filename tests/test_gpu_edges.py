@@ -148,3 +148,20 @@ def test_sixteen_columns_over_several_chunks(M, dora):
         assert step is None, f"request {i}: mixed logits part at step {step // gst[0].size}"
         assert np.array_equal(gf, rf) and np.array_equal(gc, rc), f"request {i}"
     b.close()
+
+
+@pytest.mark.parametrize("n_ctx", [1, 32, 33, 64, 65, 200])
+def test_memory_lengths_across_the_cross_attention_kernels(M, n_ctx):
+    """Conditioning of 1-32 tokens runs the 32-key cross-attention wave, 33-64 the 64-key wave,
+    65-256 the 256-thread kernel (lm.h:181-199): each against the oracle, prefill and steps."""
+    from oracle import cpu_ref as R
+    print(f"memory of {n_ctx} tokens, tiny Q8_0", flush=True)
+    m = H.model("tiny", 8, 11)
+    c = m.config
+    t5 = H.memory(12, n_ctx)
+    ids = H.codes(13, c.n_q, 10, c.card)
+    gs = M.Stream(M.Model(c, m.tensors), 16, 2, t5, True)
+    rd = R.RefDecoder(H.ref_model("tiny", 8, 11), 16, 2, t5, True)
+    for t0, t1 in [(0, 6)] + [(t, t + 1) for t in range(6, 10)]:
+        got, want = gs.forward(ids[:, t0:t1]), rd.forward(ids[:, t0:t1])
+        assert np.array_equal(got, want), f"positions {t0}..{t1 - 1}: max {np.abs(got - want).max()}"
