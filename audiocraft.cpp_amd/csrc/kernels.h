@@ -14,8 +14,8 @@ enum { PRO_LN = 0, PRO_F32 = 1, PRO_ACT = 2 };
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GELU_ACT = 3 };
 
 constexpr int ATT_CHUNK = 64;       // keys per attention chunk (fixes the reduction order)
-constexpr int ATT_SPAN = 256;       // a step's attention grid covers whole 256-key spans (4 chunks),
-                                    // so one captured step graph serves 256 positions
+constexpr int ATT_SPAN = 256;       // cache rows per head are allocated in whole 256-key spans; a
+                                    // step's attention grid covers the 64-key chunks of its key count
 constexpr int ATT_MAX_SPANS = 16;   // capacity up to 4096 positions
 constexpr int ATT_MAX_CHUNKS = ATT_MAX_SPANS * ATT_SPAN / ATT_CHUNK;
 constexpr int MAX_CARD = 2048;   // sampler's LDS rows

@@ -939,8 +939,8 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
 // exp((double)m_c - M), total = the 64-wide butterfly of S_c * w_c (zeros past the column's
 // chunks), f_c = (float)(w_c / total); lane d then sums fmaf(o_c[d], f_c, .) over the chunks in
 // order. The head's 64 outputs go to the out-projection's activation.
-// MC: the launch's chunk count (4 per 256-key span of the graph); chunks past the column's
-// position take no part.
+// MC: the launch's chunk count (the 64-key chunks of its largest key count); chunks past the
+// column's position take no part.
 template <int MC>
 __global__ __launch_bounds__(64) void k_attn_combine(AttnArgs a) {
     const int h = blockIdx.x, n = blockIdx.y, lane = threadIdx.x;
@@ -1896,23 +1896,21 @@ void launch_gemv(const GemvArgs& a0, hipStream_t s) {
         }
     }
 }
-template <int SP>
-static void launch_combine(const AttnArgs& a, int spans, hipStream_t s) {
-    if constexpr (SP <= ATT_MAX_SPANS) {
-        if (spans == SP) hipLaunchKernelGGL(k_attn_combine<4 * SP>, dim3(a.heads, a.ncol), dim3(64), 0, s, a);
-        else launch_combine<SP + 1>(a, spans, s);
+template <int MC>
+static void launch_combine(const AttnArgs& a, int nch, hipStream_t s) {
+    if constexpr (MC <= ATT_MAX_CHUNKS) {
+        if (nch == MC) hipLaunchKernelGGL(k_attn_combine<MC>, dim3(a.heads, a.ncol), dim3(64), 0, s, a);
+        else launch_combine<MC + 1>(a, nch, s);
     }
 }
-// nch: the chunk grid, 4 chunks per 256-key span (the launch's key count rounded up to spans)
+// nch: the chunk grid, the 64-key chunks of the launch's largest key count
 void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
-    if (nch % 4 != 0 || nch < 4 || nch / 4 > ATT_MAX_SPANS || nch > a.max_chunks || a.ncol < 1 ||
-        a.ncol > MF_MAX_COLS)
+    if (nch < 1 || nch > ATT_MAX_CHUNKS || nch > a.max_chunks || a.ncol < 1 || a.ncol > MF_MAX_COLS)
         throw std::logic_error("internal: attention launch of " + std::to_string(nch) + " chunks over " +
-                               std::to_string(a.ncol) + " columns (whole 256-key spans up to " +
-                               std::to_string(ATT_MAX_SPANS) + ", at most " + std::to_string(a.max_chunks) +
+                               std::to_string(a.ncol) + " columns (at most " + std::to_string(a.max_chunks) +
                                " chunk slots)");
     hipLaunchKernelGGL(k_attn_chunk, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
-    launch_combine<1>(a, nch / 4, s);
+    launch_combine<1>(a, nch, s);
 }
 // Sum over the 16 lanes of a lane group of 8 values per lane: levels 8, 4 and 2 halve the
 // values, level 1 adds in place. Lanes t and t ^ 1 end with value 4*((t>>3)&1) + 2*((t>>2)&1) +

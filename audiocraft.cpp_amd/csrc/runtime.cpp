@@ -259,7 +259,7 @@ bool mf_src(const mgx::DevMat& w, int ncol, int epi) {
 // - ids_base]. With `heads`, the step's logits land in s->logits. `position` is the host's view
 // of the largest position: it sizes the attention grids (the kernels read each column's exact
 // key count on the device). Ends by advancing the device positions.
-int att_spans(int position) { return position / mgx::ATT_SPAN + 1; }
+int att_chunks(int position) { return position / mgx::ATT_CHUNK + 1; }
 
 void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int ids_req_stride, bool heads,
           const mgx::SampleArgs* sample, int position, int ncol = 0) {
@@ -298,7 +298,7 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
             at.out_f = L.ad[P_OUT] ? s->act_o.f : nullptr;
             // f32 K and V of every key attended, every stream
             at.stamp = s->stamp_slot(PROF_ATTN, 2.0 * N * c.heads * (position + 1) * 64 * 4);
-            mgx::launch_attention(at, att_spans(position) * (mgx::ATT_SPAN / mgx::ATT_CHUNK), s->hs);
+            mgx::launch_attention(at, att_chunks(position), s->hs);
         }
         {
             s->prof_tag = MGX_PROF_OUT;
@@ -838,15 +838,15 @@ struct mgx_session {
     double prefill_seconds = 0.0, decode_seconds = 0.0;
     int prof_every = 0;
     // Captured prefill positions (no heads) and decode steps (heads, CFG mix, sampling,
-    // position advance), one pair per attention span count: every kernel reads the position
-    // from the device, so a graph replays for every position with that many 256-key spans.
-    hipGraphExec_t g_body[mgx::ATT_MAX_SPANS] = {}, g_step[mgx::ATT_MAX_SPANS] = {};
+    // position advance), one pair per attention chunk count: every kernel reads the position
+    // from the device, so a graph replays for every position with that many 64-key chunks.
+    hipGraphExec_t g_body[mgx::ATT_MAX_CHUNKS] = {}, g_step[mgx::ATT_MAX_CHUNKS] = {};
     // MGX_GRAPHS=0 launches the same kernels one by one (for tools that do not follow
     // stream capture, such as kernel tracers).
     bool use_graphs = true;
     ~mgx_session() {
         if (s && s->hs) (void)hipStreamSynchronize(s->hs);
-        for (int i = 0; i < mgx::ATT_MAX_SPANS; ++i) {
+        for (int i = 0; i < mgx::ATT_MAX_CHUNKS; ++i) {
             if (g_body[i]) (void)hipGraphExecDestroy(g_body[i]);
             if (g_step[i]) (void)hipGraphExecDestroy(g_step[i]);
         }
@@ -980,7 +980,7 @@ void run_position(mgx_session* ss, bool full, bool profiled, int position) {
         step(s, ss->dseq, ss->S, 0, ss->K * ss->S, full, full ? &ss->sa : nullptr, position);
         return;
     }
-    hipGraphExec_t& g = (full ? ss->g_step : ss->g_body)[att_spans(position) - 1];
+    hipGraphExec_t& g = (full ? ss->g_step : ss->g_body)[att_chunks(position) - 1];
     if (!g) g = capture(ss, full, position);
     HIP_OK(hipGraphLaunch(g, s->hs));
 }
@@ -1205,7 +1205,7 @@ struct mgx_slots {
     uint8_t* hmask = nullptr;
     float *huni = nullptr, *ht5 = nullptr;
     mgx::SampleArgs sa{};
-    hipGraphExec_t g[mgx::ATT_MAX_SPANS] = {};
+    hipGraphExec_t g[mgx::ATT_MAX_CHUNKS] = {};
     bool use_graphs = true;
     struct Slot { bool live = false, unread = false; int pos = 0, start = 0, S = 0, T = 0; };
     std::vector<Slot> slot;
@@ -1381,7 +1381,7 @@ void slots_run(mgx_slots* sl, int steps) {
         if (!sl->use_graphs) {
             step(s, sl->dseq, sl->seq_len, 0, sl->K * sl->seq_len, true, &sl->sa, top);
         } else {
-            hipGraphExec_t& g = sl->g[att_spans(top) - 1];
+            hipGraphExec_t& g = sl->g[att_chunks(top) - 1];
             if (!g) g = slots_capture(sl, top);
             HIP_OK(hipGraphLaunch(g, s->hs));
         }
