@@ -1,8 +1,8 @@
 """Summaries of rocprofv3 CSV output for the decode-step kernels.
 
     python3 -m mgx.rocprof_summary stats <kernel_stats.csv>
-        per-kernel calls / total / average / min / max duration, GEMV instances also summed
-        into one "k_gemv (all instances)" line;
+        per-kernel calls / total / average / min / max duration, the GEMV and attention-combine
+        instances also summed into one "(all instances)" line each;
     python3 -m mgx.rocprof_summary traffic <fetch counter_collection.csv> <write counter_collection.csv> <copy MiB>
                                            [<name>=<regex>[+<regex>...] [last=<n>]]
         average FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the GEMV dispatches -- or, with a
@@ -34,14 +34,16 @@ def stats(path):
         agg[r["Name"]] = (int(r["Calls"]), float(r["TotalDurationNs"]), float(r["AverageNs"]), float(r["MinNs"]),
                           float(r["MaxNs"]), float(r["Percentage"]))
     out = [f"{'kernel':96s} {'calls':>8s} {'total_ms':>10s} {'avg_us':>8s} {'min_us':>8s} {'max_us':>8s} {'pct':>6s}"]
-    g_calls, g_total = 0, 0.0
+    families = {"k_gemv": [0, 0.0], "k_attn_combine": [0, 0.0]}
     for name, (calls, total, avg, mn, mx, pct) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
         out.append(f"{_short(name):96s} {calls:8d} {total / 1e6:10.3f} {avg / 1e3:8.2f} {mn / 1e3:8.2f} {mx / 1e3:8.2f} {pct:6.2f}")
-        if "k_gemv" in name:
-            g_calls += calls
-            g_total += total
-    if g_calls:
-        out.append(f"{'k_gemv (all instances)':96s} {g_calls:8d} {g_total / 1e6:10.3f} {g_total / g_calls / 1e3:8.2f}")
+        for fam, acc in families.items():
+            if fam in name:
+                acc[0] += calls
+                acc[1] += total
+    for fam, (calls, total) in families.items():
+        if calls:
+            out.append(f"{fam + ' (all instances)':96s} {calls:8d} {total / 1e6:10.3f} {total / calls / 1e3:8.2f}")
     return "\n".join(out)
 
 
