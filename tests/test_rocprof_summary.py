@@ -1,0 +1,61 @@
+"""The rocprofv3 CSV summaries behind the committed profiles: per-kernel stats with the GEMV and
+attention-combine families summed, and the counter traffic per launch scaled by the copy of
+known size (FETCH_SIZE reads half of a copy's bytes on this GPU, WRITE_SIZE all of them)."""
+import csv
+
+import pytest
+
+from mgx import rocprof_summary as S
+
+
+def write(path, rows, fields):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=fields)
+        w.writeheader()
+        for r in rows:
+            w.writerow(r)
+
+
+def counters(path, counter, per_kernel, copy_kib):
+    rows, d = [], 0
+    for name, vals in per_kernel:
+        for v in vals:
+            d += 1
+            rows.append({"Dispatch_Id": d, "Kernel_Name": name, "Counter_Name": counter, "Counter_Value": v})
+    rows.append({"Dispatch_Id": 0, "Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": counter,
+                 "Counter_Value": copy_kib})
+    write(path, rows, ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+
+
+def test_traffic_scales_by_the_copy_and_takes_the_last_dispatches(tmp_path):
+    f, w = tmp_path / "f.csv", tmp_path / "w.csv"
+    qkv = "void mgx::k_gemv<8, 2, 16, 3, 0, 2, 8>(mgx::GemvArgs)"
+    ff0 = "void mgx::k_gemv<8, 2, 16, 3, 0, 3, 8>(mgx::GemvArgs)"
+    # early dispatches (prefill) read more; the unit takes the last two of its kernel
+    counters(f, "FETCH_SIZE", [(qkv, [9000.0, 3000.0, 3000.0]), (ff0, [5000.0])], 512.0 * 1024)
+    counters(w, "WRITE_SIZE", [(qkv, [90.0, 30.0, 30.0]), (ff0, [20.0])], 1024.0 * 1024)
+    out = S.traffic(str(f), str(w), 1024, "qkv=k_gemv<8, 2, 16, 3, 0, 2, 8>", last=2)
+    line = [l for l in out.splitlines() if l.startswith("traffic_bytes_per_launch qkv:")][0]
+    assert float(line.split(":")[1]) == pytest.approx((3000.0 * 2.0 + 30.0 * 1.0) * 1024)
+    # a unit of two kernels adds one dispatch of each
+    out = S.traffic(str(f), str(w), 1024, "both=k_gemv<8, 2, 16, 3, 0, 2+k_gemv<8, 2, 16, 3, 0, 3", last=1)
+    line = [l for l in out.splitlines() if l.startswith("traffic_bytes_per_launch both:")][0]
+    assert float(line.split(":")[1]) == pytest.approx(((3000.0 + 5000.0) * 2.0 + (30.0 + 20.0)) * 1024)
+
+
+def test_stats_sums_the_instance_families(tmp_path):
+    p = tmp_path / "stats.csv"
+    rows = [("void mgx::k_gemv<8, 2, 16, 3, 0, 2, 8>(mgx::GemvArgs)", 10, 60000.0),
+            ("void mgx::k_gemv<8, 1, 16, 3, 0, 0, 4>(mgx::GemvArgs)", 10, 40000.0),
+            ("void mgx::k_attn_combine<20>(mgx::AttnArgs)", 4, 12000.0),
+            ("void mgx::k_attn_combine<21>(mgx::AttnArgs)", 4, 14000.0),
+            ("mgx::k_attn_chunk(mgx::AttnArgs)", 8, 64000.0)]
+    write(p, [{"Name": n, "Calls": c, "TotalDurationNs": t, "AverageNs": t / c, "MinNs": t / c, "MaxNs": t / c,
+               "Percentage": 0.0} for n, c, t in rows],
+          ["Name", "Calls", "TotalDurationNs", "AverageNs", "MinNs", "MaxNs", "Percentage"])
+    out = S.stats(str(p)).splitlines()
+    assert out[1].startswith("mgx::k_attn_chunk")                 # largest total first
+    gemv = [l for l in out if l.startswith("k_gemv (all instances)")][0].split()
+    assert gemv[3:6] == ["20", "0.100", "5.00"]
+    comb = [l for l in out if l.startswith("k_attn_combine (all instances)")][0].split()
+    assert comb[3:6] == ["8", "0.026", "3.25"]
