@@ -3,7 +3,7 @@ a stream reset and reused over stale cache rows (the reference fills its caches 
 so a read past `used` shows, tests/kv_attention_test.cpp:96-103), the reference's two
 Decoder::forward errors (KV overflow, kv_cache.h:73-77; a multi-token forward after history,
 pipeline.cpp:81-83), prefill groups that end in a ragged 16-column group, and 16-column
-decode steps attending several 256-key chunks."""
+decode steps attending many 64-key chunks."""
 import numpy as np
 import pytest
 
@@ -24,7 +24,7 @@ def M():
 
 @pytest.mark.parametrize("wtype", [8, 1])
 def test_reset_over_stale_rows_matches_fresh_oracle(M, wtype):
-    """A long sequence fills 300 rows of every cache (two 256-key chunks); after a reset a
+    """A long sequence fills 300 rows of every cache (five 64-key chunks, two 256-key spans); after a reset a
     shorter, different sequence must give exactly what a fresh decoder gives: no row past the
     new position may leak into the attention, whatever it holds."""
     from oracle import cpu_ref as R
@@ -119,8 +119,8 @@ def test_ragged_wide_group_with_adapters(M, n_seq, prefill, dora):
 @pytest.mark.parametrize("dora", [False, True])
 def test_sixteen_columns_over_several_chunks(M, dora):
     """The batched serving shape in small: 8 guided requests (16 columns per step) with a
-    300-frame prompt and 600 frames in all, so decode steps attend up to 603 keys: three
-    256-key chunks at 16 columns, each request against its own oracle generation."""
+    300-frame prompt and 600 frames in all, so decode steps attend up to 603 keys: ten
+    64-key chunks at 16 columns, each request against its own oracle generation."""
     from oracle import cpu_ref as R
     print(f"8 guided requests x 600 frames, tiny Q8_0, dora={dora}", flush=True)
     m = H.model("tiny", 8, 9)

@@ -80,7 +80,7 @@ def test_grouped_prefill_matches_oracle(mgx, wtype, n_seq):
     """A prefill runs its positions 64 / n_seq at a time (each column at its own position, causal
     by key count; the matrix-core GEMVs take the 64 columns as four 16-column groups against one
     load of the weights): prompts of 2, 17, 70 and 300 tokens -- one partial group, partial
-    16-column groups, several groups, a 256-key chunk boundary inside a group -- then single
+    16-column groups, several groups, a 256-key span boundary inside a group -- then single
     steps, against the oracle's masked prefill (n_seq 3 and 16 keep one position at a time and
     are covered above)."""
     from oracle import cpu_ref as R
