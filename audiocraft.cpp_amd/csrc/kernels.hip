@@ -64,13 +64,15 @@ __device__ __forceinline__ float dexpf(float x) { return (float)dexp((double)x);
 
 // erf: two Chebyshev interpolants in monomial form (erf_coeffs.py derives them from 40-digit
 // values): |x| < 1: x * P(2x^2 - 1), P of degree 11; 1 <= |x| < 4: 1 - Q(|x| * 2/3 - 5/3), Q
-// (erfc on [1, 4]) of degree 20; +-1 beyond. Absolute error below 1.5e-15 and 1.3e-12.
-__device__ __constant__ double ERF_P[12] = {
+// (erfc on [1, 4]) of degree 20; +-1 beyond. Absolute error below 1.5e-15 and 1.3e-12. The
+// coefficients are compile-time constants: the unrolled Horner loops take them as immediates
+// (an array in constant memory cost a cold scalar load in every GELU epilogue).
+constexpr double ERF_P[12] = {
     0x1.ee51eb23cb7ebp-1, -0x1.1fd162921520ep-3, 0x1.454368017b319p-6,
     -0x1.2b902b7b26e28p-9, 0x1.c82aa24968f47p-13, -0x1.263991d3aca15p-16,
     0x1.4866394fa4c3ep-20, -0x1.429e4c163b13bp-24, 0x1.1ad503d95b599p-28,
     -0x1.c02cc0da54c52p-33, 0x1.4424c09b26e7bp-37, -0x1.2d4c29f5686cbp-42};
-__device__ __constant__ double ERF_Q[21] = {
+constexpr double ERF_Q[21] = {
     0x1.aab859b20b140p-12, -0x1.ac44a2cdb3c80p-9, 0x1.9180586b55ae8p-7,
     -0x1.cdb9fd59ee319p-6, 0x1.65964ef5668ffp-5, -0x1.7c8c5ebf7f0ccp-5,
     0x1.0521f53919ddep-5, -0x1.2faaceec90308p-7, -0x1.b5d2183e391e9p-8,
@@ -79,7 +81,7 @@ __device__ __constant__ double ERF_Q[21] = {
     0x1.3dc0c2909a110p-12, -0x1.e193532b72642p-14, -0x1.3af7b90db0f1ap-15,
     0x1.17a5709f8fe8ap-15, 0x1.048f70bb1e4f4p-20, -0x1.e180cb94805c1p-19};
 
-__device__ double derf(double x) {
+__device__ __forceinline__ double derf(double x) {
     const double ax = __builtin_fabs(x);
     if (ax < 1.0) {
         const double t = __builtin_fma(2.0 * x, x, -1.0);
