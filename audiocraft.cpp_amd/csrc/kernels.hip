@@ -1192,6 +1192,11 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
     const float* uniforms = a.uniforms + (size_t)r * a.seq_len * a.n_q;
     int32_t* seq = a.seq + (size_t)r * a.n_q * a.seq_len;
     const uint8_t* mask = a.mask + (size_t)r * a.mask_stride;
+    // the step's mask byte, uniform and sequence slot, read up front (each used only after
+    // several barriers; this block is the slot's only writer)
+    const uint8_t mask_v = mask[(size_t)q * a.seq_len + offset];
+    const float u_v = uniforms[(size_t)offset * a.n_q + q];
+    const int32_t slot_v = seq[(size_t)q * a.seq_len + offset];
     for (int i = tid; i < C; i += 256) {
         float v = cond[i];
         if (guided) v = null_l[i] + (cond[i] - null_l[i]) * cfg_coef;
@@ -1200,7 +1205,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
         if (stepl) stepl[i] = v;
     }
     __syncthreads();
-    const bool timed = mask[(size_t)q * a.seq_len + offset] != 0;
+    const bool timed = mask_v != 0;
     int token;
     if (!timed) token = a.special;
     else if (!use_sampling || !(temperature > 0.0f)) {
@@ -1337,7 +1342,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
             pick_sh = C - 1;
         }
         __syncthreads();
-        const double target = (double)uniforms[(size_t)offset * a.n_q + q] * 1.0;
+        const double target = (double)u_v * 1.0;
         if (exact_sh) {
             // thread t owns elements [SMP_PER*t, SMP_PER*t + SMP_PER); exact prefix sums
             double loc[SMP_PER];
@@ -1377,10 +1382,7 @@ __global__ __launch_bounds__(256) void k_sample(SampleArgs a) {
         __syncthreads();
         token = pick_sh;
     }
-    if (tid == 0) {
-        int32_t* slot = seq + (size_t)q * a.seq_len + offset;
-        if (*slot == -1) *slot = token;
-    }
+    if (tid == 0 && slot_v == -1) seq[(size_t)q * a.seq_len + offset] = token;
 }
 
 // ------------------------------------------------------------------------------------
@@ -2085,20 +2087,36 @@ __global__ __launch_bounds__(256) void k_prep(GemvArgs a) {
     x.in = in;
     x.bm_col = -1;
     x.f = (float*)lds;
+    // this wave's row of A, read before the LayerNorm so it arrives during it (rows up to
+    // 2048 wide: at most KA 8-element units per lane; wider rows read the rest afterwards)
+    constexpr int KA = 4;
+    const int k = ((int)blockIdx.y - first) * 4 + wave;
+    const float* A = (const float*)a.w.q + (size_t)(k < a.w.out ? k : a.w.out - 1) * in;
+    float4 wa[KA][2];
+#pragma unroll
+    for (int i = 0; i < KA; ++i) {
+        const int u = lane + 64 * i, uc = u < in / 8 ? u : in / 8 - 1;
+        wa[i][0] = *(const float4*)(A + 8 * uc);
+        wa[i][1] = *(const float4*)(A + 8 * uc + 4);
+    }
     prologue<T_F32, KG, LN>(a, x, red, 0, tid, lane, xr, wr, br);
     lds_barrier();
-    const int k = ((int)blockIdx.y - first) * 4 + wave;
     if (k >= a.w.out) return;
-    const float* A = (const float*)a.w.q + (size_t)k * in;
-    float p = 0.0f;
-    for (int u = lane; u < in / 8; u += 64) {
-        const float4 w0 = *(const float4*)(A + 8 * u), w1 = *(const float4*)(A + 8 * u + 4);
+    // units u = lane, lane + 64, ... in order: the prefetched ones, then any beyond
+    const auto unit = [&](float p, const float4& w0, const float4& w1, int u) {
         const float4 x0 = *(const float4*)(x.f + 8 * u), x1 = *(const float4*)(x.f + 8 * u + 4);
         p = __builtin_fmaf(w0.x, x0.x, p); p = __builtin_fmaf(w0.y, x0.y, p);
         p = __builtin_fmaf(w0.z, x0.z, p); p = __builtin_fmaf(w0.w, x0.w, p);
         p = __builtin_fmaf(w1.x, x1.x, p); p = __builtin_fmaf(w1.y, x1.y, p);
         p = __builtin_fmaf(w1.z, x1.z, p); p = __builtin_fmaf(w1.w, x1.w, p);
-    }
+        return p;
+    };
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KA; ++i)
+        if (lane + 64 * i < in / 8) p = unit(p, wa[i][0], wa[i][1], lane + 64 * i);
+    for (int u = lane + 64 * KA; u < in / 8; u += 64)
+        p = unit(p, *(const float4*)(A + 8 * u), *(const float4*)(A + 8 * u + 4), u);
     p = fold64(p);
     if (lane == 0) a.y[(size_t)col * a.y_stride + k] = p;
 }
