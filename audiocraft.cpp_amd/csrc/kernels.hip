@@ -1572,6 +1572,17 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     __shared__ int posl[16];
     int posr = 0;
     if (EPI == EPI_QKV && !WIDE) posr = a.pos[(a.col0 + (tid < ncol ? (tid & 15) : ncol - 1)) >> a.cshift];
+    // the residual epilogue's x values of the outputs this thread finishes (decode groups)
+    constexpr int RES_PER = (ROWS * 16 + NT - 1) / NT;
+    float yres[RES_PER];
+    if constexpr (EPI == EPI_RESID && !WIDE) {
+#pragma unroll
+        for (int k = 0; k < RES_PER; ++k) {
+            const int idx = tid + NT * k, n = idx / ROWS, r = idx % ROWS;
+            const int nc = idx < ROWS * 16 && n < ncol ? n : ncol - 1, row = row0 + r < a.w.out ? row0 + r : a.w.out - 1;
+            yres[k] = a.y[(size_t)nc * a.y_stride + row];
+        }
+    }
     // keep every load above in flight together: the scheduler would otherwise sink each next
     // to its first use and pay the memory latency once per leaf
     __builtin_amdgcn_sched_barrier(0);
@@ -1580,7 +1591,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     // a per-lane load of the chosen field.)
     float* const kcache = a.k;
     float* const vcache = a.v;
-    const auto finish = [&](int n, int r, float y) {
+    const auto finish = [&](int n, int r, float y, float yr) {
         const int row = row0 + r;
         const bool live = n < ncol;
         if (a.ad_ax && live)    // the staged A x holds column n's group (n < 16 when not WIDE)
@@ -1607,7 +1618,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
             if (live && a.dst_f) a.dst_f[(size_t)n * d.stride + row] = ge;
         } else if (live && (EPI == EPI_QKV || !a.gate || a.gate[a.col0 + n])) {
             if (EPI == EPI_STORE) a.y[(size_t)n * a.y_stride + row] = y;
-            else if (EPI == EPI_RESID) a.y[(size_t)n * a.y_stride + row] = a.y[(size_t)n * a.y_stride + row] + y;
+            else if (EPI == EPI_RESID) a.y[(size_t)n * a.y_stride + row] = (WIDE ? a.y[(size_t)n * a.y_stride + row] : yr) + y;
             else {
                 const int sec = row / a.dim, wi = row - sec * a.dim, head = wi >> 6, dm = wi & 63;
                 if (sec == 0) a.y[(size_t)n * a.dim + wi] = y;
@@ -1681,8 +1692,9 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
         if (EPI == EPI_QKV && tid < 16) posl[tid] = posr;
     }
     __syncthreads();
-    for (int idx0 = 0; idx0 < ROWS * 16; idx0 += NT) {
-        const int idx = idx0 + tid;
+#pragma unroll
+    for (int k = 0; k < RES_PER; ++k) {
+        const int idx0 = NT * k, idx = idx0 + tid;
         if (idx0 + (tid & ~63) >= ROWS * 16) break;    // whole waves past the tile
         const int n = idx / ROWS, r = idx % ROWS;
         float v[KW];
@@ -1693,7 +1705,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
 #pragma unroll
             for (int q = 0; q < off; ++q) v[q] = v[q] + v[q + off];
         if constexpr (WIDE) yg[cg][r][n] = v[0];
-        else finish(n, r, v[0]);
+        else finish(n, r, v[0], (EPI == EPI_RESID) ? yres[k] : 0.0f);
     }
     if constexpr (!WIDE) break;
     if (++cg >= groups) break;
@@ -1721,7 +1733,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
                 const int idx = idx0 + tid;
                 if (idx0 + (tid & ~63) >= groups * ROWS * 16) break;    // whole waves past the last group
                 const int n = idx / ROWS, r = idx % ROWS;
-                finish(n, r, yg[n >> 4][r][n & 15]);
+                finish(n, r, yg[n >> 4][r][n & 15], 0.0f);
             }
         } else {
             for (int g2 = 0; g2 < groups; ++g2) {
@@ -1738,7 +1750,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
                     const int idx = idx0 + tid;
                     if (idx0 + (tid & ~63) >= ROWS * 16) break;    // whole waves past the group
                     const int nl = idx / ROWS, r = idx % ROWS;
-                    finish(g2 * 16 + nl, r, yg[g2][r][nl]);
+                    finish(g2 * 16 + nl, r, yg[g2][r][nl], 0.0f);
                 }
                 __syncthreads();   // the next group rewrites the staged operands
             }
