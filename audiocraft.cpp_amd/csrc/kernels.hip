@@ -325,6 +325,25 @@ __device__ __forceinline__ float grp8_bcast(float v, int lane) {
     s = take_dn<4>(v); v = (lane & 4) ? s : v;
     return v;
 }
+// Loads of data read once per step and too large to stay cached (the K / V rows and the
+// weights: GBs per step): non-temporal, so they do not evict what the step reads again
+// (activations, positions, attention partials). Measured: c5 +7 %, c4 +3 % frames/s.
+typedef float nt_f4 __attribute__((ext_vector_type(4)));
+typedef int nt_i4 __attribute__((ext_vector_type(4)));
+typedef unsigned nt_u2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ int4 ld_stream_i4(const void* p) {
+    const nt_i4 v = __builtin_nontemporal_load((const nt_i4*)p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld_stream_u2(const void* p) {
+    const nt_u2 v = __builtin_nontemporal_load((const nt_u2*)p);
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ float4 ld_stream(const float4* p) {
+    const nt_f4 v = __builtin_nontemporal_load((const nt_f4*)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // Workgroup barrier for LDS traffic only: global loads in flight are not waited for.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
@@ -366,22 +385,22 @@ template <> struct WUnit<T_Q8_0> {
     uint16_t d;
     __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
         const int8_t* p = (const int8_t*)m.q + (size_t)r * m.in + u * 32;
-        a = *(const int4*)p; b = *(const int4*)(p + 16);
-        d = m.d[(size_t)r * (m.in / 32) + u];
+        a = ld_stream_i4(p); b = ld_stream_i4(p + 16);
+        d = __builtin_nontemporal_load(m.d + (size_t)r * (m.in / 32) + u);
     }
 };
 template <> struct WUnit<T_Q4_0> {
     int4 a;
     uint16_t d;
     __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
-        a = *(const int4*)((const uint8_t*)m.q + (size_t)r * (m.in / 2) + u * 16);
-        d = m.d[(size_t)r * (m.in / 32) + u];
+        a = ld_stream_i4((const uint8_t*)m.q + (size_t)r * (m.in / 2) + u * 16);
+        d = __builtin_nontemporal_load(m.d + (size_t)r * (m.in / 32) + u);
     }
 };
 template <> struct WUnit<T_F16> {
     int4 a;
     __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
-        a = *(const int4*)((const uint16_t*)m.q + (size_t)r * m.in + u * 8);
+        a = ld_stream_i4((const uint16_t*)m.q + (size_t)r * m.in + u * 8);
     }
 };
 template <> struct WUnit<T_F32> {
@@ -877,11 +896,11 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     const float4 q = ((const float4*)(a.q + (size_t)n * a.dim + h * 64))[t];
     float4 kv[4];
 #pragma unroll
-    for (int it = 0; it < 4; ++it) kv[it] = ((const float4*)(K + (size_t)(it * 16 + wave * 4 + g) * 64))[t];
+    for (int it = 0; it < 4; ++it) kv[it] = ld_stream((const float4*)(K + (size_t)(it * 16 + wave * 4 + g) * 64) + t);
     const int pv = tid >> 4, dq = tid & 15;
     float4 vv[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) vv[m] = ((const float4*)(V + (size_t)(pv + 16 * m) * 64))[dq];
+    for (int m = 0; m < 4; ++m) vv[m] = ld_stream((const float4*)(V + (size_t)(pv + 16 * m) * 64) + dq);
     const int u = a.pos[n >> a.cshift] + 1;
     if (j0 >= u) {
         if (a.stamp && threadIdx.x == 0) atomicMin(stamp_sub(a.stamp), t0);
@@ -1472,12 +1491,12 @@ __host__ __device__ constexpr int ilog2() { return N <= 1 ? 0 : 1 + ilog2<N / 2>
 template <int WT> struct MfW;
 template <> struct MfW<T_Q8_0> {
     using T = uint2;
-    static __device__ __forceinline__ T load(const int8_t* qm, size_t i) { return ((const uint2*)qm)[i]; }
+    static __device__ __forceinline__ T load(const int8_t* qm, size_t i) { return ld_stream_u2((const uint2*)qm + i); }
     static __device__ __forceinline__ long op(T w) { return (long)(((unsigned long long)w.y << 32) | w.x); }
 };
 template <> struct MfW<T_Q4_0> {
     using T = uint32_t;
-    static __device__ __forceinline__ T load(const int8_t* qm, size_t i) { return ((const uint32_t*)qm)[i]; }
+    static __device__ __forceinline__ T load(const int8_t* qm, size_t i) { return __builtin_nontemporal_load((const uint32_t*)qm + i); }
     static __device__ __forceinline__ long op(T w) {
         const uint32_t lo = ((w & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
         const uint32_t hi = (((w >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
@@ -1547,7 +1566,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
             xd[j][s] = x.d[(size_t)b * 16 + c16];
 #pragma unroll
             for (int t = 0; t < TILES; ++t)
-                dw[t][j][s] = *(const uint2*)(a.w.dt + ((size_t)(row0 / 16 + t) * NB + b) * 16 + 4 * g);
+                dw[t][j][s] = ld_stream_u2(a.w.dt + ((size_t)(row0 / 16 + t) * NB + b) * 16 + 4 * g);
         }
     }
     // adapter operands behind the weights (used only in the epilogue)
