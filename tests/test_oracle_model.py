@@ -195,3 +195,25 @@ def test_dora_rows_against_float64():
         merged.replace(a["target"], 0, wd.astype(np.float32))
     want = brute_forward(merged, ids, None, 1, False)
     assert np.abs(got - want).max() <= 5e-5 * np.abs(want).max()
+
+
+def test_timing_mode_runs_the_decode_steps_without_the_prefill():
+    """The oracle's timing mode (the CPU baseline's sample of late decode steps) marks the
+    prompt's positions as held by the cache instead of computing them: the decode steps then
+    run at the same key counts, the prefill takes no time, and the mode switches back off."""
+    m = synth.SyntheticModel("tiny", 8, seed=3)
+    rm = R.RefModel(m.config, m.tensors)
+    t5 = synth.synth_memory(1, 5)
+    P, T = 40, 60
+    prompt = synth.synth_codes(2, m.config.n_q, P, m.config.card)
+    R.lib().ref_set_timing_history(1)
+    try:
+        codes, _, rep, _ = rm.generate(t5, prompt, P, T, seed=1, max_forwards=6)
+    finally:
+        R.lib().ref_set_timing_history(0)
+    assert rep.forwards == 6 and rep.prefill_seconds < 1e-3
+    assert np.array_equal(codes[:, :P], prompt)          # the prompt stays in the sequence
+    # off again: the same call computes the prefill and matches a run that never used the mode
+    c1, f1, rep1, _ = rm.generate(t5, prompt, P, T, seed=1)
+    c2, f2, _, _ = R.RefModel(m.config, m.tensors).generate(t5, prompt, P, T, seed=1)
+    assert rep1.forwards > 6 and np.array_equal(c1, c2) and np.array_equal(f1, f2)
