@@ -19,6 +19,7 @@ constexpr int ATT_SPAN = 256;       // cache rows per head are allocated in whol
 constexpr int ATT_MAX_SPANS = 16;   // capacity up to 4096 positions
 constexpr int ATT_MAX_CHUNKS = ATT_MAX_SPANS * ATT_SPAN / ATT_CHUNK;
 constexpr int MAX_CARD = 2048;   // sampler's LDS rows
+constexpr int STAMP_SUB = 256;   // sub-slots of a profiled launch's timing slot
 constexpr int MF_MAX_COLS = 64;  // matrix-core GEMV columns per launch (16-column groups; 16 with an adapter)
 
 // A weight matrix in device layout: `out` rows of `in`. Q8_0: int8 q[out][in] + fp16
@@ -90,7 +91,7 @@ struct GemvArgs {
     // optional per-column gate (STORE / RESID): columns whose gate is 0 keep their destination
     const int* gate;
     int col0;             // the launch's first column in the caller's numbering (pos, gate)
-    unsigned long long* stamp;   // optional [64][2]: per-sub-slot earliest start, latest end (GPU wall clock)
+    unsigned long long* stamp;   // optional [STAMP_SUB][2]: per-sub-slot earliest start, latest end (GPU wall clock)
 };
 
 struct AttnArgs {
@@ -107,7 +108,7 @@ struct AttnArgs {
     int kv_cols;          // 0, or the cache column count when columns share caches (column n -> n % kv_cols)
     ActBuf out;           // the out-projection's activation
     float* out_f;         // optional f32 copy [col][dim] (an adapted out-projection's A x reads it)
-    unsigned long long* stamp;   // optional [64][2]: the chunk kernel's earliest starts, the combine's latest ends
+    unsigned long long* stamp;   // optional [STAMP_SUB][2]: the chunk kernel's earliest starts, the combine's latest ends
 };
 
 // One block per (head, request r): q + r*dim, k / v + r*heads*n_ctx*64, output column r.
@@ -194,7 +195,7 @@ void launch_fill_i32(int* p, int n, int v, hipStream_t s);
 // Opens request r of a slotted batch: position 0, live, its parameters and conditioning length.
 void launch_slot_open(int* pos, int* live, ReqParams* par, int* nc, int r, const ReqParams& p, int n_ctx,
                       hipStream_t s);
-// fills n launch-timing slots (64 sub-slots each) with {UINT64_MAX, 0}
+// fills n launch-timing slots (STAMP_SUB sub-slots each) with {UINT64_MAX, 0}
 // A x for an adapter (w = A as an f32 matrix [rank][in]; pro LN or F32 with x / x_stride /
 // ln_*; y = [col][y_stride]), the column built as the adapted projection builds it
 void launch_adapter_ax(const GemvArgs& a, hipStream_t s);

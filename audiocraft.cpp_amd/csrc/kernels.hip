@@ -347,26 +347,31 @@ __device__ __forceinline__ float4 ld_stream(const float4* p) {
 // Workgroup barrier for LDS traffic only: global loads in flight are not waited for.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// Launch timing (profiled launches only): a launch's slot holds 64 sub-slots of {earliest
-// start, latest end} on the GPU's constant-rate wall clock; block b publishes into sub-slot
-// b mod 64 once its waves are done (spreading the atomics keeps them off the kernel's own
-// memory traffic). The host takes the min / max over the sub-slots: the span a kernel tracer
-// reports as the launch's duration.
-constexpr int STAMP_SUB = 64;
+// Launch timing (profiled launches only): a launch's slot holds STAMP_SUB sub-slots of
+// {earliest start, latest end} on the GPU's constant-rate wall clock. Block b publishes its end
+// into sub-slot b mod STAMP_SUB once its waves are done, and the first STAMP_SUB blocks (the
+// first dispatched, so the earliest start is among them) their start: at most a few atomics
+// per address, so the stamps do not serialize behind each other (64 sub-slots with every block
+// stamping added several us to a launch of 9000 blocks). The host takes the min / max over the
+// sub-slots: the span a kernel tracer reports as the launch's duration.
 __device__ __forceinline__ unsigned long long stamp_begin(const unsigned long long* p) {
     return p ? (unsigned long long)wall_clock64() : 0ull;
 }
+__device__ __forceinline__ unsigned stamp_block() {
+    return blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+}
 __device__ __forceinline__ unsigned long long* stamp_sub(unsigned long long* p) {
-    const unsigned b = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    return p + 2 * (b % STAMP_SUB);
+    return p + 2 * (stamp_block() % STAMP_SUB);
+}
+__device__ __forceinline__ void stamp_start(unsigned long long* p, unsigned long long t0) {
+    if (stamp_block() < (unsigned)STAMP_SUB) atomicMin(stamp_sub(p), t0);
 }
 __device__ __forceinline__ void stamp_end(unsigned long long* p, unsigned long long t0) {
     if (!p) return;
     __syncthreads();
     if (threadIdx.x == 0) {
-        unsigned long long* q = stamp_sub(p);
-        atomicMin(q, t0);
-        atomicMax(q + 1, (unsigned long long)wall_clock64());
+        stamp_start(p, t0);
+        atomicMax(stamp_sub(p) + 1, (unsigned long long)wall_clock64());
     }
 }
 
@@ -903,7 +908,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     for (int m = 0; m < 4; ++m) vv[m] = ld_stream((const float4*)(V + (size_t)(pv + 16 * m) * 64) + dq);
     const int u = a.pos[n >> a.cshift] + 1;
     if (j0 >= u) {
-        if (a.stamp && threadIdx.x == 0) atomicMin(stamp_sub(a.stamp), t0);
+        if (a.stamp && threadIdx.x == 0) stamp_start(a.stamp, t0);
         return;
     }
     const int uc = u - j0 < ATT_CHUNK ? u - j0 : ATT_CHUNK;
@@ -953,7 +958,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
             a.csum[head * a.max_chunks + c] = sum;
         }
     }
-    if (a.stamp && threadIdx.x == 0) atomicMin(stamp_sub(a.stamp), t0);
+    if (a.stamp && threadIdx.x == 0) stamp_start(a.stamp, t0);
 }
 
 // The chunks of one (head, column) combined: lane c holds chunk c; M = max m_c, w_c =

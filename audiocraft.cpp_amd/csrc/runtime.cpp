@@ -119,7 +119,7 @@ struct mgx_stream {
     // Launch timing: when `prof_on`, every GEMV and attention launch gets a slot in `stamps`
     // (device [slot][2]: earliest block start, latest wave end on the GPU wall clock).
     struct Mark { int slot, kind, tag; double bytes; };
-    static constexpr int STAMP_SLOTS = 16384;   // launches; 64 sub-slots of 16 B each
+    static constexpr int STAMP_SLOTS = 8192;    // launches; STAMP_SUB sub-slots of 16 B each
     bool prof_on = false;
     int prof_pos = 0;                        // host view of the position, for profiling
     int prof_tag = -1;                       // the projection (MGX_PROF_*) the next launches belong to
@@ -145,7 +145,7 @@ struct mgx_stream {
     unsigned long long* stamp_slot(int kind, double bytes) {
         if (!prof_on || !stamps || (int)marks.size() >= STAMP_SLOTS) return nullptr;
         marks.push_back({(int)marks.size(), kind, prof_tag, bytes});
-        return stamps + 2 * 64 * (size_t)marks.back().slot;
+        return stamps + 2 * mgx::STAMP_SUB * (size_t)marks.back().slot;
     }
     // one layer's K (or V) cache: every cache column's heads x rows (a prefill view steps over
     // the kv_layer columns of the stream it serves)
@@ -1120,7 +1120,7 @@ int mgx_session_profile(mgx_session* ss, int32_t every) {
         mgx_stream* s = ss->s.get();
         if (every > 0 && !s->stamps) {
             HIP_OK(hipSetDevice(ss->m->device));
-            s->stamps = s->mem.alloc<unsigned long long>(2 * 64 * (size_t)mgx_stream::STAMP_SLOTS);
+            s->stamps = s->mem.alloc<unsigned long long>(2 * mgx::STAMP_SUB * (size_t)mgx_stream::STAMP_SLOTS);
             mgx::launch_stamp_init(s->stamps, mgx_stream::STAMP_SLOTS, s->hs);
             HIP_OK(hipGetLastError());
             int khz = 0;
@@ -1139,14 +1139,14 @@ int mgx_session_profile_read(mgx_session* ss, int32_t kind, double* ms_total, do
         double ms = 0.0, by = 0.0;
         int n = 0;
         if (!s->marks.empty()) {
-            std::vector<unsigned long long> st(2 * 64 * s->marks.size());
+            std::vector<unsigned long long> st(2 * mgx::STAMP_SUB * s->marks.size());
             HIP_OK(hipMemcpy(st.data(), s->stamps, st.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost));
             for (const auto& mk : s->marks) {
                 if (mk.kind != kind && mk.tag != kind) continue;
                 unsigned long long b = ~0ull, e = 0ull;
-                for (int k = 0; k < 64; ++k) {
-                    b = std::min(b, st[2 * (64 * (size_t)mk.slot + k)]);
-                    e = std::max(e, st[2 * (64 * (size_t)mk.slot + k) + 1]);
+                for (int k = 0; k < mgx::STAMP_SUB; ++k) {
+                    b = std::min(b, st[2 * (mgx::STAMP_SUB * (size_t)mk.slot + k)]);
+                    e = std::max(e, st[2 * (mgx::STAMP_SUB * (size_t)mk.slot + k) + 1]);
                 }
                 if (e <= b) continue;   // a launch that recorded nothing
                 ms += (double)(e - b) / s->clock_khz; by += mk.bytes; ++n;
