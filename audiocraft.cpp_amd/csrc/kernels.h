@@ -91,6 +91,8 @@ struct GemvArgs {
     // optional per-column gate (STORE / RESID): columns whose gate is 0 keep their destination
     const int* gate;
     int col0;             // the launch's first column in the caller's numbering (pos, gate)
+    int stream_w;         // vector GEMV: 1 when this launch is the only one reading the weights
+                          // this step (non-temporal loads), 0 when column pairs re-read them
     unsigned long long* stamp;   // optional [STAMP_SUB][2]: per-sub-slot earliest start, latest end (GPU wall clock)
 };
 

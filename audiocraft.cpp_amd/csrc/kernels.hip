@@ -385,32 +385,39 @@ struct LdsAct {
 };
 
 template <int WT> struct WUnit;
+// NT: the launch reads these weights once (it covers every column of the step): non-temporal.
+// Launches in column pairs re-read them right after, from the caches.
 template <> struct WUnit<T_Q8_0> {
     int4 a, b;
     uint16_t d;
-    __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
+    template <bool NT> __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
         const int8_t* p = (const int8_t*)m.q + (size_t)r * m.in + u * 32;
-        a = ld_stream_i4(p); b = ld_stream_i4(p + 16);
-        d = __builtin_nontemporal_load(m.d + (size_t)r * (m.in / 32) + u);
+        const uint16_t* pd = m.d + (size_t)r * (m.in / 32) + u;
+        if constexpr (NT) { a = ld_stream_i4(p); b = ld_stream_i4(p + 16); d = __builtin_nontemporal_load(pd); }
+        else { a = *(const int4*)p; b = *(const int4*)(p + 16); d = *pd; }
     }
 };
 template <> struct WUnit<T_Q4_0> {
     int4 a;
     uint16_t d;
-    __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
-        a = ld_stream_i4((const uint8_t*)m.q + (size_t)r * (m.in / 2) + u * 16);
-        d = __builtin_nontemporal_load(m.d + (size_t)r * (m.in / 32) + u);
+    template <bool NT> __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
+        const uint8_t* p = (const uint8_t*)m.q + (size_t)r * (m.in / 2) + u * 16;
+        const uint16_t* pd = m.d + (size_t)r * (m.in / 32) + u;
+        if constexpr (NT) { a = ld_stream_i4(p); d = __builtin_nontemporal_load(pd); }
+        else { a = *(const int4*)p; d = *pd; }
     }
 };
 template <> struct WUnit<T_F16> {
     int4 a;
-    __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
-        a = ld_stream_i4((const uint16_t*)m.q + (size_t)r * m.in + u * 8);
+    template <bool NT> __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
+        const uint16_t* p = (const uint16_t*)m.q + (size_t)r * m.in + u * 8;
+        if constexpr (NT) a = ld_stream_i4(p);
+        else a = *(const int4*)p;
     }
 };
 template <> struct WUnit<T_F32> {
     float4 a, b;
-    __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
+    template <bool NT> __device__ __forceinline__ void load(const DevMat& m, int r, int u) {
         const float* p = (const float*)m.q + (size_t)r * m.in + u * 8;
         a = *(const float4*)p; b = *(const float4*)(p + 4);
     }
@@ -616,7 +623,7 @@ __device__ __forceinline__ float adapt(const GemvArgs& a, int row, int col, floa
 
 // U > 0: every lane owns exactly U units (units == G * U). U == 0: any unit count, a runtime
 // loop in passes of 8 units per lane (needs G == 8 so a pass covers each partial once).
-template <int WT, int NC, int G, int U, int PRO, int EPI, int WAVES>
+template <int WT, int NC, int G, int U, int PRO, int EPI, int WAVES, bool NTW>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
     constexpr int M = 64 / G, R = WAVES * M, NT = 64 * WAVES;
     constexpr int IN = U > 0 ? unit_elems<WT>() * G * U : 2048;   // prologue size bound
@@ -684,7 +691,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
     WUnit<WT> w[U > 0 ? U : 1];
     if constexpr (U > 0) {
 #pragma unroll
-        for (int i = 0; i < U; ++i) w[i].load(a.w, row_ld, t + G * i);
+        for (int i = 0; i < U; ++i) w[i].template load<NTW>(a.w, row_ld, t + G * i);
     }
     // 3. residual
     float yo[NC];
@@ -732,7 +739,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
 #pragma unroll
             for (int ii = 0; ii < M; ++ii) {
                 const int i = i0 + ii < upl ? i0 + ii : upl - 1;
-                wp[ii].load(a.w, row_ld, t + G * i);
+                wp[ii].template load<NTW>(a.w, row_ld, t + G * i);
             }
 #pragma unroll
             for (int ii = 0; ii < M; ++ii) {
@@ -884,6 +891,7 @@ __device__ __forceinline__ float4 fold_partials16(const float4 (&P)[4]) {
 // the 16 key-strided fmaf partials folded by the butterfly. Writes o [64], m and the sum; a
 // chunk wholly past the column's position writes nothing (the combine reads only chunks that
 // exist).
+template <bool NT>
 __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     const unsigned long long t0 = stamp_begin(a.stamp);
     const int c = blockIdx.x, h = blockIdx.y, n = blockIdx.z, j0 = c * ATT_CHUNK;
@@ -901,11 +909,17 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     const float4 q = ((const float4*)(a.q + (size_t)n * a.dim + h * 64))[t];
     float4 kv[4];
 #pragma unroll
-    for (int it = 0; it < 4; ++it) kv[it] = ld_stream((const float4*)(K + (size_t)(it * 16 + wave * 4 + g) * 64) + t);
+    for (int it = 0; it < 4; ++it) {
+        const float4* p = (const float4*)(K + (size_t)(it * 16 + wave * 4 + g) * 64) + t;
+        kv[it] = NT ? ld_stream(p) : *p;
+    }
     const int pv = tid >> 4, dq = tid & 15;
     float4 vv[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) vv[m] = ld_stream((const float4*)(V + (size_t)(pv + 16 * m) * 64) + dq);
+    for (int m = 0; m < 4; ++m) {
+        const float4* p = (const float4*)(V + (size_t)(pv + 16 * m) * 64) + dq;
+        vv[m] = NT ? ld_stream(p) : *p;
+    }
     const int u = a.pos[n >> a.cshift] + 1;
     if (j0 >= u) {
         if (a.stamp && threadIdx.x == 0) stamp_start(a.stamp, t0);
@@ -1459,10 +1473,10 @@ void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s) {
     hipLaunchKernelGGL(k_add_bias, dim3((n * ncol + 255) / 256), dim3(256), 0, s, y, b, n, ncol);
 }
 
-template <int WT, int NC, int G, int U, int PRO, int EPI, int WAVES>
+template <int WT, int NC, int G, int U, int PRO, int EPI, int WAVES, bool NTW>
 __global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
     const unsigned long long t0 = stamp_begin(a.stamp);
-    gemv_body<WT, NC, G, U, PRO, EPI, WAVES>(a);
+    gemv_body<WT, NC, G, U, PRO, EPI, WAVES, NTW>(a);
     stamp_end(a.stamp, t0);
 }
 
@@ -1785,19 +1799,19 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
 
 
 // ---- GEMV launch: kernel choice by weight type, prologue / epilogue kind and unit count
-template <int WT, int NC, int G, int U, int PRO, int EPI, int W>
+template <int WT, int NC, int G, int U, int PRO, int EPI, int W, bool NTW>
 static void gemv_go(const GemvArgs& a, hipStream_t s) {
     constexpr int R = W * (64 / G);
     const size_t lds = lds_act_bytes(WT, NC, a.w.in) + (size_t)NC * R * 4 + (PRO == PRO_ACT ? 0 : (size_t)NC * 512 * 8);
-    hipLaunchKernelGGL((k_gemv<WT, NC, G, U, PRO, EPI, W>), dim3((a.w.out + R - 1) / R), dim3(64 * W), lds, s, a);
+    hipLaunchKernelGGL((k_gemv<WT, NC, G, U, PRO, EPI, W, NTW>), dim3((a.w.out + R - 1) / R), dim3(64 * W), lds, s, a);
 }
 
 // Tries (G, U, W) = the listed shapes whose G * U matches the row's unit count; else the
 // runtime-loop kernel.
-#define GEMV_TRY(G_, U_, W_) if (units == (G_) * (U_)) return gemv_go<WT, NC, G_, U_, PRO, EPI, W_>(a, s)
+#define GEMV_TRY(G_, U_, W_) if (units == (G_) * (U_)) return gemv_go<WT, NC, G_, U_, PRO, EPI, W_, NTW>(a, s)
 
 
-template <int WT, int NC, int PRO, int EPI> static void gemv_pick(const GemvArgs& a, hipStream_t s) {
+template <int WT, int NC, int PRO, int EPI, bool NTW> static void gemv_pick(const GemvArgs& a, hipStream_t s) {
     const int units = a.w.in / unit_elems<WT>();
     if constexpr (PRO == PRO_ACT) {
         if constexpr (WT == T_Q8_0 || WT == T_Q4_0) {
@@ -1823,21 +1837,28 @@ template <int WT, int NC, int PRO, int EPI> static void gemv_pick(const GemvArgs
             GEMV_TRY(8, 2, 4 * NC);
         }
     }
-    if constexpr (PRO == PRO_ACT) gemv_go<WT, NC, 8, 0, PRO, EPI, 4>(a, s);
-    else gemv_go<WT, NC, 8, 0, PRO, EPI, 4 * NC>(a, s);
+    if constexpr (PRO == PRO_ACT) gemv_go<WT, NC, 8, 0, PRO, EPI, 4, NTW>(a, s);
+    else gemv_go<WT, NC, 8, 0, PRO, EPI, 4 * NC, NTW>(a, s);
 }
 #undef GEMV_TRY
 
-template <int WT, int NC> static void gemv_nc(const GemvArgs& a, hipStream_t s) {
-    if (a.pro == PRO_ACT) gemv_pick<WT, NC, PRO_ACT, EPI_RESID>(a, s);   // every PRO_ACT site adds the residual
-    else if (a.pro == PRO_F32) gemv_pick<WT, NC, PRO_F32, EPI_STORE>(a, s);
-    else if (a.epi == EPI_QKV) gemv_pick<WT, NC, PRO_LN, EPI_QKV>(a, s);
-    else if (a.epi == EPI_GELU_ACT) gemv_pick<WT, NC, PRO_LN, EPI_GELU_ACT>(a, s);
-    else gemv_pick<WT, NC, PRO_LN, EPI_STORE>(a, s);
+template <int WT, int NC, bool NTW> static void gemv_nc(const GemvArgs& a, hipStream_t s) {
+    if (a.pro == PRO_ACT) gemv_pick<WT, NC, PRO_ACT, EPI_RESID, NTW>(a, s);   // every PRO_ACT site adds the residual
+    else if (a.pro == PRO_F32) gemv_pick<WT, NC, PRO_F32, EPI_STORE, NTW>(a, s);
+    else if (a.epi == EPI_QKV) gemv_pick<WT, NC, PRO_LN, EPI_QKV, NTW>(a, s);
+    else if (a.epi == EPI_GELU_ACT) gemv_pick<WT, NC, PRO_LN, EPI_GELU_ACT, NTW>(a, s);
+    else gemv_pick<WT, NC, PRO_LN, EPI_STORE, NTW>(a, s);
 }
+// stream_w: the launch covers every column of the step, so its weights are read once and
+// bypass the caches; launches over column pairs of a wider step read them again right after.
 template <int WT> static void gemv_wt(const GemvArgs& a, hipStream_t s) {
-    if (a.ncol == 1) gemv_nc<WT, 1>(a, s);
-    else gemv_nc<WT, 2>(a, s);
+    if (a.stream_w) {
+        if (a.ncol == 1) gemv_nc<WT, 1, true>(a, s);
+        else gemv_nc<WT, 2, true>(a, s);
+    } else {
+        if (a.ncol == 1) gemv_nc<WT, 1, false>(a, s);
+        else gemv_nc<WT, 2, false>(a, s);
+    }
 }
 
 // Columns go in groups of two (every per-column pointer advanced by the group's offset).
@@ -1909,6 +1930,7 @@ void launch_gemv(const GemvArgs& a0, hipStream_t s) {
     for (int c0 = 0; c0 < a0.ncol; c0 += 2) {
         GemvArgs a = a0;
         a.ncol = a0.ncol - c0 < 2 ? a0.ncol - c0 : 2;
+        a.stream_w = a0.ncol <= 2 ? 1 : 0;
         if (c0) {
             a.x = a0.x ? a0.x + (size_t)c0 * a0.x_stride : nullptr;
             const auto adv = [c0](ActBuf& b) {
@@ -1949,7 +1971,10 @@ void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
         throw std::logic_error("internal: attention launch of " + std::to_string(nch) + " chunks over " +
                                std::to_string(a.ncol) + " columns (at most " + std::to_string(a.max_chunks) +
                                " chunk slots)");
-    hipLaunchKernelGGL(k_attn_chunk, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
+    // one stream per column: K and V are read once per step (non-temporal); columns sharing a
+    // cache (a prefill group's positions) re-read the same chunks, which then stay cached
+    if (a.kv_cols) hipLaunchKernelGGL(k_attn_chunk<false>, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(k_attn_chunk<true>, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
     launch_combine<1>(a, nch, s);
 }
 // Sum over the 16 lanes of a lane group of 8 values per lane: levels 8, 4 and 2 halve the
