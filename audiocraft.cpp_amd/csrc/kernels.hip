@@ -891,7 +891,6 @@ __device__ __forceinline__ float4 fold_partials16(const float4 (&P)[4]) {
 // the 16 key-strided fmaf partials folded by the butterfly. Writes o [64], m and the sum; a
 // chunk wholly past the column's position writes nothing (the combine reads only chunks that
 // exist).
-template <bool NT>
 __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     const unsigned long long t0 = stamp_begin(a.stamp);
     const int c = blockIdx.x, h = blockIdx.y, n = blockIdx.z, j0 = c * ATT_CHUNK;
@@ -911,14 +910,14 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const float4* p = (const float4*)(K + (size_t)(it * 16 + wave * 4 + g) * 64) + t;
-        kv[it] = NT ? ld_stream(p) : *p;
+        kv[it] = ld_stream(p);
     }
     const int pv = tid >> 4, dq = tid & 15;
     float4 vv[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         const float4* p = (const float4*)(V + (size_t)(pv + 16 * m) * 64) + dq;
-        vv[m] = NT ? ld_stream(p) : *p;
+        vv[m] = ld_stream(p);
     }
     const int u = a.pos[n >> a.cshift] + 1;
     if (j0 >= u) {
@@ -970,6 +969,105 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
         if (lane == 0) {
             a.cmax[head * a.max_chunks + c] = m;
             a.csum[head * a.max_chunks + c] = sum;
+        }
+    }
+    if (a.stamp && threadIdx.x == 0) stamp_start(a.stamp, t0);
+}
+
+// Butterfly over 16 values in registers: v[i] += v[i + off], off = 8, 4, 2, 1 -- the tree that
+// halving4 (the scores) and fold_partials16 (the V.e partials) apply across lanes.
+__device__ __forceinline__ float tree16(float (&v)[16]) {
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1)
+#pragma unroll
+        for (int i = 0; i < off; ++i) v[i] = v[i] + v[i + off];
+    return v[0];
+}
+
+// Prefill attention, columns sharing caches (kv_cols > 0: a prefill group's positions, column n
+// on cache n % kv_cols): one block of ATT_PF_WAVES waves per (64-key chunk, head, cache, group of
+// ATT_PF_WAVES query columns) stages the chunk's K and V in LDS once; wave w then serves query
+// column w of the group. Each column's chunk result is the same arithmetic as k_attn_chunk's,
+// term for term: lane j takes key j -- the 16 four-dim fmaf partials of q.k in a register
+// butterfly (halving4's tree), times the scale, the wave's max over the keys inside the
+// column's position, e = expf(s - m), the double sum of e by the 64-wide butterfly with key j in
+// lane j -- then lane d takes dimension d: the 16 key-strided partials (keys p, p + 16, p + 32,
+// p + 48 by fmaf in order) in fold_partials16's tree. A chunk wholly past a column's position
+// writes nothing for it.
+__global__ __launch_bounds__(64 * ATT_PF_WAVES) void k_attn_prefill(AttnArgs a) {
+    const unsigned long long t0 = stamp_begin(a.stamp);
+    constexpr int KS = 68;   // padded K row: 8 lanes' float4 reads hit distinct banks
+    constexpr int NT = 64 * ATT_PF_WAVES;
+    __shared__ __align__(16) float Ks[ATT_CHUNK * KS];
+    __shared__ __align__(16) float Vs[ATT_CHUNK * 64];
+    __shared__ __align__(16) float es[ATT_PF_WAVES][64];
+    __shared__ __align__(16) float4 qs[ATT_PF_WAVES][16];
+    const int c = blockIdx.x, h = blockIdx.y, kc = blockIdx.z % a.kv_cols, j0 = c * ATT_CHUNK;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int nq = (a.ncol - kc + a.kv_cols - 1) / a.kv_cols;   // columns kc, kc + kv_cols, ..
+    const int i = (int)(blockIdx.z / a.kv_cols) * ATT_PF_WAVES + wave;
+    const bool live = i < nq;
+    const int n = kc + a.kv_cols * (live ? i : nq - 1);
+    const size_t kvh = ((size_t)kc * a.heads + h) * a.cap * 64 + (size_t)j0 * 64;
+    // the chunk's rows lie inside the cache's whole 256-key spans; rows past a column's
+    // position only ever enter masked lanes
+    constexpr int PER = ATT_CHUNK * 16 / NT;
+    float4 kr[PER], vr[PER];
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+        kr[m] = ((const float4*)(a.k + kvh))[tid + NT * m];
+        vr[m] = ((const float4*)(a.v + kvh))[tid + NT * m];
+    }
+    const float4 q4 = ((const float4*)(a.q + (size_t)n * a.dim + h * 64))[lane & 15];
+    const int u = a.pos[n >> a.cshift] + 1;
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+        const int f = tid + NT * m, row = f >> 4, c4 = f & 15;
+        *(float4*)(Ks + row * KS + c4 * 4) = kr[m];
+        *(float4*)(Vs + row * 64 + c4 * 4) = vr[m];
+    }
+    if (lane < 16) qs[wave][lane] = q4;
+    lds_barrier();
+    if (live && j0 < u) {
+        const int uc = u - j0 < ATT_CHUNK ? u - j0 : ATT_CHUNK;
+        const float4* kq = (const float4*)(Ks + lane * KS);
+        float P[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const float4 k4 = kq[t], q = qs[wave][t];
+            float v = __builtin_fmaf(q.x, k4.x, 0.0f);
+            v = __builtin_fmaf(q.y, k4.y, v);
+            v = __builtin_fmaf(q.z, k4.z, v);
+            P[t] = __builtin_fmaf(q.w, k4.w, v);
+        }
+        const float sc = tree16(P) * a.scale;
+        const float m = xor_reduce<32>(lane < uc ? sc : -__builtin_inff(), fmax_sel);
+        const float e = lane < uc ? dexpf(sc - m) : 0.0f;
+        es[wave][lane] = e;
+        const double sum = fold64d_b((double)e);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's e row, before any lane reads it
+        float A[16];
+#pragma unroll
+        for (int p = 0; p < 16; ++p) A[p] = 0.0f;
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+#pragma unroll
+            for (int p4 = 0; p4 < 4; ++p4) {
+                const float4 e4 = ((const float4*)es[wave])[4 * mm + p4];   // keys 16 mm + 4 p4 .. + 3
+                const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int p = 4 * p4 + k, j = 16 * mm + p;
+                    if (j < uc) A[p] = __builtin_fmaf(ev[k], Vs[j * 64 + lane], A[p]);
+                }
+            }
+        }
+        const float o = tree16(A);
+        const size_t hc = ((size_t)n * a.heads + h) * a.max_chunks + c;
+        a.opart[hc * 64 + lane] = o;
+        if (lane == 0) {
+            a.cmax[hc] = m;
+            a.csum[hc] = sum;
         }
     }
     if (a.stamp && threadIdx.x == 0) stamp_start(a.stamp, t0);
@@ -1971,10 +2069,15 @@ void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
         throw std::logic_error("internal: attention launch of " + std::to_string(nch) + " chunks over " +
                                std::to_string(a.ncol) + " columns (at most " + std::to_string(a.max_chunks) +
                                " chunk slots)");
-    // one stream per column: K and V are read once per step (non-temporal); columns sharing a
-    // cache (a prefill group's positions) re-read the same chunks, which then stay cached
-    if (a.kv_cols) hipLaunchKernelGGL(k_attn_chunk<false>, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(k_attn_chunk<true>, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
+    if (a.kv_cols) {
+        // columns sharing caches (a prefill group's positions): each chunk is loaded once per cache
+        if (a.kv_cols > a.ncol) throw std::logic_error("internal: attention over more caches than columns");
+        const int nq = (a.ncol + a.kv_cols - 1) / a.kv_cols, groups = (nq + ATT_PF_WAVES - 1) / ATT_PF_WAVES;
+        hipLaunchKernelGGL(k_attn_prefill, dim3(nch, a.heads, a.kv_cols * groups), dim3(64 * ATT_PF_WAVES), 0, s, a);
+    } else {
+        // one stream per column: K and V are read once per step (non-temporal)
+        hipLaunchKernelGGL(k_attn_chunk, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
+    }
     launch_combine<1>(a, nch, s);
 }
 // Sum over the 16 lanes of a lane group of 8 values per lane: levels 8, 4 and 2 halve the
