@@ -1640,10 +1640,14 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     __shared__ float adsh[AD_MAX];
     const unsigned long long t0 = stamp_begin(a.stamp);
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
-    // WIDE (17 to 64 columns): the column groups one after another against one load of the
-    // weights, every group's epilogue after the last (an adapter's operands staged group by
-    // group); else one group, epilogue in place
-    const int row0 = blockIdx.x * ROWS, ncol = a.ncol, groups = WIDE ? (ncol + 15) >> 4 : 1;
+    // WIDE (17 to 64 columns): the block's column groups (blockIdx.y's share of the launch's)
+    // one after another against one load of the weights, every group's epilogue after the last
+    // (an adapter's operands staged group by group); else one group, epilogue in place
+    const int row0 = blockIdx.x * ROWS, ncol = a.ncol;
+    const int gpb = WIDE ? (((ncol + 15) >> 4) + gridDim.y - 1) / gridDim.y : 1;
+    const int cg0 = WIDE ? blockIdx.y * gpb : 0;
+    const int cg1 = WIDE ? (cg0 + gpb < ((ncol + 15) >> 4) ? cg0 + gpb : ((ncol + 15) >> 4)) : 1;
+    if (cg0 >= cg1) return;   // (the launcher gives every block a group)
     const ActBuf& x = a.src;
     const int8_t* Wm = a.w.qm;
     // one 16-column group of the block-major source: stride * 16 quant bytes, stride / 2 scales
@@ -1679,8 +1683,8 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
 #pragma unroll
             for (int t = 0; t < TILES; ++t)
                 wa[t][j][s] = MfW<WT>::load(Wm, ((size_t)(row0 / 16 + t) * NB + b) * 64 + lane);
-            xb[j][s] = *(const uint2*)(x.q + ((size_t)b * 64 + lane) * 8);
-            xd[j][s] = x.d[(size_t)b * 16 + c16];
+            xb[j][s] = *(const uint2*)(x.q + cg0 * gq + ((size_t)b * 64 + lane) * 8);
+            xd[j][s] = x.d[cg0 * gd + (size_t)b * 16 + c16];
 #pragma unroll
             for (int t = 0; t < TILES; ++t)
                 dw[t][j][s] = ld_stream_u2(a.w.dt + ((size_t)(row0 / 16 + t) * NB + b) * 16 + 4 * g);
@@ -1764,8 +1768,8 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
         }
     };
     // column groups one after another against the same weights (in registers)
-    for (int cg = 0;;) {
-    if (WIDE && !PREFETCH && cg > 0) {
+    for (int cg = cg0;;) {
+    if (WIDE && !PREFETCH && cg > cg0) {
         load_x(cg);
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -1811,7 +1815,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
         }
     }
     // the next group's activations, behind this group's reduction (when the registers allow)
-    if (WIDE && PREFETCH && cg + 1 < groups) load_x(cg + 1);
+    if (WIDE && PREFETCH && cg + 1 < cg1) load_x(cg + 1);
     __builtin_amdgcn_sched_barrier(0);
     // 3. the KW subtree sums -> the top of the tree, one (row, column) per thread
 #pragma unroll
@@ -1844,7 +1848,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
         else finish(n, r, v[0], (EPI == EPI_RESID) ? yres[k] : 0.0f);
     }
     if constexpr (!WIDE) break;
-    if (++cg >= groups) break;
+    if (++cg >= cg1) break;
     __syncthreads();   // the next group rewrites red
     // the empty asm makes the weights look new to the next group, so their conversions (fp16
     // scales, Q4_0 nibbles) are not hoisted out of the loop into twice the registers; at the
@@ -1865,14 +1869,14 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     if constexpr (WIDE) {
         __syncthreads();
         if (!a.ad_ax) {
-            for (int idx0 = 0; idx0 < groups * ROWS * 16; idx0 += NT) {
+            for (int idx0 = 0; idx0 < (cg1 - cg0) * ROWS * 16; idx0 += NT) {
                 const int idx = idx0 + tid;
-                if (idx0 + (tid & ~63) >= groups * ROWS * 16) break;    // whole waves past the last group
-                const int n = idx / ROWS, r = idx % ROWS;
+                if (idx0 + (tid & ~63) >= (cg1 - cg0) * ROWS * 16) break;    // whole waves past the last group
+                const int n = cg0 * 16 + idx / ROWS, r = idx % ROWS;
                 finish(n, r, yg[n >> 4][r][n & 15], 0.0f);
             }
         } else {
-            for (int g2 = 0; g2 < groups; ++g2) {
+            for (int g2 = cg0; g2 < cg1; ++g2) {
                 // the group's adapter operands: the tile's B rows, its 16 columns' A x (0 past the
                 // launch's columns), DoRA m and norm -- the layout the non-WIDE staging builds
                 const int ax0 = g2 * 16 * a.ad_rank, axn = ncol * a.ad_rank;
@@ -1981,8 +1985,14 @@ bool gemv_mf_ok(const GemvArgs& a) {
            (a.epi != EPI_GELU_ACT || a.w.in <= 2048);
 }
 template <int WT, int NB, int KW, int TILES, int EPI> static void mf_go(const GemvArgs& a, hipStream_t s) {
-    if (a.ncol > 16)
-        hipLaunchKernelGGL((k_gemv_mf<WT, NB, KW, TILES, EPI, true>), dim3(a.w.out / (16 * TILES)), dim3(64 * KW), 0, s, a);
+    if (a.ncol > 16) {
+        // the column groups in two halves over blockIdx.y (each block loads its tile's weights
+        // once per half): twice the blocks of a 96- to 384-tile launch. Measured prefill: c3
+        // 76.6 -> 70.1 ms, c4 319 -> 288 ms, c5 780 -> 706 ms; quarters 76.3, 327, 732 ms. The
+        // GELU launch (32-row tiles, 4 waves) is faster whole: 10.6 against 12.9 ms at c3.
+        const int tiles = a.w.out / (16 * TILES), split = (a.ncol > 16 && EPI != EPI_GELU_ACT) ? 2 : 1;
+        hipLaunchKernelGGL((k_gemv_mf<WT, NB, KW, TILES, EPI, true>), dim3(tiles, split), dim3(64 * KW), 0, s, a);
+    }
     else
         hipLaunchKernelGGL((k_gemv_mf<WT, NB, KW, TILES, EPI, false>), dim3(a.w.out / (16 * TILES)), dim3(64 * KW), 0, s, a);
 }
