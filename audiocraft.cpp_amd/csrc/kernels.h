@@ -128,6 +128,7 @@ struct XAttnArgs {
     float scale;
     ActBuf out;       // cross.out's activation, column r
     float* out_f;     // optional f32 copy [n_req][dim]
+    unsigned long long* stamp;   // optional [STAMP_SUB][2]: the launch's earliest block start, latest end
 };
 
 constexpr int MAX_REQ = 16;      // requests of one batched session

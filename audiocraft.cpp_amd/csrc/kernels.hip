@@ -1208,12 +1208,14 @@ __device__ __forceinline__ void xattn_head(const float* qh, const float* K, cons
 
 // cross-attention of each request's conditional stream: one block per (head, request)
 __global__ __launch_bounds__(256) void k_xattn(XAttnArgs a) {
+    const unsigned long long t0 = stamp_begin(a.stamp);
     const int h = blockIdx.x, r = blockIdx.y, H = gridDim.x;
     const int nc = a.nc ? a.nc[r] : a.n_ctx;
     const size_t kr = a.shared_kv ? 0 : (size_t)r;
     const float* bias = a.bias ? a.bias + ((size_t)h * gridDim.y + r) * a.bias_stride : nullptr;
     xattn_head(a.q + (size_t)r * a.dim + h * 64, a.k + (kr * H + h) * a.n_ctx * 64,
                    a.v + (kr * H + h) * a.n_ctx * 64, nc, a.scale, bias, a.out, a.out_f, a.dim, h, r);
+    stamp_end(a.stamp, t0);
 }
 
 // The hoisted cross K/V: projected [n_ctx][2*dim] -> K [H][rows][64], V [H][rows][64] (first n_ctx rows).
@@ -2203,7 +2205,9 @@ __device__ __forceinline__ void xattn_wave(const XAttnArgs& a, int h, int r, int
 }
 template <int NK>
 __global__ __launch_bounds__(64) void k_xattn_w(XAttnArgs a) {
+    const unsigned long long t0 = stamp_begin(a.stamp);
     xattn_wave<NK>(a, blockIdx.x, blockIdx.y, gridDim.x, gridDim.y);
+    stamp_end(a.stamp, t0);
 }
 
 void launch_xattn(const XAttnArgs& a, int heads, int n_req, hipStream_t s) {

@@ -322,6 +322,9 @@ void step(mgx_stream* s, const int32_t* ids, int ids_stride, int ids_base, int i
             xa.shared_kv = s->shared_mem ? 1 : 0;
             xa.out = s->act_c.view(L.w[P_COUT].type, bc);
             xa.out_f = L.ad[P_COUT] ? s->act_c.f : nullptr;
+            s->prof_tag = MGX_PROF_XATTN;
+            // f32 K and V of each request's memory rows
+            xa.stamp = s->stamp_slot(MGX_PROF_XATTN, 2.0 * R * c.heads * s->n_ctx * 64 * 4);
             mgx::launch_xattn(xa, c.heads, R, s->hs);
             s->prof_tag = MGX_PROF_CROSS_OUT;
             mgx::GemvArgs b = ga(L.w[P_COUT], R);

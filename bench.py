@@ -441,7 +441,7 @@ def main():
     # launch of `profile_steps` steps at the timed segment's middle keys (or right after it)
     # stamps its span on the GPU clock.
     kinds = {"gemv": 0, "attention": 1, "qkv": 2, "self.out": 3, "cross.q": 4, "cross.out": 5, "ff.0": 6,
-             "ff.2": 7, "heads": 8}
+             "ff.2": 7, "heads": 8, "cross-attention": 9}
     prof = {k: [0.0, 0.0, 0] for k in kinds}
     P = max(0, args.profile_steps)
     if P:
@@ -482,7 +482,8 @@ def main():
               "cross.out": f"cross.out GEMV ({wname}, residual)",
               "ff.0": f"ff.0 GEMV ({wname} weights, LayerNorm prologue, GELU epilogue)",
               "ff.2": f"ff.2 GEMV ({wname}, residual)", "heads": f"output heads GEMV ({wname}, out_norm)",
-              "attention": "self-attention (f32 K/V of the keys attended, every stream)"}
+              "attention": "self-attention (f32 K/V of the keys attended, every stream)",
+              "cross-attention": "cross-attention (f32 K/V of each request's memory rows)"}
     fps = R * timed_steps / timed                          # frames of every request
     gemv_rate = rate("gemv")
     keys_mean = sum((a + b) * (b - a + 1) / 2 for a, b in segments) / max(timed_steps, 1)

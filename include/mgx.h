@@ -227,16 +227,18 @@ void mgx_server_destroy(mgx_server* server);
 /* Launch timing (no reference counterpart; the reference has wall clocks only,
    pipeline.cpp:15-18): with every > 0, every `every`-th loop iteration runs outside the
    captured graph (same kernels, launched one by one) and each of its GEMV (kind 0) and
-   self-attention (kind 1) launches records its span on the GPU's constant-rate wall clock
+   self-attention (kind 1) and cross-attention (kind 9) launches records its span on the GPU's
+   constant-rate wall clock
    (earliest block start to latest wave end -- a kernel tracer's duration; for attention, the
    chunk kernel's first block start to the combine kernel's last wave end, the boundary between
    them included). profile_read sums those milliseconds, the algorithmic bytes (weights at their stored
    precision; f32 K and V of the keys attended) and the launch count, for one kind of launch:
-   MGX_PROF_GEMV every weight GEMV, MGX_PROF_ATTN the self-attention, or the GEMV of one
-   projection (its adapter's A x launch, if any, is not included). */
+   MGX_PROF_GEMV every weight GEMV, MGX_PROF_ATTN the self-attention, MGX_PROF_XATTN the
+   cross-attention, or the GEMV of one projection (its adapter's A x launch, if any, is not
+   included). */
 enum {
     MGX_PROF_GEMV = 0, MGX_PROF_ATTN = 1, MGX_PROF_QKV = 2, MGX_PROF_OUT = 3, MGX_PROF_CROSS_Q = 4,
-    MGX_PROF_CROSS_OUT = 5, MGX_PROF_FF0 = 6, MGX_PROF_FF2 = 7, MGX_PROF_HEADS = 8
+    MGX_PROF_CROSS_OUT = 5, MGX_PROF_FF0 = 6, MGX_PROF_FF2 = 7, MGX_PROF_HEADS = 8, MGX_PROF_XATTN = 9
 };
 int mgx_session_profile(mgx_session* session, int32_t every);
 int mgx_session_profile_read(mgx_session* session, int32_t kind, double* ms_total, double* bytes_total,
