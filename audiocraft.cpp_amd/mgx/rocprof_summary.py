@@ -9,7 +9,12 @@
         unit spec, of each listed kernel's last n dispatches, summed over the kernels (one
         "launch" of a unit such as the attention is one dispatch of each) -- each scaled by the
         same counter on the device-to-device copy of <copy MiB> that ran in the same process,
-        and the resulting HBM bytes per launch.
+        and the resulting HBM bytes per launch;
+    python3 -m mgx.rocprof_summary window <kernel_trace.csv> <first regex> <end regex>
+        the dispatches from the first one whose kernel matches <first regex> up to (not
+        including) the next one matching <end regex> -- e.g. a prompt's prefill, from its first
+        wide matrix-core GEMV to the first sampler launch: the window's wall time, its busy time
+        and per-kernel calls / total / average duration.
 
 Used to write the text summaries under profiles/; needs only the CSV files.
 """
@@ -87,9 +92,36 @@ def traffic(fetch_csv, write_csv, copy_mib, unit=None, last=0):
     return "\n".join(lines)
 
 
+def window(path, first, end):
+    import re
+    rows = sorted(_rows(path), key=lambda r: int(r["Start_Timestamp"]))
+    rf, re_end = re.compile(first), re.compile(end)
+    i0 = next((i for i, r in enumerate(rows) if rf.search(r["Kernel_Name"])), None)
+    if i0 is None:
+        return f"no dispatch matches {first!r}"
+    i1 = next((i for i in range(i0 + 1, len(rows)) if re_end.search(rows[i]["Kernel_Name"])), len(rows))
+    w = rows[i0:i1]
+    agg = collections.defaultdict(lambda: [0, 0.0])
+    for r in w:
+        name = r["Kernel_Name"].split("(")[0]
+        if "k_attn_combine" in name:
+            name = "k_attn_combine<*>"
+        agg[name][0] += 1
+        agg[name][1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    wall = (int(w[-1]["End_Timestamp"]) - int(w[0]["Start_Timestamp"])) / 1e6
+    busy = sum(v[1] for v in agg.values()) / 1e3
+    out = [f"window: {len(w)} dispatches, {wall:.2f} ms wall, {busy:.2f} ms busy",
+           f"{'kernel':72s} {'calls':>7s} {'total_ms':>9s} {'avg_us':>8s} {'share':>6s}"]
+    for name, (calls, us) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        out.append(f"{_short(name):72s} {calls:7d} {us / 1e3:9.2f} {us / calls:8.2f} {us / 1e3 / busy:6.1%}")
+    return "\n".join(out)
+
+
 def main(argv):
     if len(argv) >= 2 and argv[0] == "stats":
         print(stats(argv[1]))
+    elif len(argv) >= 4 and argv[0] == "window":
+        print(window(argv[1], argv[2], argv[3]))
     elif len(argv) >= 4 and argv[0] == "traffic":
         unit = argv[4] if len(argv) >= 5 else None
         last = int(argv[5].split("=", 1)[1]) if len(argv) >= 6 else 0

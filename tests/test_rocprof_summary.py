@@ -59,3 +59,27 @@ def test_stats_sums_the_instance_families(tmp_path):
     assert gemv[3:6] == ["20", "0.100", "5.00"]
     comb = [l for l in out if l.startswith("k_attn_combine (all instances)")][0].split()
     assert comb[3:6] == ["8", "0.026", "3.25"]
+
+
+def test_window_takes_the_dispatches_between_the_markers(tmp_path):
+    p = tmp_path / "trace.csv"
+    # (kernel, start ns, end ns): a decode launch, the window (two wide GEMVs, an attention,
+    # two combines), the sampler that ends it, and a later wide GEMV outside it
+    rows = [("void mgx::k_gemv<8, 2, 16, 3, 0, 2, 8>(mgx::GemvArgs)", 0, 5000),
+            ("void mgx::k_gemv_mf<8, 48, 16, 1, 1, true>(mgx::GemvArgs)", 10000, 16000),
+            ("mgx::k_attn_prefill(mgx::AttnArgs)", 17000, 29000),
+            ("void mgx::k_attn_combine<3>(mgx::AttnArgs)", 30000, 34000),
+            ("void mgx::k_attn_combine<4>(mgx::AttnArgs)", 35000, 37000),
+            ("void mgx::k_gemv_mf<8, 48, 16, 1, 1, true>(mgx::GemvArgs)", 38000, 42000),
+            ("mgx::k_sample(mgx::SampleArgs)", 43000, 60000),
+            ("void mgx::k_gemv_mf<8, 48, 16, 1, 1, true>(mgx::GemvArgs)", 61000, 70000)]
+    # rows out of start order: the window sorts them
+    write(p, [{"Kernel_Name": n, "Start_Timestamp": s, "End_Timestamp": e} for n, s, e in reversed(rows)],
+          ["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+    out = S.window(str(p), "k_gemv_mf", "k_sample").splitlines()
+    assert out[0] == "window: 5 dispatches, 0.03 ms wall, 0.03 ms busy"
+    gemv = [l for l in out if l.startswith("void mgx::k_gemv_mf")][0].split()
+    assert gemv[-4:] == ["2", "0.01", "5.00", "35.7%"]
+    comb = [l for l in out if l.startswith("k_attn_combine<*>")][0].split()
+    assert comb[1:4] == ["2", "0.01", "3.00"]
+    assert out[2].startswith("mgx::k_attn_prefill")              # largest total first
