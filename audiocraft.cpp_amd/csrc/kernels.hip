@@ -1967,8 +1967,12 @@ template <int WT> static void gemv_wt(const GemvArgs& a, hipStream_t s) {
 
 // Columns go in groups of two (every per-column pointer advanced by the group's offset).
 // ---- matrix-core GEMV: (blocks per row, waves per 16-row tile) choices
-static int mf_kw(int nb, int tiles_out) {
+static int mf_kw(int nb, int tiles_out, bool wide) {
     if (nb >= 256) return 8;   // 8192-wide rows: 16 waves would need more than 128 registers
+    // decode batches (3-16 columns): 16 waves whatever the row count (c5's qkv: 6.8 -> 6.1 us,
+    // 4 waves at 288 row tiles before); wide launches keep 4 / 8 waves at 256 row tiles and up
+    // (16 waves there: c5's prefill 694 -> 726 ms)
+    if (!wide && nb % 16 == 0) return 16;
     const int base = nb >= 128 ? 8 : 4;
     const int kw = tiles_out >= 256 ? base : 16;
     return nb % kw == 0 ? kw : base;
@@ -2008,7 +2012,7 @@ template <int WT, int NB, int KW> static void mf_epi(const GemvArgs& a, hipStrea
 }
 template <int WT, int NB> static void mf_nb(const GemvArgs& a, hipStream_t s) {
     // mf_kw gives 4 only below 128 blocks, 8 only at 128 and up, 16 only when it divides NB and NB < 256
-    switch (mf_kw(NB, a.w.out / (a.epi == EPI_GELU_ACT ? 32 : 16))) {
+    switch (mf_kw(NB, a.w.out / (a.epi == EPI_GELU_ACT ? 32 : 16), a.ncol > 16)) {
     case 4: if constexpr (NB < 128) mf_epi<WT, NB, 4>(a, s); break;
     case 8: if constexpr (NB >= 128) mf_epi<WT, NB, 8>(a, s); break;
     default: if constexpr (NB % 16 == 0 && NB < 256) mf_epi<WT, NB, 16>(a, s); break;
