@@ -10,11 +10,12 @@
         "launch" of a unit such as the attention is one dispatch of each) -- each scaled by the
         same counter on the device-to-device copy of <copy MiB> that ran in the same process,
         and the resulting HBM bytes per launch;
-    python3 -m mgx.rocprof_summary window <kernel_trace.csv> <first regex> <end regex>
-        the dispatches from the first one whose kernel matches <first regex> up to (not
-        including) the next one matching <end regex> -- e.g. a prompt's prefill, from its first
-        wide matrix-core GEMV to the first sampler launch: the window's wall time, its busy time
-        and per-kernel calls / total / average duration.
+    python3 -m mgx.rocprof_summary window <kernel_trace.csv> <first regex> <end regex> [skip=<n>]
+        the dispatches from the first one whose kernel matches <first regex> (the (n+1)-th with
+        skip) up to (not including) the next one matching <end regex> ("$" for the trace's end)
+        -- e.g. a prompt's prefill, from its first wide matrix-core GEMV to the first sampler
+        launch, or the decode steps after the first n: the window's wall time, its busy time and
+        per-kernel calls / total / average duration.
 
 Used to write the text summaries under profiles/; needs only the CSV files.
 """
@@ -92,14 +93,19 @@ def traffic(fetch_csv, write_csv, copy_mib, unit=None, last=0):
     return "\n".join(lines)
 
 
-def window(path, first, end):
+def window(path, first, end, skip=0):
     import re
     rows = sorted(_rows(path), key=lambda r: int(r["Start_Timestamp"]))
-    rf, re_end = re.compile(first), re.compile(end)
-    i0 = next((i for i, r in enumerate(rows) if rf.search(r["Kernel_Name"])), None)
-    if i0 is None:
-        return f"no dispatch matches {first!r}"
-    i1 = next((i for i in range(i0 + 1, len(rows)) if re_end.search(rows[i]["Kernel_Name"])), len(rows))
+    rf = re.compile(first)
+    hits = [i for i, r in enumerate(rows) if rf.search(r["Kernel_Name"])]
+    if len(hits) <= skip:
+        return f"{len(hits)} dispatches match {first!r}, fewer than skip + 1 = {skip + 1}"
+    i0 = hits[skip]
+    if end == "$":
+        i1 = len(rows)
+    else:
+        re_end = re.compile(end)
+        i1 = next((i for i in range(i0 + 1, len(rows)) if re_end.search(rows[i]["Kernel_Name"])), len(rows))
     w = rows[i0:i1]
     agg = collections.defaultdict(lambda: [0, 0.0])
     for r in w:
@@ -121,7 +127,8 @@ def main(argv):
     if len(argv) >= 2 and argv[0] == "stats":
         print(stats(argv[1]))
     elif len(argv) >= 4 and argv[0] == "window":
-        print(window(argv[1], argv[2], argv[3]))
+        skip = int(argv[4].split("=", 1)[1]) if len(argv) >= 5 else 0
+        print(window(argv[1], argv[2], argv[3], skip))
     elif len(argv) >= 4 and argv[0] == "traffic":
         unit = argv[4] if len(argv) >= 5 else None
         last = int(argv[5].split("=", 1)[1]) if len(argv) >= 6 else 0

@@ -83,3 +83,17 @@ def test_window_takes_the_dispatches_between_the_markers(tmp_path):
     comb = [l for l in out if l.startswith("k_attn_combine<*>")][0].split()
     assert comb[1:4] == ["2", "0.01", "3.00"]
     assert out[2].startswith("mgx::k_attn_prefill")              # largest total first
+
+
+def test_window_skips_to_the_nth_match_and_runs_to_the_end(tmp_path):
+    p = tmp_path / "trace.csv"
+    rows = [("mgx::k_sample(mgx::SampleArgs)", 0, 1000), ("mgx::k_attn_chunk(mgx::AttnArgs)", 2000, 3000),
+            ("mgx::k_sample(mgx::SampleArgs)", 4000, 5000), ("mgx::k_attn_chunk(mgx::AttnArgs)", 6000, 9000),
+            ("mgx::k_sample(mgx::SampleArgs)", 10000, 11000)]
+    write(p, [{"Kernel_Name": n, "Start_Timestamp": s, "End_Timestamp": e} for n, s, e in rows],
+          ["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+    out = S.window(str(p), "k_sample", "$", skip=1).splitlines()
+    assert out[0].startswith("window: 3 dispatches")
+    chunk = [l for l in out if l.startswith("mgx::k_attn_chunk")][0].split()
+    assert chunk[1:4] == ["1", "0.00", "3.00"]
+    assert "fewer than" in S.window(str(p), "k_sample", "$", skip=3)
