@@ -1967,15 +1967,15 @@ template <int WT> static void gemv_wt(const GemvArgs& a, hipStream_t s) {
 
 // Columns go in groups of two (every per-column pointer advanced by the group's offset).
 // ---- matrix-core GEMV: (blocks per row, waves per 16-row tile) choices
-static int mf_kw(int nb, int tiles_out, bool wide) {
+static int mf_kw(int nb, int tiles_out, bool wide, bool gelu) {
     if (nb >= 256) return 8;   // 8192-wide rows: 16 waves would need more than 128 registers
+    if (nb % 16) return 4;     // 128-wide rows (small test models)
     // decode batches (3-16 columns): 16 waves whatever the row count (c5's qkv: 6.8 -> 6.1 us,
-    // 4 waves at 288 row tiles before); wide launches keep 4 / 8 waves at 256 row tiles and up
-    // (16 waves there: c5's prefill 694 -> 726 ms)
-    if (!wide && nb % 16 == 0) return 16;
-    const int base = nb >= 128 ? 8 : 4;
-    const int kw = tiles_out >= 256 ? base : 16;
-    return nb % kw == 0 ? kw : base;
+    // 4 waves at 288 row tiles before); the wide GELU launch too (c4 ff.0: 19.2 -> 13.0 us,
+    // 8 waves 14.8); other wide launches of 256 row tiles and up 8 (c4 qkv 17.0 -> 11.0 us,
+    // c3 qkv 9.45 -> 8.7; 16 there: 11.8 at c3, c5's prefill 694 -> 726 ms), fewer tiles 16
+    if (!wide || gelu) return 16;
+    return tiles_out >= 256 ? 8 : 16;
 }
 // widths 128 .. 6144 (8192 would need more than the 128 registers of a 1024-thread block)
 static bool mf_width(int nb) {
@@ -2011,10 +2011,10 @@ template <int WT, int NB, int KW> static void mf_epi(const GemvArgs& a, hipStrea
     }
 }
 template <int WT, int NB> static void mf_nb(const GemvArgs& a, hipStream_t s) {
-    // mf_kw gives 4 only below 128 blocks, 8 only at 128 and up, 16 only when it divides NB and NB < 256
-    switch (mf_kw(NB, a.w.out / (a.epi == EPI_GELU_ACT ? 32 : 16), a.ncol > 16)) {
-    case 4: if constexpr (NB < 128) mf_epi<WT, NB, 4>(a, s); break;
-    case 8: if constexpr (NB >= 128) mf_epi<WT, NB, 8>(a, s); break;
+    // mf_kw gives 4 only for NB not a multiple of 16, 16 only when it divides NB and NB < 256
+    switch (mf_kw(NB, a.w.out / (a.epi == EPI_GELU_ACT ? 32 : 16), a.ncol > 16, a.epi == EPI_GELU_ACT)) {
+    case 4: if constexpr (NB % 16 != 0) mf_epi<WT, NB, 4>(a, s); break;
+    case 8: if constexpr (NB % 16 == 0) mf_epi<WT, NB, 8>(a, s); break;
     default: if constexpr (NB % 16 == 0 && NB < 256) mf_epi<WT, NB, 16>(a, s); break;
     }
 }
