@@ -109,6 +109,7 @@ struct AttnArgs {
     const int* pos;       // [request] device positions: column n attends keys [0, pos[n >> cshift]]
     int cshift;
     int kv_cols;          // 0, or the cache column count when columns share caches (column n -> n % kv_cols)
+    int nch;              // set by launch_attention: the launch's chunk count
     ActBuf out;           // the out-projection's activation
     float* out_f;         // optional f32 copy [col][dim] (an adapted out-projection's A x reads it)
     unsigned long long* stamp;   // optional [STAMP_SUB][2]: the chunk kernel's earliest starts, the combine's latest ends

@@ -24,6 +24,7 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 #include <stdexcept>
+#include <type_traits>
 #include <string>
 
 #include "kernels.h"
@@ -825,6 +826,14 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
 // ------------------------------------------------------------------------------------
 // decode self-attention over keys [0, pos] (nn.h:186-191, no mask for one query)
 // ------------------------------------------------------------------------------------
+// acc + e * v per component (fmaf) where `take`, else acc unchanged: the same values as a
+// branch around the fmaf, without one (the caller's e read is unconditional and in bounds)
+__device__ __forceinline__ float4 fmaf4_if(bool take, float e, const float4& v, const float4& acc) {
+    const float4 t = make_float4(__builtin_fmaf(e, v.x, acc.x), __builtin_fmaf(e, v.y, acc.y),
+                                 __builtin_fmaf(e, v.z, acc.z), __builtin_fmaf(e, v.w, acc.w));
+    return take ? t : acc;
+}
+
 // Sum over the 16 lanes of a lane group of 16 values per lane, by recursive halving: after
 // the four levels lane t holds the sum of value t. Each value's additions follow the
 // butterfly p[l] + p[l+off], off = 8, 4, 2, 1 (the side that keeps a value adds its partner's).
@@ -945,17 +954,13 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     for (int w = 1; w < 4; ++w) m = m > red_f[w] ? m : red_f[w];
     if ((t & 3) == 0) el[jt] = jt < uc ? dexpf(sc - m) : 0.0f;
     lds_barrier();
+    // keys past the position keep the running value (a select: every e is in LDS, 0 past the
+    // position, so no lane branches around its read)
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int mm = 0; mm < 4; ++mm) {
         const int j = pv + 16 * mm;
-        if (j < uc) {
-            const float e = el[j];
-            acc.x = __builtin_fmaf(e, vv[mm].x, acc.x);
-            acc.y = __builtin_fmaf(e, vv[mm].y, acc.y);
-            acc.z = __builtin_fmaf(e, vv[mm].z, acc.z);
-            acc.w = __builtin_fmaf(e, vv[mm].w, acc.w);
-        }
+        acc = fmaf4_if(j < uc, el[j], vv[mm], acc);
     }
     vred[pv][dq] = acc;
     const double sum = wave == 0 ? fold64d_b((double)el[lane]) : 0.0;
@@ -1002,10 +1007,17 @@ __global__ __launch_bounds__(64 * ATT_PF_WAVES) void k_attn_prefill(AttnArgs a) 
     __shared__ __align__(16) float Vs[ATT_CHUNK * 64];
     __shared__ __align__(16) float es[ATT_PF_WAVES][64];
     __shared__ __align__(16) float4 qs[ATT_PF_WAVES][16];
-    const int c = blockIdx.x, h = blockIdx.y, kc = blockIdx.z % a.kv_cols, j0 = c * ATT_CHUNK;
+    // block L -> (item, query group): the groups of one item (chunk, head, cache) are blocks
+    // L, L + 8, L + 16, .. -- one XCD (blocks go to the 8 XCDs in turn), dispatched together, so
+    // the chunk comes from HBM once and from that XCD's L2 for the other groups
+    const int groups = ((a.ncol + a.kv_cols - 1) / a.kv_cols + ATT_PF_WAVES - 1) / ATT_PF_WAVES, L = (int)blockIdx.x;
+    const int item = (L / (8 * groups)) * 8 + (L & 7), grp = (L >> 3) % groups;
+    const int nch = a.nch;
+    if (item >= nch * a.heads * a.kv_cols) return;
+    const int c = item % nch, h = (item / nch) % a.heads, kc = item / (nch * a.heads), j0 = c * ATT_CHUNK;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int nq = (a.ncol - kc + a.kv_cols - 1) / a.kv_cols;   // columns kc, kc + kv_cols, ..
-    const int i = (int)(blockIdx.z / a.kv_cols) * ATT_PF_WAVES + wave;
+    const int i = grp * ATT_PF_WAVES + wave;
     const bool live = i < nq;
     const int n = kc + a.kv_cols * (live ? i : nq - 1);
     const size_t kvh = ((size_t)kc * a.heads + h) * a.cap * 64 + (size_t)j0 * 64;
@@ -1046,22 +1058,30 @@ __global__ __launch_bounds__(64 * ATT_PF_WAVES) void k_attn_prefill(AttnArgs a) 
         es[wave][lane] = e;
         const double sum = fold64d_b((double)e);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's e row, before any lane reads it
+        // keys past the position take no part: a whole chunk runs without a per-key test (a
+        // test per key made each V read its own branch and LDS round trip); a partial chunk
+        // keeps the running value by a select
         float A[16];
 #pragma unroll
         for (int p = 0; p < 16; ++p) A[p] = 0.0f;
+        const auto pv = [&](auto whole) {
 #pragma unroll
-        for (int mm = 0; mm < 4; ++mm) {
+            for (int mm = 0; mm < 4; ++mm) {
 #pragma unroll
-            for (int p4 = 0; p4 < 4; ++p4) {
-                const float4 e4 = ((const float4*)es[wave])[4 * mm + p4];   // keys 16 mm + 4 p4 .. + 3
-                const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+                for (int p4 = 0; p4 < 4; ++p4) {
+                    const float4 e4 = ((const float4*)es[wave])[4 * mm + p4];   // keys 16 mm + 4 p4 .. + 3
+                    const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const int p = 4 * p4 + k, j = 16 * mm + p;
-                    if (j < uc) A[p] = __builtin_fmaf(ev[k], Vs[j * 64 + lane], A[p]);
+                    for (int k = 0; k < 4; ++k) {
+                        const int p = 4 * p4 + k, j = 16 * mm + p;
+                        const float t = __builtin_fmaf(ev[k], Vs[j * 64 + lane], A[p]);
+                        A[p] = (decltype(whole)::value || j < uc) ? t : A[p];
+                    }
                 }
             }
-        }
+        };
+        if (uc == ATT_CHUNK) pv(std::true_type{});
+        else pv(std::false_type{});
         const float o = tree16(A);
         const size_t hc = ((size_t)n * a.heads + h) * a.max_chunks + c;
         a.opart[hc * 64 + lane] = o;
@@ -1170,13 +1190,7 @@ __device__ __forceinline__ void xattn_head(const float* qh, const float* K, cons
 #pragma unroll
         for (int mm = 0; mm < 4; ++mm) {
             const int j = g + 4 * k + 16 * mm;
-            if (j < uc) {
-                const float e = el[j0 + j];
-                acc.x = __builtin_fmaf(e, vv[4 * k + mm].x, acc.x);
-                acc.y = __builtin_fmaf(e, vv[4 * k + mm].y, acc.y);
-                acc.z = __builtin_fmaf(e, vv[4 * k + mm].z, acc.z);
-                acc.w = __builtin_fmaf(e, vv[4 * k + mm].w, acc.w);
-            }
+            acc = fmaf4_if(j < uc, el[j0 + j], vv[4 * k + mm], acc);
         }
         P[k] = acc;
     }
@@ -2089,7 +2103,11 @@ void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
         // columns sharing caches (a prefill group's positions): each chunk is loaded once per cache
         if (a.kv_cols > a.ncol) throw std::logic_error("internal: attention over more caches than columns");
         const int nq = (a.ncol + a.kv_cols - 1) / a.kv_cols, groups = (nq + ATT_PF_WAVES - 1) / ATT_PF_WAVES;
-        hipLaunchKernelGGL(k_attn_prefill, dim3(nch, a.heads, a.kv_cols * groups), dim3(64 * ATT_PF_WAVES), 0, s, a);
+        // a 1-D grid: whole rows of 8 items (chunk, head, cache) times the query groups
+        AttnArgs b = a;
+        b.nch = nch;
+        const int items = nch * a.heads * a.kv_cols;
+        hipLaunchKernelGGL(k_attn_prefill, dim3((items + 7) / 8 * 8 * groups), dim3(64 * ATT_PF_WAVES), 0, s, b);
     } else {
         // one stream per column: K and V are read once per step (non-temporal)
         hipLaunchKernelGGL(k_attn_chunk, dim3(nch, a.heads, a.ncol), dim3(256), 0, s, a);
@@ -2190,13 +2208,7 @@ __device__ __forceinline__ void xattn_wave(const XAttnArgs& a, int h, int r, int
 #pragma unroll
         for (int mm = 0; mm < NMM; ++mm) {
             const int j = g + 4 * k + 16 * mm;
-            if (j < nc) {
-                const float e = el[j];
-                acc.x = __builtin_fmaf(e, vv[NMM * k + mm].x, acc.x);
-                acc.y = __builtin_fmaf(e, vv[NMM * k + mm].y, acc.y);
-                acc.z = __builtin_fmaf(e, vv[NMM * k + mm].z, acc.z);
-                acc.w = __builtin_fmaf(e, vv[NMM * k + mm].w, acc.w);
-            }
+            acc = fmaf4_if(j < nc, el[j], vv[NMM * k + mm], acc);
         }
         P[k] = acc;
     }
