@@ -2009,7 +2009,7 @@ template <int WT, int NB, int KW, int TILES, int EPI> static void mf_go(const Ge
         // the column groups in two halves over blockIdx.y (each block loads its tile's weights
         // once per half): twice the blocks of a 96- to 384-tile launch. Measured prefill: c3
         // 76.6 -> 70.1 ms, c4 319 -> 288 ms, c5 780 -> 706 ms; quarters 76.3, 327, 732 ms. The
-        // GELU launch (32-row tiles, 4 waves) is faster whole: 10.6 against 12.9 ms at c3.
+        // GELU launch (32-row tiles) is faster whole: 10.6 against 12.9 ms at c3.
         const int tiles = a.w.out / (16 * TILES), split = (a.ncol > 16 && EPI != EPI_GELU_ACT) ? 2 : 1;
         hipLaunchKernelGGL((k_gemv_mf<WT, NB, KW, TILES, EPI, true>), dim3(tiles, split), dim3(64 * KW), 0, s, a);
     }
@@ -2100,7 +2100,8 @@ void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
                                std::to_string(a.ncol) + " columns (at most " + std::to_string(a.max_chunks) +
                                " chunk slots)");
     if (a.kv_cols) {
-        // columns sharing caches (a prefill group's positions): each chunk is loaded once per cache
+        // columns sharing caches (a prefill group's positions): each chunk is staged in LDS once
+        // per 8 query columns of its cache
         if (a.kv_cols > a.ncol) throw std::logic_error("internal: attention over more caches than columns");
         const int nq = (a.ncol + a.kv_cols - 1) / a.kv_cols, groups = (nq + ATT_PF_WAVES - 1) / ATT_PF_WAVES;
         // a 1-D grid: whole rows of 8 items (chunk, head, cache) times the query groups
