@@ -1967,19 +1967,33 @@ template <int WT, int NC, bool NTW> static void gemv_nc(const GemvArgs& a, hipSt
     else if (a.epi == EPI_GELU_ACT) gemv_pick<WT, NC, PRO_LN, EPI_GELU_ACT, NTW>(a, s);
     else gemv_pick<WT, NC, PRO_LN, EPI_STORE, NTW>(a, s);
 }
+template <int WT, bool NTW> static void gemv_ncol(const GemvArgs& a, hipStream_t s) {
+    if (a.ncol == 1) gemv_nc<WT, 1, NTW>(a, s);
+    else if (a.ncol == 2) gemv_nc<WT, 2, NTW>(a, s);
+    else if constexpr (WT == T_F16 || WT == T_F32) gemv_nc<WT, 4, NTW>(a, s);
+    else throw std::logic_error("internal: a quantized vector GEMV of more than 2 columns");
+}
 // stream_w: the launch covers every column of the step, so its weights are read once and
-// bypass the caches; launches over column pairs of a wider step read them again right after.
+// bypass the caches; launches over column groups of a wider step read them again right after.
 template <int WT> static void gemv_wt(const GemvArgs& a, hipStream_t s) {
-    if (a.stream_w) {
-        if (a.ncol == 1) gemv_nc<WT, 1, true>(a, s);
-        else gemv_nc<WT, 2, true>(a, s);
-    } else {
-        if (a.ncol == 1) gemv_nc<WT, 1, false>(a, s);
-        else gemv_nc<WT, 2, false>(a, s);
-    }
+    if (a.stream_w) gemv_ncol<WT, true>(a, s);
+    else gemv_ncol<WT, false>(a, s);
+}
+// Columns per vector-GEMV launch: 4 for F16 / F32 weights over more than 2 columns when the
+// columns fit the block's LDS (those wide steps -- prompt groups, T5's tokens -- have no
+// matrix-core path; each lane's weights then serve 4 columns, summed per column in the same
+// order), else 2. A prologue launch gives each column 4 waves, so 4 columns halve its row
+// blocks: it takes 4 only over 2048 rows and up, and the f32-source prologue never. Measured:
+// activation-source launches T5 242 -> 283 encodes/s, small F16 prefill 254 -> 226 ms; the
+// LayerNorm launches of 2048+ rows too 226 -> 204 ms; every prologue launch, T5 176.
+static int gemv_step(const GemvArgs& a) {
+    if (a.ncol <= 2 || (a.w.type != T_F16 && a.w.type != T_F32)) return 2;
+    if (a.pro == PRO_F32 || (a.pro == PRO_LN && a.w.out < 2048)) return 2;
+    // the columns, the epilogue tile (at most 128 rows a block) and the LayerNorm partials
+    const size_t lds = lds_act_bytes(a.w.type, 4, a.w.in) + 4 * 128 * 4 + (a.pro == PRO_ACT ? 0 : 4 * 512 * 8);
+    return lds <= 65536 ? 4 : 2;
 }
 
-// Columns go in groups of two (every per-column pointer advanced by the group's offset).
 // ---- matrix-core GEMV: (blocks per row, waves per 16-row tile) choices
 static int mf_kw(int nb, int tiles_out, bool wide, bool gelu) {
     if (nb >= 256) return 8;   // 8192-wide rows: 16 waves would need more than 128 registers
@@ -2049,16 +2063,19 @@ static void launch_gemv_mf(const GemvArgs& a, hipStream_t s) {
     else mf_wt<T_Q8_0>(a, s);
 }
 
+// Vector GEMVs go in groups of gemv_step columns (every per-column pointer advanced by the
+// group's offset).
 void launch_gemv(const GemvArgs& a0, hipStream_t s) {
     if (gemv_mf_ok(a0)) {
         launch_gemv_mf(a0, s);
         return;
     }
     if (a0.pro == PRO_ACT && a0.src.bm) return;   // the caller checks gemv_mf_ok before making one
-    for (int c0 = 0; c0 < a0.ncol; c0 += 2) {
+    const int step = gemv_step(a0);
+    for (int c0 = 0; c0 < a0.ncol; c0 += step) {
         GemvArgs a = a0;
-        a.ncol = a0.ncol - c0 < 2 ? a0.ncol - c0 : 2;
-        a.stream_w = a0.ncol <= 2 ? 1 : 0;
+        a.ncol = a0.ncol - c0 < step ? a0.ncol - c0 : step;
+        a.stream_w = a0.ncol <= step ? 1 : 0;
         if (c0) {
             a.x = a0.x ? a0.x + (size_t)c0 * a0.x_stride : nullptr;
             const auto adv = [c0](ActBuf& b) {
