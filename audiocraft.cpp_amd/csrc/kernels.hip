@@ -991,35 +991,33 @@ __device__ __forceinline__ float tree16(float (&v)[16]) {
 
 // Prefill attention, columns sharing caches (kv_cols > 0: a prefill group's positions, column n
 // on cache n % kv_cols): one block of ATT_PF_WAVES waves per (64-key chunk, head, cache, group of
-// ATT_PF_WAVES query columns) stages the chunk's K and V in LDS once; wave w then serves query
-// column w of the group. Each column's chunk result is the same arithmetic as k_attn_chunk's,
-// term for term: lane j takes key j -- the 16 four-dim fmaf partials of q.k in a register
-// butterfly (halving4's tree), times the scale, the wave's max over the keys inside the
-// column's position, e = expf(s - m), the double sum of e by the 64-wide butterfly with key j in
-// lane j -- then lane d takes dimension d: the 16 key-strided partials (keys p, p + 16, p + 32,
-// p + 48 by fmaf in order) in fold_partials16's tree. A chunk wholly past a column's position
-// writes nothing for it.
+// ATT_PF_COLS query columns) stages the chunk's K and V in LDS once; wave w then serves query
+// columns 2w and 2w + 1 of the group together (every K and V read feeds both). Each column's
+// chunk result is the same arithmetic as k_attn_chunk's, term for term: lane j takes key j --
+// the 16 four-dim fmaf partials of q.k in a register butterfly (halving4's tree), times the
+// scale, the wave's max over the keys inside the column's position, e = expf(s - m), the double
+// sum of e by the 64-wide butterfly with key j in lane j -- then lane d takes dimension d: the
+// 16 key-strided partials (keys p, p + 16, p + 32, p + 48 by fmaf in order) in
+// fold_partials16's tree. A chunk wholly past a column's position writes nothing for it.
 __global__ __launch_bounds__(64 * ATT_PF_WAVES) void k_attn_prefill(AttnArgs a) {
     const unsigned long long t0 = stamp_begin(a.stamp);
     constexpr int KS = 68;   // padded K row: 8 lanes' float4 reads hit distinct banks
     constexpr int NT = 64 * ATT_PF_WAVES;
     __shared__ __align__(16) float Ks[ATT_CHUNK * KS];
     __shared__ __align__(16) float Vs[ATT_CHUNK * 64];
-    __shared__ __align__(16) float es[ATT_PF_WAVES][64];
-    __shared__ __align__(16) float4 qs[ATT_PF_WAVES][16];
+    __shared__ __align__(16) float es[ATT_PF_WAVES][2][64];
+    __shared__ __align__(16) float4 qs[ATT_PF_WAVES][2][16];
     // block L -> (item, query group): the groups of one item (chunk, head, cache) are blocks
     // L, L + 8, L + 16, .. -- one XCD (blocks go to the 8 XCDs in turn), dispatched together, so
     // the chunk comes from HBM once and from that XCD's L2 for the other groups
-    const int groups = ((a.ncol + a.kv_cols - 1) / a.kv_cols + ATT_PF_WAVES - 1) / ATT_PF_WAVES, L = (int)blockIdx.x;
+    const int groups = ((a.ncol + a.kv_cols - 1) / a.kv_cols + ATT_PF_COLS - 1) / ATT_PF_COLS, L = (int)blockIdx.x;
     const int item = (L / (8 * groups)) * 8 + (L & 7), grp = (L >> 3) % groups;
     const int nch = a.nch;
     if (item >= nch * a.heads * a.kv_cols) return;
     const int c = item % nch, h = (item / nch) % a.heads, kc = item / (nch * a.heads), j0 = c * ATT_CHUNK;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int nq = (a.ncol - kc + a.kv_cols - 1) / a.kv_cols;   // columns kc, kc + kv_cols, ..
-    const int i = grp * ATT_PF_WAVES + wave;
-    const bool live = i < nq;
-    const int n = kc + a.kv_cols * (live ? i : nq - 1);
+    const int i0 = grp * ATT_PF_COLS + 2 * wave;
     const size_t kvh = ((size_t)kc * a.heads + h) * a.cap * 64 + (size_t)j0 * 64;
     // the chunk's rows lie inside the cache's whole 256-key spans; rows past a column's
     // position only ever enter masked lanes
@@ -1030,64 +1028,82 @@ __global__ __launch_bounds__(64 * ATT_PF_WAVES) void k_attn_prefill(AttnArgs a) 
         kr[m] = ((const float4*)(a.k + kvh))[tid + NT * m];
         vr[m] = ((const float4*)(a.v + kvh))[tid + NT * m];
     }
-    const float4 q4 = ((const float4*)(a.q + (size_t)n * a.dim + h * 64))[lane & 15];
-    const int u = a.pos[n >> a.cshift] + 1;
+    // the wave's two columns (one past the group's end repeats the last and is not written)
+    const int na = kc + a.kv_cols * (i0 < nq ? i0 : nq - 1), nb = kc + a.kv_cols * (i0 + 1 < nq ? i0 + 1 : nq - 1);
+    const float4 q4 = ((const float4*)(a.q + (size_t)(lane < 16 ? na : nb) * a.dim + h * 64))[lane & 15];
+    const int ua = a.pos[na >> a.cshift] + 1, ub = a.pos[nb >> a.cshift] + 1;
 #pragma unroll
     for (int m = 0; m < PER; ++m) {
         const int f = tid + NT * m, row = f >> 4, c4 = f & 15;
         *(float4*)(Ks + row * KS + c4 * 4) = kr[m];
         *(float4*)(Vs + row * 64 + c4 * 4) = vr[m];
     }
-    if (lane < 16) qs[wave][lane] = q4;
+    if (lane < 32) qs[wave][lane >> 4][lane & 15] = q4;
     lds_barrier();
-    if (live && j0 < u) {
-        const int uc = u - j0 < ATT_CHUNK ? u - j0 : ATT_CHUNK;
+    const bool la = i0 < nq && j0 < ua, lb = i0 + 1 < nq && j0 < ub;
+    if (la || lb) {
+        // keys inside each column's position (0: a column without this chunk)
+        const int uca = la ? (ua - j0 < ATT_CHUNK ? ua - j0 : ATT_CHUNK) : 0;
+        const int ucb = lb ? (ub - j0 < ATT_CHUNK ? ub - j0 : ATT_CHUNK) : 0;
         const float4* kq = (const float4*)(Ks + lane * KS);
-        float P[16];
+        float Pa[16], Pb[16];
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
-            const float4 k4 = kq[t], q = qs[wave][t];
-            float v = __builtin_fmaf(q.x, k4.x, 0.0f);
-            v = __builtin_fmaf(q.y, k4.y, v);
-            v = __builtin_fmaf(q.z, k4.z, v);
-            P[t] = __builtin_fmaf(q.w, k4.w, v);
+            const float4 k4 = kq[t], qa = qs[wave][0][t], qb = qs[wave][1][t];
+            float v = __builtin_fmaf(qa.x, k4.x, 0.0f);
+            v = __builtin_fmaf(qa.y, k4.y, v);
+            v = __builtin_fmaf(qa.z, k4.z, v);
+            Pa[t] = __builtin_fmaf(qa.w, k4.w, v);
+            float w = __builtin_fmaf(qb.x, k4.x, 0.0f);
+            w = __builtin_fmaf(qb.y, k4.y, w);
+            w = __builtin_fmaf(qb.z, k4.z, w);
+            Pb[t] = __builtin_fmaf(qb.w, k4.w, w);
         }
-        const float sc = tree16(P) * a.scale;
-        const float m = xor_reduce<32>(lane < uc ? sc : -__builtin_inff(), fmax_sel);
-        const float e = lane < uc ? dexpf(sc - m) : 0.0f;
-        es[wave][lane] = e;
-        const double sum = fold64d_b((double)e);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's e row, before any lane reads it
-        // keys past the position take no part: a whole chunk runs without a per-key test (a
-        // test per key made each V read its own branch and LDS round trip); a partial chunk
-        // keeps the running value by a select
-        float A[16];
+        const float sa = tree16(Pa) * a.scale, sb = tree16(Pb) * a.scale;
+        const float ma = xor_reduce<32>(lane < uca ? sa : -__builtin_inff(), fmax_sel);
+        const float mb = xor_reduce<32>(lane < ucb ? sb : -__builtin_inff(), fmax_sel);
+        const float ea = lane < uca ? dexpf(sa - ma) : 0.0f, eb = lane < ucb ? dexpf(sb - mb) : 0.0f;
+        es[wave][0][lane] = ea;
+        es[wave][1][lane] = eb;
+        const double suma = fold64d_b((double)ea), sumb = fold64d_b((double)eb);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's e rows, before any lane reads them
+        // keys past a position take no part: whole chunks run without a per-key test (a test
+        // per key made each V read its own branch and LDS round trip); otherwise each column
+        // keeps its running value by a select
+        float Aa[16], Ab[16];
 #pragma unroll
-        for (int p = 0; p < 16; ++p) A[p] = 0.0f;
+        for (int p = 0; p < 16; ++p) { Aa[p] = 0.0f; Ab[p] = 0.0f; }
         const auto pv = [&](auto whole) {
 #pragma unroll
             for (int mm = 0; mm < 4; ++mm) {
 #pragma unroll
                 for (int p4 = 0; p4 < 4; ++p4) {
-                    const float4 e4 = ((const float4*)es[wave])[4 * mm + p4];   // keys 16 mm + 4 p4 .. + 3
-                    const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+                    const float4 ea4 = ((const float4*)es[wave][0])[4 * mm + p4];   // keys 16 mm + 4 p4 .. + 3
+                    const float4 eb4 = ((const float4*)es[wave][1])[4 * mm + p4];
+                    const float eav[4] = {ea4.x, ea4.y, ea4.z, ea4.w}, ebv[4] = {eb4.x, eb4.y, eb4.z, eb4.w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
                         const int p = 4 * p4 + k, j = 16 * mm + p;
-                        const float t = __builtin_fmaf(ev[k], Vs[j * 64 + lane], A[p]);
-                        A[p] = (decltype(whole)::value || j < uc) ? t : A[p];
+                        const float v = Vs[j * 64 + lane];
+                        const float ta = __builtin_fmaf(eav[k], v, Aa[p]), tb = __builtin_fmaf(ebv[k], v, Ab[p]);
+                        Aa[p] = (decltype(whole)::value || j < uca) ? ta : Aa[p];
+                        Ab[p] = (decltype(whole)::value || j < ucb) ? tb : Ab[p];
                     }
                 }
             }
         };
-        if (uc == ATT_CHUNK) pv(std::true_type{});
+        if (uca == ATT_CHUNK && ucb == ATT_CHUNK) pv(std::true_type{});
         else pv(std::false_type{});
-        const float o = tree16(A);
-        const size_t hc = ((size_t)n * a.heads + h) * a.max_chunks + c;
-        a.opart[hc * 64 + lane] = o;
-        if (lane == 0) {
-            a.cmax[hc] = m;
-            a.csum[hc] = sum;
+        const float oa = tree16(Aa), ob = tree16(Ab);
+        if (la) {
+            const size_t hc = ((size_t)na * a.heads + h) * a.max_chunks + c;
+            a.opart[hc * 64 + lane] = oa;
+            if (lane == 0) { a.cmax[hc] = ma; a.csum[hc] = suma; }
+        }
+        if (lb) {
+            const size_t hc = ((size_t)nb * a.heads + h) * a.max_chunks + c;
+            a.opart[hc * 64 + lane] = ob;
+            if (lane == 0) { a.cmax[hc] = mb; a.csum[hc] = sumb; }
         }
     }
     if (a.stamp && threadIdx.x == 0) stamp_start(a.stamp, t0);
@@ -2120,7 +2136,7 @@ void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
         // columns sharing caches (a prefill group's positions): each chunk is staged in LDS once
         // per 8 query columns of its cache
         if (a.kv_cols > a.ncol) throw std::logic_error("internal: attention over more caches than columns");
-        const int nq = (a.ncol + a.kv_cols - 1) / a.kv_cols, groups = (nq + ATT_PF_WAVES - 1) / ATT_PF_WAVES;
+        const int nq = (a.ncol + a.kv_cols - 1) / a.kv_cols, groups = (nq + ATT_PF_COLS - 1) / ATT_PF_COLS;
         // a 1-D grid: whole rows of 8 items (chunk, head, cache) times the query groups
         AttnArgs b = a;
         b.nch = nch;
