@@ -35,8 +35,8 @@ def test_tiny_forward_matches_oracle(mgx, wtype):
     assert gs.used() == 12 and gs.forwards() == 5
 
 
-@pytest.mark.parametrize("shape,wtype", [("mini1024", 8), ("mini1024", 2), ("mini1024", 1), ("mini1536", 8),
-                                         ("mini2048", 2), ("mini2048", 8)])
+@pytest.mark.parametrize("shape,wtype", [("mini1024", 8), ("mini1024", 2), ("mini1024", 1), ("mini1024", 0),
+                                         ("mini1536", 8), ("mini2048", 2), ("mini2048", 8)])
 @pytest.mark.parametrize("n_seq", [1, 2, 3, 16])
 def test_width_forward_matches_oracle(mgx, shape, wtype, n_seq):
     """The specialised GEMV shapes (dims 1024 / 1536 / 2048, ff 4x) and the column groups."""
@@ -74,7 +74,7 @@ def test_many_streams_forward_matches_oracle(mgx):
         assert np.array_equal(gs.forward(ids[:, t:t + 1]), rd.forward(ids[:, t:t + 1]))
 
 
-@pytest.mark.parametrize("wtype", [8, 2, 1])
+@pytest.mark.parametrize("wtype", [8, 2, 1, 0])
 @pytest.mark.parametrize("n_seq", [1, 2, 4, 8])
 def test_grouped_prefill_matches_oracle(mgx, wtype, n_seq):
     """A prefill runs its positions 64 / n_seq at a time (each column at its own position, causal
