@@ -1665,11 +1665,16 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     constexpr int ROWS = 16 * TILES, NT = 64 * KW;
     static_assert(NB % KW == 0 && (NB < 64 || NB % 64 == 0), "unsupported width");
     static_assert(EPI != EPI_GELU_ACT || ROWS == 32, "GELU blocks quantize whole 32-row blocks");
-    __shared__ float red[KW][ROWS][17];
     __shared__ float yg[WIDE ? MF_MAX_COLS / 16 : 1][ROWS][17];   // WIDE: every column group's sums
     // adapter operands: the tile's B rows, one column group's A x (rank <= 64), DoRA m and norm
     constexpr int AD_MAX = (ROWS + 16) * 64 + 2 * ROWS, AD_PER = (AD_MAX + 64 * KW - 1) / (64 * KW);
     __shared__ float adsh[AD_MAX];
+    // the waves' subtree sums; WIDE launches alternate two buffers where LDS allows, so a group's
+    // writes need no barrier behind the previous group's reads (the barrier after each group's
+    // writes orders the reads of the buffer two groups back)
+    constexpr int RED_FLOATS = KW * ROWS * 17;
+    constexpr int NRED = WIDE && (2 * RED_FLOATS + (MF_MAX_COLS / 16) * ROWS * 17 + AD_MAX) * 4 <= 56 * 1024 ? 2 : 1;
+    __shared__ float red[NRED][KW][ROWS][17];
     const unsigned long long t0 = stamp_begin(a.stamp);
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
     // WIDE (17 to 64 columns): the block's column groups (blockIdx.y's share of the launch's)
@@ -1852,10 +1857,10 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     // 3. the KW subtree sums -> the top of the tree, one (row, column) per thread
 #pragma unroll
     for (int t = 0; t < TILES; ++t) {
-        red[w][16 * t + 4 * g + 0][c16] = lev[t][LB].x;
-        red[w][16 * t + 4 * g + 1][c16] = lev[t][LB].y;
-        red[w][16 * t + 4 * g + 2][c16] = lev[t][LB].z;
-        red[w][16 * t + 4 * g + 3][c16] = lev[t][LB].w;
+        red[cg & (NRED - 1)][w][16 * t + 4 * g + 0][c16] = lev[t][LB].x;
+        red[cg & (NRED - 1)][w][16 * t + 4 * g + 1][c16] = lev[t][LB].y;
+        red[cg & (NRED - 1)][w][16 * t + 4 * g + 2][c16] = lev[t][LB].z;
+        red[cg & (NRED - 1)][w][16 * t + 4 * g + 3][c16] = lev[t][LB].w;
     }
     if constexpr (!WIDE) {
 #pragma unroll
@@ -1871,7 +1876,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
         const int n = idx / ROWS, r = idx % ROWS;
         float v[KW];
 #pragma unroll
-        for (int q = 0; q < KW; ++q) v[q] = red[q][r][n];
+        for (int q = 0; q < KW; ++q) v[q] = red[cg & (NRED - 1)][q][r][n];
 #pragma unroll
         for (int off = KW / 2; off >= 1; off >>= 1)
 #pragma unroll
@@ -1881,7 +1886,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     }
     if constexpr (!WIDE) break;
     if (++cg >= cg1) break;
-    __syncthreads();   // the next group rewrites red
+    if constexpr (NRED == 1) __syncthreads();   // the next group rewrites red
     // the empty asm makes the weights look new to the next group, so their conversions (fp16
     // scales, Q4_0 nibbles) are not hoisted out of the loop into twice the registers; at the
     // loop's end, so the first group's products still start while its later loads are in flight
