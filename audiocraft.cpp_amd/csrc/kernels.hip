@@ -1582,15 +1582,13 @@ void launch_advance(int* pos, int* live, const ReqParams* par, int n_req, hipStr
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, pos, live, par, n_req);
 }
 __global__ __launch_bounds__(64) void k_set_positions(int* pos, int n, int p0) {
-    const int r = threadIdx.x;
-    if (r < n) pos[r] = p0 + r;
+    for (int r = threadIdx.x; r < n; r += 64) pos[r] = p0 + r;
 }
 void launch_set_positions(int* pos, int n, int p0, hipStream_t s) {
     hipLaunchKernelGGL(k_set_positions, dim3(1), dim3(64), 0, s, pos, n, p0);
 }
 __global__ __launch_bounds__(64) void k_fill_i32(int* p, int n, int v) {
-    const int r = threadIdx.x;
-    if (r < n) p[r] = v;
+    for (int r = threadIdx.x; r < n; r += 64) p[r] = v;
 }
 void launch_fill_i32(int* p, int n, int v, hipStream_t s) {
     hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(64), 0, s, p, n, v);
@@ -1665,7 +1663,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     constexpr int ROWS = 16 * TILES, NT = 64 * KW;
     static_assert(NB % KW == 0 && (NB < 64 || NB % 64 == 0), "unsupported width");
     static_assert(EPI != EPI_GELU_ACT || ROWS == 32, "GELU blocks quantize whole 32-row blocks");
-    __shared__ float yg[WIDE ? MF_MAX_COLS / 16 : 1][ROWS][17];   // WIDE: every column group's sums
+    __shared__ float yg[WIDE ? MF_WIDE_GROUPS : 1][ROWS][17];   // WIDE: the block's column groups' sums
     // adapter operands: the tile's B rows, one column group's A x (rank <= 64), DoRA m and norm
     constexpr int AD_MAX = (ROWS + 16) * 64 + 2 * ROWS, AD_PER = (AD_MAX + 64 * KW - 1) / (64 * KW);
     __shared__ float adsh[AD_MAX];
@@ -1673,7 +1671,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     // writes need no barrier behind the previous group's reads (the barrier after each group's
     // writes orders the reads of the buffer two groups back)
     constexpr int RED_FLOATS = KW * ROWS * 17;
-    constexpr int NRED = WIDE && (2 * RED_FLOATS + (MF_MAX_COLS / 16) * ROWS * 17 + AD_MAX) * 4 <= 56 * 1024 ? 2 : 1;
+    constexpr int NRED = WIDE && (2 * RED_FLOATS + MF_WIDE_GROUPS * ROWS * 17 + AD_MAX) * 4 <= 56 * 1024 ? 2 : 1;
     __shared__ float red[NRED][KW][ROWS][17];
     const unsigned long long t0 = stamp_begin(a.stamp);
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
@@ -1881,7 +1879,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
         for (int off = KW / 2; off >= 1; off >>= 1)
 #pragma unroll
             for (int q = 0; q < off; ++q) v[q] = v[q] + v[q + off];
-        if constexpr (WIDE) yg[cg][r][n] = v[0];
+        if constexpr (WIDE) yg[cg - cg0][r][n] = v[0];
         else finish(n, r, v[0], (EPI == EPI_RESID) ? yres[k] : 0.0f);
     }
     if constexpr (!WIDE) break;
@@ -1910,7 +1908,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
                 const int idx = idx0 + tid;
                 if (idx0 + (tid & ~63) >= (cg1 - cg0) * ROWS * 16) break;    // whole waves past the last group
                 const int n = cg0 * 16 + idx / ROWS, r = idx % ROWS;
-                finish(n, r, yg[n >> 4][r][n & 15], 0.0f);
+                finish(n, r, yg[(n >> 4) - cg0][r][n & 15], 0.0f);
             }
         } else {
             for (int g2 = cg0; g2 < cg1; ++g2) {
@@ -1927,7 +1925,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
                     const int idx = idx0 + tid;
                     if (idx0 + (tid & ~63) >= ROWS * 16) break;    // whole waves past the group
                     const int nl = idx / ROWS, r = idx % ROWS;
-                    finish(g2 * 16 + nl, r, yg[g2][r][nl], 0.0f);
+                    finish(g2 * 16 + nl, r, yg[g2 - cg0][r][nl], 0.0f);
                 }
                 __syncthreads();   // the next group rewrites the staged operands
             }
@@ -2041,11 +2039,15 @@ bool gemv_mf_ok(const GemvArgs& a) {
 }
 template <int WT, int NB, int KW, int TILES, int EPI> static void mf_go(const GemvArgs& a, hipStream_t s) {
     if (a.ncol > 16) {
-        // the column groups in two halves over blockIdx.y (each block loads its tile's weights
-        // once per half): twice the blocks of a 96- to 384-tile launch. Measured prefill: c3
-        // 76.6 -> 70.1 ms, c4 319 -> 288 ms, c5 780 -> 706 ms; quarters 76.3, 327, 732 ms. The
-        // GELU launch (32-row tiles) is faster whole: 10.6 against 12.9 ms at c3.
-        const int tiles = a.w.out / (16 * TILES), split = (a.ncol > 16 && EPI != EPI_GELU_ACT) ? 2 : 1;
+        // the column groups over blockIdx.y, MF_WIDE_GROUPS per block (each block loads its
+        // tile's weights once for its groups), 2 per block up to 64 columns. Measured prefill at
+        // 64-column groups: 2 per block against 4 c3 76.6 -> 70.1 ms, c4 319 -> 288 ms (1 per
+        // block 76.3, 327 ms), the GELU launch (32-row tiles) better at 4 (10.6 against 12.9 ms
+        // at c3); at 128- and 256-column groups 4 per block beat 2 (c4 189.5 -> 186.6, 165.1 ->
+        // 156.1 ms).
+        const int groups = (a.ncol + 15) / 16;
+        const int per = (EPI == EPI_GELU_ACT || groups > 4) ? MF_WIDE_GROUPS : 2;
+        const int tiles = a.w.out / (16 * TILES), split = (groups + per - 1) / per;
         hipLaunchKernelGGL((k_gemv_mf<WT, NB, KW, TILES, EPI, true>), dim3(tiles, split), dim3(64 * KW), 0, s, a);
     }
     else

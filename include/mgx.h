@@ -186,7 +186,7 @@ int32_t mgx_session_requests(const mgx_session* session);
    called mg_generate, and blocks until its result is ready. One worker thread owns `slots`
    request slots; between rounds of at most steps_per_round batch steps it admits queued
    requests into free slots (first come, first served). A request's prompt is prefilled into
-   its slot at admission (32 positions per step), then its loop runs in the batch steps; its
+   its slot at admission (256 positions per step when guided), then its loop runs in the batch steps; its
    slot frees after its own last step. Requests in
    one batch differ in anything: prompt and generation length (up to max_gen_len),
    conditioning (up to max_ctx tokens), guidance, seed and sampling parameters; each one's

@@ -71,9 +71,9 @@ def test_adapter_ranks_at_real_widths(M, shape, wtype, rank):
 @pytest.mark.parametrize("dora", [False, True])
 def test_adapter_wide_prefill_matches_oracle(M, shape, wtype, rank, dora):
     """A 40-token prefill with every projection adapted runs its first 39 positions through the
-    prefill view: one full 64-column group (32 positions x 2 streams, four 16-column groups
-    against one load of the weights, the adapter's A x staged group by group) and a ragged
-    group of 7 positions; then single steps."""
+    prefill view: 78 columns (39 positions x 2 streams), five 16-column groups in one launch --
+    the last one ragged, blocks of up to four groups against one load of the weights, the
+    adapter's A x staged group by group; then single steps."""
     print(f"adapter wide prefill {shape} wtype={wtype} rank={rank} dora={dora}", flush=True)
     c = H.model(shape, wtype, 5).config
     ads = synth.synth_adapters(c, rank=rank, targets=ALL, dora=dora, seed=rank + 1)

@@ -138,7 +138,7 @@ def test_full_length_generation_matches_fixture(M, name):
 def test_c5_batch_matches_fixture(M):
     """The batched serving workload at full size: 8 guided medium Q8_0 requests (16 columns, 48
     layers, rank-16 DoRA rows on qkv / ff.0 / ff.2), 500-frame prompts prefilled through the
-    64-column view (ragged last groups), then 1502 decode steps attending up to 2003 keys (32
+    512-column view (256 positions, then a ragged group of 243), then 1502 decode steps attending up to 2003 keys (32
     64-key chunks at 16 columns): every request's mixed logits at every step (CRC), first
     logits and codes equal the oracle's generation of that request alone."""
     import sys

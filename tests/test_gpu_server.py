@@ -155,15 +155,15 @@ def test_server_with_dora_adapters_at_medium_width(M):
 
 
 def test_server_dora_long_prompts_prefill_in_wide_groups(M):
-    """Admissions with DoRA rows and prompts past one 64-column prefill group (32 positions x 2
-    streams): each slot's prompt runs through the aimed view in a full group and a ragged one."""
+    """Admissions with DoRA rows and prompts past one prefill group (256 positions x 2 streams):
+    each slot's prompt runs through the aimed view in a full group and a ragged one."""
     print("server with DoRA, long prompts, mini1536 Q8_0, 4 slots", flush=True)
     m = H.model("mini1536", 8, 15)
     c = m.config
     gm = M.Model(c, m.tensors)
     gm.set_adapters(synth.synth_adapters(c, rank=16, targets=("self.qkv", "ff.0", "ff.2"), dora=True, seed=5))
     n_ctx = synth.SHAPES["mini1536"]["n_ctx"]
-    reqs = [request(M, c, 60, 48, 40, n_ctx), request(M, c, 61, 44, 35, n_ctx, top_k=20),
+    reqs = [request(M, c, 60, 278, 270, n_ctx), request(M, c, 61, 272, 265, n_ctx, top_k=20),
             request(M, c, 62, 20, 5, n_ctx)]
     out, progress, counters = serve(M, gm, reqs, 4)
     check_alone(M, gm, reqs, out, progress)
