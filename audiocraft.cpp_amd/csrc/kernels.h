@@ -18,8 +18,9 @@ constexpr int ATT_SPAN = 256;       // cache rows per head are allocated in whol
                                     // step's attention grid covers the 64-key chunks of its key count
 constexpr int ATT_MAX_SPANS = 16;   // capacity up to 4096 positions
 constexpr int ATT_MAX_CHUNKS = ATT_MAX_SPANS * ATT_SPAN / ATT_CHUNK;
-constexpr int ATT_PF_WAVES = 4;  // prefill attention: waves per block, two query columns each,
-constexpr int ATT_PF_COLS = 2 * ATT_PF_WAVES;   // sharing one staged chunk's K / V in LDS
+constexpr int ATT_PF_WAVES = 4;   // prefill attention: waves per block, two query columns per
+constexpr int ATT_PF_PASSES = 4;  // wave and pass, all sharing one staged chunk's K / V in LDS
+constexpr int ATT_PF_COLS = 2 * ATT_PF_WAVES * ATT_PF_PASSES;
 constexpr int MAX_CARD = 2048;   // sampler's LDS rows
 constexpr int STAMP_SUB = 256;   // sub-slots of a profiled launch's timing slot
 constexpr int MF_MAX_COLS = 512;   // matrix-core GEMV columns per launch (16-column groups): a prefill group

@@ -991,8 +991,9 @@ __device__ __forceinline__ float tree16(float (&v)[16]) {
 
 // Prefill attention, columns sharing caches (kv_cols > 0: a prefill group's positions, column n
 // on cache n % kv_cols): one block of ATT_PF_WAVES waves per (64-key chunk, head, cache, group of
-// ATT_PF_COLS query columns) stages the chunk's K and V in LDS once; wave w then serves query
-// columns 2w and 2w + 1 of the group together (every K and V read feeds both). Each column's
+// ATT_PF_COLS query columns) stages the chunk's K and V in LDS once; wave w then serves, in pass
+// p, query columns 2 (p WAVES + w) and the next of the group together (every K and V read feeds
+// both; the q rows come by scalar loads). Each column's
 // chunk result is the same arithmetic as k_attn_chunk's, term for term: lane j takes key j --
 // the 16 four-dim fmaf partials of q.k in a register butterfly (halving4's tree), times the
 // scale, the wave's max over the keys inside the column's position, e = expf(s - m), the double
@@ -1006,7 +1007,6 @@ __global__ __launch_bounds__(64 * ATT_PF_WAVES) void k_attn_prefill(AttnArgs a) 
     __shared__ __align__(16) float Ks[ATT_CHUNK * KS];
     __shared__ __align__(16) float Vs[ATT_CHUNK * 64];
     __shared__ __align__(16) float es[ATT_PF_WAVES][2][64];
-    __shared__ __align__(16) float4 qs[ATT_PF_WAVES][2][16];
     // block L -> (item, query group): the groups of one item (chunk, head, cache) are blocks
     // L, L + 8, L + 16, .. -- one XCD (blocks go to the 8 XCDs in turn), dispatched together, so
     // the chunk comes from HBM once and from that XCD's L2 for the other groups
@@ -1017,7 +1017,6 @@ __global__ __launch_bounds__(64 * ATT_PF_WAVES) void k_attn_prefill(AttnArgs a) 
     const int c = item % nch, h = (item / nch) % a.heads, kc = item / (nch * a.heads), j0 = c * ATT_CHUNK;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int nq = (a.ncol - kc + a.kv_cols - 1) / a.kv_cols;   // columns kc, kc + kv_cols, ..
-    const int i0 = grp * ATT_PF_COLS + 2 * wave;
     const size_t kvh = ((size_t)kc * a.heads + h) * a.cap * 64 + (size_t)j0 * 64;
     // the chunk's rows lie inside the cache's whole 256-key spans; rows past a column's
     // position only ever enter masked lanes
@@ -1028,37 +1027,45 @@ __global__ __launch_bounds__(64 * ATT_PF_WAVES) void k_attn_prefill(AttnArgs a) 
         kr[m] = ((const float4*)(a.k + kvh))[tid + NT * m];
         vr[m] = ((const float4*)(a.v + kvh))[tid + NT * m];
     }
-    // the wave's two columns (one past the group's end repeats the last and is not written)
-    const int na = kc + a.kv_cols * (i0 < nq ? i0 : nq - 1), nb = kc + a.kv_cols * (i0 + 1 < nq ? i0 + 1 : nq - 1);
-    const float4 q4 = ((const float4*)(a.q + (size_t)(lane < 16 ? na : nb) * a.dim + h * 64))[lane & 15];
-    const int ua = a.pos[na >> a.cshift] + 1, ub = a.pos[nb >> a.cshift] + 1;
 #pragma unroll
     for (int m = 0; m < PER; ++m) {
         const int f = tid + NT * m, row = f >> 4, c4 = f & 15;
         *(float4*)(Ks + row * KS + c4 * 4) = kr[m];
         *(float4*)(Vs + row * 64 + c4 * 4) = vr[m];
     }
-    if (lane < 32) qs[wave][lane >> 4][lane & 15] = q4;
     lds_barrier();
-    const bool la = i0 < nq && j0 < ua, lb = i0 + 1 < nq && j0 < ub;
+    // the columns' q rows are the same for every lane: scalar loads (read-only during the
+    // kernel, hence the constant address space) into SGPRs, no LDS broadcast per use
+    typedef const float __attribute__((address_space(4)))* qrow_t;
+    for (int ps = 0; ps < ATT_PF_PASSES; ++ps) {
+    // the pass's two columns (one past the group's end repeats the last and is not written)
+    const int i0 = grp * ATT_PF_COLS + 2 * (ps * ATT_PF_WAVES + wave);
+    if (i0 >= nq) break;
+    const int na = kc + a.kv_cols * i0, nb = kc + a.kv_cols * (i0 + 1 < nq ? i0 + 1 : i0);
+    const qrow_t qa_p = (qrow_t)(a.q + (size_t)na * a.dim + h * 64);
+    const qrow_t qb_p = (qrow_t)(a.q + (size_t)nb * a.dim + h * 64);
+    const int ua = a.pos[na >> a.cshift] + 1, ub = a.pos[nb >> a.cshift] + 1;
+    const bool la = j0 < ua, lb = i0 + 1 < nq && j0 < ub;
     if (la || lb) {
         // keys inside each column's position (0: a column without this chunk)
         const int uca = la ? (ua - j0 < ATT_CHUNK ? ua - j0 : ATT_CHUNK) : 0;
         const int ucb = lb ? (ub - j0 < ATT_CHUNK ? ub - j0 : ATT_CHUNK) : 0;
-        const float4* kq = (const float4*)(Ks + lane * KS);
-        float Pa[16], Pb[16];
+        // the lane's key row in registers, then each column's 16 partials in turn
+        float4 k4[16];
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            const float4 k4 = kq[t], qa = qs[wave][0][t], qb = qs[wave][1][t];
-            float v = __builtin_fmaf(qa.x, k4.x, 0.0f);
-            v = __builtin_fmaf(qa.y, k4.y, v);
-            v = __builtin_fmaf(qa.z, k4.z, v);
-            Pa[t] = __builtin_fmaf(qa.w, k4.w, v);
-            float w = __builtin_fmaf(qb.x, k4.x, 0.0f);
-            w = __builtin_fmaf(qb.y, k4.y, w);
-            w = __builtin_fmaf(qb.z, k4.z, w);
-            Pb[t] = __builtin_fmaf(qb.w, k4.w, w);
-        }
+        for (int t = 0; t < 16; ++t) k4[t] = ((const float4*)(Ks + lane * KS))[t];
+        float Pa[16], Pb[16];
+        const auto qk = [&](qrow_t qp, float (&P)[16]) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                float v = __builtin_fmaf(qp[4 * t], k4[t].x, 0.0f);
+                v = __builtin_fmaf(qp[4 * t + 1], k4[t].y, v);
+                v = __builtin_fmaf(qp[4 * t + 2], k4[t].z, v);
+                P[t] = __builtin_fmaf(qp[4 * t + 3], k4[t].w, v);
+            }
+        };
+        qk(qa_p, Pa);
+        qk(qb_p, Pb);
         const float sa = tree16(Pa) * a.scale, sb = tree16(Pb) * a.scale;
         const float ma = xor_reduce<32>(lane < uca ? sa : -__builtin_inff(), fmax_sel);
         const float mb = xor_reduce<32>(lane < ucb ? sb : -__builtin_inff(), fmax_sel);
@@ -1105,6 +1112,7 @@ __global__ __launch_bounds__(64 * ATT_PF_WAVES) void k_attn_prefill(AttnArgs a) 
             a.opart[hc * 64 + lane] = ob;
             if (lane == 0) { a.cmax[hc] = mb; a.csum[hc] = sumb; }
         }
+    }
     }
     if (a.stamp && threadIdx.x == 0) stamp_start(a.stamp, t0);
 }
@@ -1675,7 +1683,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_mf(GemvArgs a) {
     __shared__ float red[NRED][KW][ROWS][17];
     const unsigned long long t0 = stamp_begin(a.stamp);
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
-    // WIDE (17 to 64 columns): the block's column groups (blockIdx.y's share of the launch's)
+    // WIDE (17 to MF_MAX_COLS columns): the block's column groups (blockIdx.y's share of the launch's)
     // one after another against one load of the weights, every group's epilogue after the last
     // (an adapter's operands staged group by group); else one group, epilogue in place
     const int row0 = blockIdx.x * ROWS, ncol = a.ncol;
@@ -2040,7 +2048,8 @@ bool gemv_mf_ok(const GemvArgs& a) {
 template <int WT, int NB, int KW, int TILES, int EPI> static void mf_go(const GemvArgs& a, hipStream_t s) {
     if (a.ncol > 16) {
         // the column groups over blockIdx.y, MF_WIDE_GROUPS per block (each block loads its
-        // tile's weights once for its groups), 2 per block up to 64 columns. Measured prefill at
+        // tile's weights once for its groups), 2 per block up to 64 columns (a short prompt's
+        // group or an unguided view's tail). Measured prefill at
         // 64-column groups: 2 per block against 4 c3 76.6 -> 70.1 ms, c4 319 -> 288 ms (1 per
         // block 76.3, 327 ms), the GELU launch (32-row tiles) better at 4 (10.6 against 12.9 ms
         // at c3); at 128- and 256-column groups 4 per block beat 2 (c4 189.5 -> 186.6, 165.1 ->
@@ -2141,7 +2150,7 @@ void launch_attention(const AttnArgs& a, int nch, hipStream_t s) {
                                " chunk slots)");
     if (a.kv_cols) {
         // columns sharing caches (a prefill group's positions): each chunk is staged in LDS once
-        // per 8 query columns of its cache
+        // per ATT_PF_COLS query columns of its cache
         if (a.kv_cols > a.ncol) throw std::logic_error("internal: attention over more caches than columns");
         const int nq = (a.ncol + a.kv_cols - 1) / a.kv_cols, groups = (nq + ATT_PF_COLS - 1) / ATT_PF_COLS;
         // a 1-D grid: whole rows of 8 items (chunk, head, cache) times the query groups
