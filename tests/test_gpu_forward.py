@@ -79,16 +79,17 @@ def test_many_streams_forward_matches_oracle(mgx):
 def test_grouped_prefill_matches_oracle(mgx, wtype, n_seq):
     """A prefill runs its positions 512 / n_seq at a time (each column at its own position, causal
     by key count; the matrix-core GEMVs take the columns in 16-column groups, up to four per
-    block against one load of the weights): prompts of 2, 17, 70, 300 and 600 tokens -- one
-    partial group, partial 16-column groups, several groups at every stream count, 256-key span
-    boundaries inside a group -- then single steps, against the oracle's masked prefill (n_seq 3
-    and 16 keep one position at a time and are covered above)."""
+    block against one load of the weights): prompts of 2, 17, 70, 257, 300, 512 and 600 tokens --
+    one partial group, partial 16-column groups, several groups at every stream count, 256-key
+    span boundaries inside a group, whole groups only (512 at every stream count) and one
+    position past a whole guided group (257) -- then single steps, against the oracle's masked
+    prefill (n_seq 3 and 16 keep one position at a time and are covered above)."""
     from oracle import cpu_ref as R
     m = H.model("tiny", wtype, 3)
     c = m.config
     t5 = H.memory(1, 5)
     gm = mgx.Model(c, m.tensors)
-    for n_pre in (2, 17, 70, 300, 600):
+    for n_pre in (2, 17, 70, 257, 300, 512, 600):
         print(f"grouped prefill wtype={wtype} n_seq={n_seq} tokens={n_pre}", flush=True)
         ids = H.codes(n_pre, 4, n_pre + 2, c.card)
         gs = mgx.Stream(gm, n_pre + 4, n_seq, t5, True)
