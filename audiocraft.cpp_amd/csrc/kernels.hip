@@ -2027,10 +2027,11 @@ static int mf_kw(int nb, int tiles_out, bool wide, bool gelu) {
     if (nb % 16) return 4;     // 128-wide rows (small test models)
     // decode batches (3-16 columns): 16 waves whatever the row count (c5's qkv: 6.8 -> 6.1 us,
     // 4 waves at 288 row tiles before); the wide GELU launch too (c4 ff.0: 19.2 -> 13.0 us,
-    // 8 waves 14.8); other wide launches of 256 row tiles and up 8 (c4 qkv 17.0 -> 11.0 us,
-    // c3 qkv 9.45 -> 8.7; 16 there: 11.8 at c3, c5's prefill 694 -> 726 ms), fewer tiles 16
+    // 8 waves 14.8 at 64 columns; with 512-column groups 8 waves cost c4's prefill 2 ms more);
+    // other wide launches 8 (c4 qkv 17.0 -> 11.0 us, c3 qkv 9.45 -> 8.7; 16 there: 11.8 at c3,
+    // c5's prefill 694 -> 726 ms; at 512 columns 8 waves also beat 16 for fewer row tiles)
     if (!wide || gelu) return 16;
-    return tiles_out >= 256 ? 8 : 16;
+    return 8;
 }
 // widths 128 .. 6144 (8192 would need more than the 128 registers of a 1024-thread block)
 static bool mf_width(int nb) {
