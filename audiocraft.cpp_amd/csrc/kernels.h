@@ -24,7 +24,7 @@ constexpr int ATT_PF_COLS = 2 * ATT_PF_WAVES * ATT_PF_PASSES;
 constexpr int MAX_CARD = 2048;   // sampler's LDS rows
 constexpr int STAMP_SUB = 256;   // sub-slots of a profiled launch's timing slot
 constexpr int MF_MAX_COLS = 512;   // matrix-core GEMV columns per launch (16-column groups): a prefill group
-constexpr int MF_WIDE_GROUPS = 4;  // column groups one wide matrix-core block holds at most
+constexpr int MF_WIDE_GROUPS = 8;  // column groups one wide matrix-core block holds at most
 
 // A weight matrix in device layout: `out` rows of `in`. Q8_0: int8 q[out][in] + fp16
 // d[out][in/32]; Q4_0: the 16 nibble bytes of each block q[out][in/2] + d; F16 / F32: q only.

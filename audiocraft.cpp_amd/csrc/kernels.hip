@@ -2029,8 +2029,10 @@ static int mf_kw(int nb, int tiles_out, bool wide, bool gelu) {
     // 4 waves at 288 row tiles before); the wide GELU launch too (c4 ff.0: 19.2 -> 13.0 us,
     // 8 waves 14.8 at 64 columns; with 512-column groups 8 waves cost c4's prefill 2 ms more);
     // other wide launches 8 (c4 qkv 17.0 -> 11.0 us, c3 qkv 9.45 -> 8.7; 16 there: 11.8 at c3,
-    // c5's prefill 694 -> 726 ms; at 512 columns 8 waves also beat 16 for fewer row tiles)
-    if (!wide || gelu) return 16;
+    // c5's prefill 694 -> 726 ms; at 512 columns 8 waves also beat 16 for fewer row tiles) but
+    // the 6144-wide rows, whose 8-wave form needs 205 registers (c3 ff.2 58.2 us against 50.9;
+    // prefill c3 29.3 -> 28.6 ms, c5 324.7 -> 319.1 with 16)
+    if (!wide || gelu || nb == 192) return 16;
     return 8;
 }
 // widths 128 .. 6144 (8192 would need more than the 128 registers of a 1024-thread block)
@@ -2048,16 +2050,19 @@ bool gemv_mf_ok(const GemvArgs& a) {
 }
 template <int WT, int NB, int KW, int TILES, int EPI> static void mf_go(const GemvArgs& a, hipStream_t s) {
     if (a.ncol > 16) {
-        // the column groups over blockIdx.y, MF_WIDE_GROUPS per block (each block loads its
-        // tile's weights once for its groups), 2 per block up to 64 columns (a short prompt's
-        // group or an unguided view's tail). Measured prefill at
-        // 64-column groups: 2 per block against 4 c3 76.6 -> 70.1 ms, c4 319 -> 288 ms (1 per
-        // block 76.3, 327 ms), the GELU launch (32-row tiles) better at 4 (10.6 against 12.9 ms
-        // at c3); at 128- and 256-column groups 4 per block beat 2 (c4 189.5 -> 186.6, 165.1 ->
-        // 156.1 ms).
-        const int groups = (a.ncol + 15) / 16;
-        const int per = (EPI == EPI_GELU_ACT || groups > 4) ? MF_WIDE_GROUPS : 2;
-        const int tiles = a.w.out / (16 * TILES), split = (groups + per - 1) / per;
+        // the column groups over blockIdx.y, several per block (each block loads its tile's
+        // weights once for its groups): up to MF_WIDE_GROUPS from 128 row tiles up, 4 below,
+        // 2 up to 64 columns (a short prompt's group or an unguided view's tail). Measured
+        // prefill at 64-column groups: 2 per block against 4 c3 76.6 -> 70.1 ms, c4 319 -> 288 ms
+        // (1 per block 76.3, 327 ms), the GELU launch (32-row tiles) better at 4 (10.6 against
+        // 12.9 ms at c3); at 128- and 256-column groups 4 per block beat 2 (c4 189.5 -> 186.6,
+        // 165.1 -> 156.1 ms); at 512-column groups 8 beat 4 where the row tiles are 128 or more
+        // (c4 138.7 -> 132.7 ms, c3 29.9 -> 29.2, c5 328.7 -> 324.4) and lost below that (8 for
+        // every launch: c3 30.0 -> 30.4, c5 328.9 -> 337.4 -- their 96-tile launches then have
+        // 384 blocks)
+        const int groups = (a.ncol + 15) / 16, tiles = a.w.out / (16 * TILES);
+        const int per = (EPI == EPI_GELU_ACT || groups > 4) ? (tiles >= 128 ? MF_WIDE_GROUPS : 4) : 2;
+        const int split = (groups + per - 1) / per;
         hipLaunchKernelGGL((k_gemv_mf<WT, NB, KW, TILES, EPI, true>), dim3(tiles, split), dim3(64 * KW), 0, s, a);
     }
     else
