@@ -97,6 +97,8 @@ struct GemvArgs {
     int col0;             // the launch's first column in the caller's numbering (pos, gate)
     int stream_w;         // vector GEMV: 1 when this launch is the only one reading the weights
                           // this step (non-temporal loads), 0 when column pairs re-read them
+    int ygroups;          // vector GEMV: > 1 when blockIdx.y runs that many whole groups of the
+                          // launch's ncol columns, group g at column g * ncol of the arguments
     unsigned long long* stamp;   // optional [STAMP_SUB][2]: per-sub-slot earliest start, latest end (GPU wall clock)
 };
 

@@ -1609,11 +1609,45 @@ void launch_add_bias(float* y, const float* b, int n, int ncol, hipStream_t s) {
     hipLaunchKernelGGL(k_add_bias, dim3((n * ncol + 255) / 256), dim3(256), 0, s, y, b, n, ncol);
 }
 
+// The arguments of the column group starting at column c0 of a0's columns: every per-column
+// pointer advanced, the caller's numbering (col0) moved along; the QKV epilogue's caches stay
+// (it maps col0 + n to its cache row).
+__host__ __device__ __forceinline__ void gemv_advance(GemvArgs& a, const GemvArgs& a0, int c0) {
+    a.x = a0.x ? a0.x + (size_t)c0 * a0.x_stride : nullptr;
+    const auto adv = [c0](ActBuf& b, const ActBuf& b0) {
+        if (b0.q) b.q = b0.q + (size_t)c0 * b0.stride;
+        if (b0.d) b.d = b0.d + (size_t)c0 * (b0.stride / 32);
+        if (b0.h) b.h = b0.h + (size_t)c0 * b0.stride;
+        if (b0.f) b.f = b0.f + (size_t)c0 * b0.stride;
+    };
+    adv(a.src, a0.src);
+    adv(a.dst, a0.dst);
+    if (a0.dst_f) a.dst_f = a0.dst_f + (size_t)c0 * a0.dst.stride;
+    if (a0.ad_ax) a.ad_ax = a0.ad_ax + (size_t)c0 * a0.ad_rank;
+    a.col0 = a0.col0 + c0;
+    if (a0.epi == EPI_QKV) a.y = a0.y + (size_t)c0 * a0.dim;
+    else if (a0.y) a.y = a0.y + (size_t)c0 * a0.y_stride;
+}
+
+// blockIdx.y > 0 (F16 / F32 weights: a launch over several whole groups of NC columns): the
+// group's arguments. Quantized weights launch column groups one by one (their multi-column
+// steps go to the matrix cores), so their instances stay free of the per-group arithmetic.
 template <int WT, int NC, int G, int U, int PRO, int EPI, int WAVES, bool NTW>
-__global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
-    const unsigned long long t0 = stamp_begin(a.stamp);
-    gemv_body<WT, NC, G, U, PRO, EPI, WAVES, NTW>(a);
-    stamp_end(a.stamp, t0);
+__global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a0) {
+    const unsigned long long t0 = stamp_begin(a0.stamp);
+    // group 0 reads the kernel arguments in place; a later group's copy lives in private memory
+    if constexpr (WT == T_F16 || WT == T_F32) {
+        if (blockIdx.y) {
+            GemvArgs a = a0;
+            gemv_advance(a, a0, (int)blockIdx.y * NC);
+            gemv_body<WT, NC, G, U, PRO, EPI, WAVES, NTW>(a);
+        } else {
+            gemv_body<WT, NC, G, U, PRO, EPI, WAVES, NTW>(a0);
+        }
+    } else {
+        gemv_body<WT, NC, G, U, PRO, EPI, WAVES, NTW>(a0);
+    }
+    stamp_end(a0.stamp, t0);
 }
 
 // ------------------------------------------------------------------------------------
@@ -1948,7 +1982,8 @@ template <int WT, int NC, int G, int U, int PRO, int EPI, int W, bool NTW>
 static void gemv_go(const GemvArgs& a, hipStream_t s) {
     constexpr int R = W * (64 / G);
     const size_t lds = lds_act_bytes(WT, NC, a.w.in) + (size_t)NC * R * 4 + (PRO == PRO_ACT ? 0 : (size_t)NC * 512 * 8);
-    hipLaunchKernelGGL((k_gemv<WT, NC, G, U, PRO, EPI, W, NTW>), dim3((a.w.out + R - 1) / R), dim3(64 * W), lds, s, a);
+    hipLaunchKernelGGL((k_gemv<WT, NC, G, U, PRO, EPI, W, NTW>), dim3((a.w.out + R - 1) / R, a.ygroups > 1 ? a.ygroups : 1),
+                       dim3(64 * W), lds, s, a);
 }
 
 // Tries (G, U, W) = the listed shapes whose G * U matches the row's unit count; else the
@@ -2109,30 +2144,18 @@ void launch_gemv(const GemvArgs& a0, hipStream_t s) {
         return;
     }
     if (a0.pro == PRO_ACT && a0.src.bm) return;   // the caller checks gemv_mf_ok before making one
-    const int step = gemv_step(a0);
-    for (int c0 = 0; c0 < a0.ncol; c0 += step) {
+    const int step = gemv_step(a0), whole = a0.ncol / step;
+    const bool grid_y = a0.w.type == T_F16 || a0.w.type == T_F32;
+    // F16 / F32 weights: whole groups of `step` columns in one launch (blockIdx.y = the group:
+    // one boundary for a prompt group's hundreds of columns), then a ragged tail in its own;
+    // quantized weights one launch per group
+    for (int c0 = 0; c0 < a0.ncol;) {
         GemvArgs a = a0;
+        a.ygroups = grid_y && c0 == 0 && whole > 1 ? whole : 1;
         a.ncol = a0.ncol - c0 < step ? a0.ncol - c0 : step;
         a.stream_w = a0.ncol <= step ? 1 : 0;
-        if (c0) {
-            a.x = a0.x ? a0.x + (size_t)c0 * a0.x_stride : nullptr;
-            const auto adv = [c0](ActBuf& b) {
-                if (b.q) b.q += (size_t)c0 * b.stride;
-                if (b.d) b.d += (size_t)c0 * (b.stride / 32);
-                if (b.h) b.h += (size_t)c0 * b.stride;
-                if (b.f) b.f += (size_t)c0 * b.stride;
-            };
-            adv(a.src);
-            adv(a.dst);
-            if (a0.dst_f) a.dst_f = a0.dst_f + (size_t)c0 * a0.dst.stride;
-            if (a0.ad_ax) a.ad_ax = a0.ad_ax + (size_t)c0 * a0.ad_rank;
-            a.col0 = a0.col0 + c0;
-            if (a0.epi == EPI_QKV) {
-                a.y = a0.y + (size_t)c0 * a0.dim;   // the caches stay: the epilogue maps col0 + n
-            } else if (a0.y) {
-                a.y = a0.y + (size_t)c0 * a0.y_stride;
-            }
-        }
+        if (c0) gemv_advance(a, a0, c0);
+        c0 += a.ncol * a.ygroups;
         switch (a.w.type) {
         case T_Q8_0: gemv_wt<T_Q8_0>(a, s); break;
         case T_Q4_0: gemv_wt<T_Q4_0>(a, s); break;
