@@ -412,19 +412,27 @@ void project_memory(mgx_stream* s, int r, const float* t5, int nc) {
     const mgx_lm_config& c = m->c;
     const int R = s->n_req, rows = s->n_ctx;
     HIP_OK(hipMemcpyAsync(s->t5d, t5, sizeof(float) * (size_t)nc * c.cond_dim, hipMemcpyHostToDevice, s->hs));
-    for (int col = 0; col < nc; ++col) {
-        mgx::GemvArgs a = ga(m->cond_proj, 1);
+    // the memory tokens several to a launch (each column summed as alone): all of them over
+    // F16 / F32 weights (one launch, the column sets on blockIdx.y), pairs over quantized ones
+    // (the vector GEMV: wider sets would go to the matrix cores, whose staging buffers hold only
+    // the stream's own columns); one at a time under an adapter (its A x buffer likewise)
+    const auto per = [](const mgx::DevMat& w, const AdapterW* ad) {
+        return ad ? 1 : (w.type == mgx::T_F16 || w.type == mgx::T_F32) ? 1 << 30 : 2;
+    };
+    for (int col = 0, k = per(m->cond_proj, nullptr); col < nc; col += k) {
+        mgx::GemvArgs a = ga(m->cond_proj, nc - col < k ? nc - col : k);
         pro_f32(a, s->t5d + (size_t)col * c.cond_dim, c.cond_dim);
         epi_store(a, s->ctx + (size_t)col * c.dim, c.dim);
         gemv(s, a);
     }
     mgx::launch_add_bias(s->ctx, m->cond_proj_b, c.dim, nc, s->hs);
     for (int l = 0; l < c.layers; ++l) {
-        for (int col = 0; col < nc; ++col) {
-            mgx::GemvArgs a = ga(m->L[(size_t)l].w[P_CKV], 1);
+        const AdapterW* ad = m->L[(size_t)l].ad[P_CKV];
+        for (int col = 0, k = per(m->L[(size_t)l].w[P_CKV], ad); col < nc; col += k) {
+            mgx::GemvArgs a = ga(m->L[(size_t)l].w[P_CKV], nc - col < k ? nc - col : k);
             pro_f32(a, s->ctx + (size_t)col * c.dim, c.dim);
             epi_store(a, s->kvp + (size_t)col * 2 * c.dim, 2 * c.dim);
-            gemv_ad(s, a, m->L[(size_t)l].ad[P_CKV]);
+            gemv_ad(s, a, ad);
         }
         const size_t off = ((size_t)l * R + r) * c.heads * rows * 64;
         mgx::launch_xkv_split(s->kvp, nc, rows, c.dim, s->xk + off, s->xv + off, s->hs);
