@@ -67,13 +67,17 @@ def test_adapter_ranks_at_real_widths(M, shape, wtype, rank):
         assert np.array_equal(got, want), f"position {t}: max {np.abs(got - want).max()}"
 
 
-@pytest.mark.parametrize("shape,wtype,rank", [("mini1536", 8, 16), ("mini2048", 2, 64)])
+@pytest.mark.parametrize("shape,wtype,rank", [("mini1536", 8, 16), ("mini2048", 2, 64), ("mini1024", 1, 16),
+                                              ("mini1024", 0, 5)])
 @pytest.mark.parametrize("dora", [False, True])
 def test_adapter_wide_prefill_matches_oracle(M, shape, wtype, rank, dora):
     """A 40-token prefill with every projection adapted runs its first 39 positions through the
-    prefill view: 78 columns (39 positions x 2 streams), five 16-column groups in one launch --
-    the last one ragged, blocks of up to four groups against one load of the weights, the
-    adapter's A x staged group by group; then single steps."""
+    prefill view: 78 columns (39 positions x 2 streams). Quantized weights: five 16-column groups
+    in one matrix-core launch -- the last one ragged, blocks of several groups against one load
+    of the weights, the adapter's A x staged group by group. F16 / F32 weights: the vector GEMV's
+    whole column sets on blockIdx.y of one launch (each set's A x, sources and destinations
+    advanced by its first column), then the ragged tail set in its own launch. Then single
+    steps."""
     print(f"adapter wide prefill {shape} wtype={wtype} rank={rank} dora={dora}", flush=True)
     c = H.model(shape, wtype, 5).config
     ads = synth.synth_adapters(c, rank=rank, targets=ALL, dora=dora, seed=rank + 1)
