@@ -2000,6 +2000,10 @@ template <int WT, int NC, int PRO, int EPI, bool NTW> static void gemv_pick(cons
             GEMV_TRY(16, 2, 1); GEMV_TRY(16, 3, 1); GEMV_TRY(16, 4, 1);
             GEMV_TRY(32, 4, 4); GEMV_TRY(32, 6, 4); GEMV_TRY(32, 8, 4);      // in = ff 4096 / 6144 / 8192
             GEMV_TRY(8, 2, 2);                                               // in = 512
+        } else if constexpr (EPI == EPI_GELU_ACT) {
+            // (F16 / F32 LayerNorm projections over prepared columns) the GELU epilogue takes
+            // whole 32-row blocks: 8 lanes a row, 4 waves
+            GEMV_TRY(8, 16, 4); GEMV_TRY(8, 8, 4); GEMV_TRY(8, 2, 4);
         } else if constexpr (WT == T_F16) {
             GEMV_TRY(8, 16, 2); GEMV_TRY(64, 8, 4); GEMV_TRY(8, 2, 2); GEMV_TRY(8, 8, 2);
         } else {
@@ -2023,7 +2027,16 @@ template <int WT, int NC, int PRO, int EPI, bool NTW> static void gemv_pick(cons
 #undef GEMV_TRY
 
 template <int WT, int NC, bool NTW> static void gemv_nc(const GemvArgs& a, hipStream_t s) {
-    if (a.pro == PRO_ACT) gemv_pick<WT, NC, PRO_ACT, EPI_RESID, NTW>(a, s);   // every PRO_ACT site adds the residual
+    if (a.pro == PRO_ACT) {
+        // F16 / F32 LayerNorm projections over many columns take their columns prepared once
+        // (k_prep) instead of per row block; every other activation-source site adds the residual
+        if constexpr (WT == T_F16 || WT == T_F32) {
+            if (a.epi == EPI_QKV) return gemv_pick<WT, NC, PRO_ACT, EPI_QKV, NTW>(a, s);
+            if (a.epi == EPI_GELU_ACT) return gemv_pick<WT, NC, PRO_ACT, EPI_GELU_ACT, NTW>(a, s);
+            if (a.epi == EPI_STORE) return gemv_pick<WT, NC, PRO_ACT, EPI_STORE, NTW>(a, s);
+        }
+        gemv_pick<WT, NC, PRO_ACT, EPI_RESID, NTW>(a, s);
+    }
     else if (a.pro == PRO_F32) gemv_pick<WT, NC, PRO_F32, EPI_STORE, NTW>(a, s);
     else if (a.epi == EPI_QKV) gemv_pick<WT, NC, PRO_LN, EPI_QKV, NTW>(a, s);
     else if (a.epi == EPI_GELU_ACT) gemv_pick<WT, NC, PRO_LN, EPI_GELU_ACT, NTW>(a, s);
@@ -2350,6 +2363,18 @@ __global__ __launch_bounds__(256) void k_prep(GemvArgs a) {
     if ((int)blockIdx.y < first) {
         LdsAct g{};
         g.in = in;
+        // F16 / F32 weights' activation form: the column's converted values, in place
+        if (a.dst.kind == ACT_F16 || a.dst.kind == ACT_F32) {
+            g.bm_col = -1;
+            if (a.dst.kind == ACT_F16) {
+                g.h = a.dst.h + (size_t)col * a.dst.stride;
+                prologue<T_F16, KG, LN>(a, g, red, 0, tid, lane, xr, wr, br);
+            } else {
+                g.f = a.dst.f + (size_t)col * a.dst.stride;
+                prologue<T_F32, KG, LN>(a, g, red, 0, tid, lane, xr, wr, br);
+            }
+            return;
+        }
         g.bm_col = a.dst.bm ? col : -1;
         g.q = a.dst.bm ? a.dst.q : a.dst.q + (size_t)col * a.dst.stride;
         g.d = a.dst.bm ? a.dst.d : a.dst.d + (size_t)col * (a.dst.stride / 32);

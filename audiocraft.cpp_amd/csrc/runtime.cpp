@@ -77,7 +77,7 @@ struct ActStore {
     float* d = nullptr;
     uint16_t* h = nullptr;
     float* f = nullptr;
-    int stride = 0;
+    int stride = 0, cols = 0;   // width, and the columns allocated
     // bm: Q8 block-major, the layout a matrix-core GEMV reads (16 column slots are allocated)
     mgx::ActBuf view(int wtype, bool bm = false) const {
         mgx::ActBuf a{};
@@ -153,6 +153,7 @@ struct mgx_stream {
     void alloc_act(ActStore& a, int cols, int stride) {
         if (n_seq >= 3) cols = (std::max(cols, 16) + 15) / 16 * 16;   // block-major Q8: whole 16-column groups
         a.stride = stride;
+        a.cols = cols;
         a.q = mem.alloc<int8_t>((size_t)cols * stride);
         a.d = mem.alloc<float>((size_t)cols * stride / 32);
         a.h = mem.alloc<uint16_t>((size_t)cols * stride);
@@ -208,6 +209,28 @@ void gemv(mgx_stream* s, mgx::GemvArgs a) {
 // (its LayerNorm or f32 source; for an activation-form source, `xf` holds the same column in
 // f32), then the GEMV adds s * B(Ax) in its epilogue (lora.h:50-83).
 void gemv_ad(mgx_stream* s, mgx::GemvArgs a, const AdapterW* ad, const float* xf = nullptr, int xf_stride = 0) {
+    // F16 / F32 weights over more columns than one launch's set: the LayerNorm columns (and the
+    // adapter's A x) prepared once in their activation form, then activation-source launches --
+    // the per-row-block prologue would recompute every column's LayerNorm once per row block
+    if (a.pro == mgx::PRO_LN && (a.w.type == mgx::T_F16 || a.w.type == mgx::T_F32) && a.ncol > 4 &&
+        s->act_ln.h && a.ncol <= s->act_ln.cols && a.ncol <= s->n_seq && a.w.in <= s->act_ln.stride) {
+        mgx::GemvArgs m = a;
+        m.pro = mgx::PRO_ACT;
+        m.src = s->act_ln.view(a.w.type);
+        m.src.stride = a.w.in;
+        mgx::GemvArgs p = ga(ad ? ad->A : mgx::DevMat{}, a.ncol);
+        p.w.in = a.w.in;
+        p.pro = a.pro; p.x = a.x; p.x_stride = a.x_stride; p.ln_w = a.ln_w; p.ln_b = a.ln_b; p.eps = a.eps;
+        p.dst = m.src;
+        if (ad) { p.y = s->ax; p.y_stride = ad->rank; }
+        mgx::launch_act_prep(p, s->hs);
+        if (ad) {
+            m.ad_ax = s->ax; m.ad_B = ad->B; m.ad_m = ad->m; m.ad_norm = ad->norm; m.ad_rank = ad->rank;
+            m.ad_scale = ad->scale; m.ad_strength = ad->strength;
+        }
+        gemv(s, m);
+        return;
+    }
     if (a.pro != mgx::PRO_ACT) {
         // the matrix-core GEMV reads its columns in Q8 form: LayerNorm / quantize them (and
         // take the adapter's A x from the same f32 column) in one preparation launch
